@@ -1,0 +1,87 @@
+"""Quad page score (Stage A.1, quad mode) -- host side of ``amass_quad_score``.
+
+Same contract as the reference ``quad_score`` (selection/quad_score.py:110-139) and
+``select_pages_quad`` (:142-153): writes ``st.score`` (R, n_kv, MP) fp32 over the scored
+region [0, n_sel_hi); combine="nrm" first writes the per-head scores ``st.score_h`` and
+then the per-head-normalised mass sum_g exp(S_g - max_p S_g) into ``st.score``.
+``select_pages_quad`` folds that nrm combine into the selection launch instead of a
+separate kernel (one less launch and one less pass over score_h).
+"""
+from __future__ import annotations
+
+import torch
+
+from .._hip import NrmArgs, QuadScoreArgs, call, current_stream, ptr, require_cuda
+from .select import derive_page_params, select_pages
+
+
+def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadScoreArgs:
+    mu, mu_s, V, V_s, sig2, _ = st.layer_state(layer)
+    require_cuda(q, block_table, mu)
+    if q.dtype != torch.bfloat16 or q.stride(2) != 1:
+        raise ValueError("q must be bf16 (T, H, d) with unit stride on d")
+    if block_table.dtype != torch.int32 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be int32 with unit column stride")
+    if block_table.shape[1] < st.max_pages - st.window_pages:
+        raise ValueError("block_table narrower than the scored page range")
+    nrm = st.combine == "nrm"
+    sh = st.score_h
+    return QuadScoreArgs(
+        q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),
+        mu=ptr(mu), mu_sb=mu.stride(0), mu_scale=ptr(mu_s), mus_sb=mu_s.stride(0),
+        v=ptr(V), v_sb=V.stride(0), v_scale=ptr(V_s), vs_sb=V_s.stride(0),
+        sig2=ptr(sig2), sg_sb=sig2.stride(0),
+        block_table=ptr(block_table), bt_st=block_table.stride(0),
+        n_sel_hi=ptr(st.n_sel_hi),
+        score=ptr(st.score), sc_sr=st.score.stride(0), sc_sh=st.score.stride(1),
+        score_h=ptr(sh) if nrm else None,
+        sh_sr=sh.stride(0) if nrm else 0, sh_sh=sh.stride(1) if nrm else 0,
+        sh_sg=sh.stride(2) if nrm else 0,
+        comb_out=ptr(comb_out), scale=float(scale),
+        n_req=n_req, n_kv=st.n_kv, G=st.G, d=st.d, page=st.page, rank=st.r,
+        v_bits=st.v_bits, max_pages=st.max_pages, combine=1 if nrm else 0)
+
+
+def quad_score_launch(st, layer: int, q, block_table, n_req: int, scale: float,
+                      comb_out=None) -> None:
+    """The score kernel alone (combine="nrm": st.score_h only)."""
+    if n_req > st.max_reqs:
+        raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
+    a = _quad_args(st, layer, q, block_table, n_req, scale, comb_out)
+    call("amass_quad_score", a, current_stream(q.device))
+
+
+def nrm_combine(st, n_req: int) -> None:
+    """score[p] = sum_g exp(score_h[g, p] - max_p score_h[g, p]) over [0, n_sel_hi)."""
+    sh, sc = st.score_h, st.score
+    a = NrmArgs(score_h=ptr(sh), sh_sr=sh.stride(0), sh_sh=sh.stride(1), sh_sg=sh.stride(2),
+                score=ptr(sc), sc_sr=sc.stride(0), sc_sh=sc.stride(1),
+                n_sel_hi=ptr(st.n_sel_hi), n_req=n_req, n_kv=st.n_kv, G=st.G,
+                max_pages=st.max_pages)
+    call("amass_nrm_combine", a, current_stream(sc.device))
+
+
+def quad_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float) -> None:
+    """Stage A.1: write st.score for the scored region (st.n_sel_hi must be current)."""
+    quad_score_launch(st, layer, q, block_table, n_req, scale)
+    if st.combine == "nrm":
+        nrm_combine(st, n_req)
+
+
+def select_pages_quad(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
+                      *, derive: bool = True) -> None:
+    """One-call Stage A (quad mode): (derive) + score + selection -> st.page_table /
+    st.page_cnt.  Two launches (three with derive)."""
+    if derive:
+        derive_page_params(st, seq_lens, n_req)
+    quad_score_launch(st, layer, q, block_table, n_req, scale)
+    select_pages(st, n_req, score_h=st.score_h if st.combine == "nrm" else None)
+
+
+def clse_score(*_a, **_k):
+    raise NotImplementedError("score='clse' is outside this build's hot path "
+                              "(quad and r8 are implemented)")
+
+
+def select_pages_clse(*_a, **_k):
+    raise NotImplementedError("score='clse' is outside this build's hot path")

@@ -1,0 +1,36 @@
+"""r8 page score (Stage A.1, r8 mode) -- host side of ``amass_r8_score``.
+
+Same contract as the reference ``r8_score`` (selection/score.py:123-148): writes
+``st.score`` (R, n_kv, MP) fp32, the group max of s*mu.q + logsumexp_t(s * c_t . q~)
+over the scored region.  ``comb_out`` (optional int32 (R, n_kv, MP, G, r+1)) receives the
+exact integer d-contractions sum_d qi*code (the r columns of Vk, then mu).
+"""
+from __future__ import annotations
+
+import torch
+
+from .._hip import R8ScoreArgs, call, current_stream, ptr, require_cuda
+
+
+def r8_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
+             comb_out=None) -> None:
+    if n_req > st.max_reqs:
+        raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
+    mu, mu_s, Vk, Vk_s, c, c_s, _ = st.layer_state(layer)
+    require_cuda(q, block_table, seq_lens, mu)
+    if q.dtype != torch.bfloat16 or q.stride(2) != 1:
+        raise ValueError("q must be bf16 (T, H, d) with unit stride on d")
+    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise ValueError("block_table / seq_lens must be int32")
+    a = R8ScoreArgs(
+        q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),
+        mu=ptr(mu), mu_sb=mu.stride(0), mu_scale=ptr(mu_s), mus_sb=mu_s.stride(0),
+        vk=ptr(Vk), vk_sb=Vk.stride(0), vk_scale=ptr(Vk_s), vks_sb=Vk_s.stride(0),
+        c=ptr(c), c_sb=c.stride(0), c_scale=ptr(c_s), cs_sb=c_s.stride(0),
+        block_table=ptr(block_table), bt_st=block_table.stride(0),
+        seq_lens=ptr(seq_lens), n_sel_hi=ptr(st.n_sel_hi),
+        score=ptr(st.score), sc_sr=st.score.stride(0), sc_sh=st.score.stride(1),
+        comb_out=ptr(comb_out), scale=float(scale),
+        n_req=n_req, n_kv=st.n_kv, G=st.G, d=st.d, page=st.page, rank=st.r,
+        vk_bits=st.vk_bits, c_bits=st.c_bits, max_pages=st.max_pages)
+    call("amass_r8_score", a, current_stream(q.device))

@@ -1,0 +1,303 @@
+// mem-v tier residency for gfx950: gather plan (hits / misses / exact-LRU victims) and
+// the flat miss fetch from the pinned, device-mapped host pool into the HBM hot buffer.
+//
+// Semantics of tier/residency.py:45-139 (_miss_diff_kernel, _select_victims_kernel) and
+// :196-248 (_fetch_flat_kernel).  The reference picks victims one miss at a time per
+// kv-head (an argmin over all S slots per miss).  Because a slot chosen as a victim gets
+// clock = now and so leaves the candidate set, that sequential rule is the same as: sort
+// the slots not touched this step by (lru clock, slot index) and give the k-th DISTINCT
+// new miss (in request, position order) the k-th slot.  The victim kernel does exactly
+// that with one workgroup per kv-head: a dedup pass (atomicMin of the first flat position
+// per physical block), a block scan that ranks the first occurrences, a stable 1-bit LSD
+// radix sort of the untouched slot ids by clock (only over the bits the clocks use), and a
+// parallel apply.  No serial per-miss loop remains.
+#include "common.h"
+
+namespace amass {
+
+constexpr int TP_THREADS = 1024;
+constexpr int TP_WAVES = TP_THREADS / WAVE;
+constexpr int TP_MAXS = 8192;
+constexpr int TP_MAXREQ = 1024;
+constexpr int MD_THREADS = 256;
+
+__global__ void tier_clock_kernel(int32_t* clock, int32_t* fetch_cnt) {
+    if (threadIdx.x == 0) {
+        clock[0] += 1;
+        fetch_cnt[0] = 0;
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ int blk_excl_scan(int v, int* red, int& total) {
+    constexpr int NW = NT / WAVE;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, WAVE);
+        if (lane >= o) x += y;
+    }
+    __syncthreads();
+    if (lane == 63) red[w] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const int t = red[i];
+        if (i < w) base += t;
+        tot += t;
+    }
+    total = tot;
+    return base + x - v;
+}
+
+// ---- hits touch the LRU clock; misses are compacted in selection order ----------------
+__global__ __launch_bounds__(MD_THREADS) void miss_diff_kernel(const amass_tier_plan_args a) {
+    __shared__ int red[MD_THREADS / WAVE];
+    const int kv = blockIdx.x, r = blockIdx.y;
+    const int n = a.page_cnt[(int64_t)r * a.pc_sr + kv];
+    const int sl = a.seq_lens[r];
+    const int clk = a.clock[0];
+    const int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kv * a.pt_sh;
+    const int32_t* bt = a.block_table + (int64_t)r * a.bt_st;
+    int32_t* mp = a.miss_pages + ((int64_t)r * a.n_kv + kv) * a.max_pages;
+    int nmiss = 0;
+    for (int off = 0; off < n; off += MD_THREADS) {
+        const int idx = off + threadIdx.x;
+        int is_miss = 0, blk = 0;
+        if (idx < n) {
+            const int pt = tab[idx];
+            blk = bt[pt];
+            const bool complete = (int64_t)(pt + 1) * a.page <= (int64_t)sl;
+            const int slot = a.page2slot[(int64_t)kv * a.nb + blk];
+            if (complete && slot >= 0) a.lru_clock[(int64_t)kv * a.slots + slot] = clk;
+            is_miss = (complete && slot < 0) ? 1 : 0;
+        }
+        int tot;
+        const int pos = blk_excl_scan<MD_THREADS>(is_miss, red, tot);
+        if (is_miss) mp[nmiss + pos] = blk;
+        nmiss += tot;
+    }
+    if (threadIdx.x == 0) a.miss_cnt[(int64_t)r * a.n_kv + kv] = nmiss;
+}
+
+__device__ __forceinline__ int load_agent(const int32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- per kv-head: dedup, rank new misses, sort untouched slots, apply ------------------
+__global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_plan_args a) {
+    __shared__ int off[TP_MAXREQ + 1];
+    __shared__ uint16_t sb[2][TP_MAXS];
+    __shared__ int red[TP_WAVES];
+    __shared__ int smax_s[TP_WAVES];
+    const int kv = blockIdx.x, tid = threadIdx.x;
+    const int clk = a.clock[0];
+    const int S = a.slots;
+    const int64_t mbase_kv = (int64_t)kv * a.max_pages;
+    int32_t* fp = a.first_pos + (int64_t)kv * a.nb;
+    int32_t* p2s = a.page2slot + (int64_t)kv * a.nb;
+    int32_t* s2p = a.slot2page + (int64_t)kv * S;
+    int32_t* lru = a.lru_clock + (int64_t)kv * S;
+
+    // 1. flat offsets of every request's miss list
+    int mc = tid < a.n_req ? a.miss_cnt[(int64_t)tid * a.n_kv + kv] : 0;
+    int M;
+    const int o = blk_excl_scan<TP_THREADS>(mc, red, M);
+    if (tid < a.n_req) off[tid] = o;
+    if (tid == 0) off[a.n_req] = M;
+    __syncthreads();
+    if (M == 0) return;
+
+    const int C = (M + TP_THREADS - 1) / TP_THREADS;
+    const int f0 = min(tid * C, M), f1 = min(f0 + C, M);
+    auto locate = [&](int f, int& r) {      // r: request owning flat position f
+        while (off[r + 1] <= f) ++r;
+    };
+    auto miss_at = [&](int r, int f) -> int32_t* {
+        return a.miss_pages + (int64_t)r * a.n_kv * a.max_pages + mbase_kv + (f - off[r]);
+    };
+    int r0 = 0;
+    {   // first request of this chunk (binary search)
+        int lo = 0, hi = a.n_req - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (off[mid] <= f0) lo = mid; else hi = mid - 1;
+        }
+        r0 = lo;
+    }
+
+    // 2. first occurrence of each physical block among this step's misses
+    {
+        int r = r0;
+        for (int f = f0; f < f1; ++f) {
+            locate(f, r);
+            atomicMin(&fp[*miss_at(r, f)], f);
+        }
+    }
+    __threadfence();
+    __syncthreads();
+
+    // 3. rank the distinct new misses in flat order
+    int nfirst = 0;
+    {
+        int r = r0;
+        for (int f = f0; f < f1; ++f) {
+            locate(f, r);
+            nfirst += (load_agent(&fp[*miss_at(r, f)]) == f);
+        }
+    }
+    int Mnew;
+    const int rank0 = blk_excl_scan<TP_THREADS>(nfirst, red, Mnew);
+
+    // 4. untouched slots in slot order, then a stable radix sort by clock
+    const int CS = (S + TP_THREADS - 1) / TP_THREADS;
+    const int s0 = min(tid * CS, S), s1 = min(s0 + CS, S);
+    int nun = 0, kmax = 0;
+    for (int s = s0; s < s1; ++s) {
+        const int c = lru[s];
+        if (c < clk) { ++nun; kmax = max(kmax, c); }
+    }
+    int U;
+    int upos = blk_excl_scan<TP_THREADS>(nun, red, U);
+    for (int s = s0; s < s1; ++s)
+        if (lru[s] < clk) sb[0][upos++] = (uint16_t)s;
+    {
+        int km = kmax;
+#pragma unroll
+        for (int o2 = 32; o2 >= 1; o2 >>= 1) km = max(km, __shfl_xor(km, o2, WAVE));
+        if ((tid & 63) == 0) smax_s[tid >> 6] = km;
+    }
+    __syncthreads();
+    int kall = 0;
+#pragma unroll
+    for (int i = 0; i < TP_WAVES; ++i) kall = max(kall, smax_s[i]);
+    const int nbits = kall > 0 ? 32 - __clz(kall) : 0;
+    const int CU = (U + TP_THREADS - 1) / TP_THREADS;
+    const int u0 = min(tid * CU, U), u1 = min(u0 + CU, U);
+    for (int b = 0; b < nbits; ++b) {
+        const uint16_t* cur = sb[b & 1];
+        uint16_t* nxt = sb[(b + 1) & 1];
+        int nz = 0;
+        for (int i = u0; i < u1; ++i) nz += ((lru[cur[i]] >> b) & 1) == 0;
+        int Z;
+        int zb = blk_excl_scan<TP_THREADS>(nz, red, Z);
+        for (int i = u0; i < u1; ++i) {
+            const uint16_t s = cur[i];
+            if (((lru[s] >> b) & 1) == 0) nxt[zb++] = s;
+            else nxt[Z + (i - zb)] = s;
+        }
+        __syncthreads();
+    }
+    const uint16_t* sorted = sb[nbits & 1];
+
+    // 5. apply: the k-th new miss takes sorted[k]; duplicates and overflow get -1
+    {
+        int r = r0, rank = rank0;
+        for (int f = f0; f < f1; ++f) {
+            locate(f, r);
+            const int32_t blk = *miss_at(r, f);
+            int32_t* vict = a.victim_slots + (int64_t)r * a.n_kv * a.max_pages + mbase_kv +
+                            (f - off[r]);
+            if (load_agent(&fp[blk]) != f) {
+                *vict = -1;
+                continue;
+            }
+            const int k = rank++;
+            if (k >= U) {
+                *vict = -1;
+                a.overflow[0] = 1;
+                continue;
+            }
+            const int s = sorted[k];
+            const int old = s2p[s];
+            if (old >= 0) p2s[old] = -1;
+            p2s[blk] = s;
+            s2p[s] = blk;
+            lru[s] = clk;
+            *vict = s;
+            const int fi = atomicAdd(a.fetch_cnt, 1);
+            if (fi < a.fcap) {
+                a.fetch_list[3 * (int64_t)fi + 0] = kv;
+                a.fetch_list[3 * (int64_t)fi + 1] = blk;
+                a.fetch_list[3 * (int64_t)fi + 2] = s;
+            }
+        }
+    }
+    __syncthreads();
+    // 6. restore the dedup scratch
+    {
+        int r = r0;
+        for (int f = f0; f < f1; ++f) {
+            locate(f, r);
+            fp[*miss_at(r, f)] = 0x7FFFFFFF;
+        }
+    }
+}
+
+// ---- flat fetch: one 4 KB page per workgroup iteration, 16 B per thread -----------------
+__global__ __launch_bounds__(256) void fetch_kernel(const amass_tier_fetch_args a) {
+    const int n = min(a.fetch_cnt[0], a.fcap);
+    const int tid = threadIdx.x;
+    const int tok = tid >> 4, ch = tid & 15;   // 16 tokens x 16 chunks of 8 elements
+    const int64_t pe = (int64_t)a.page * a.d;  // elements per page
+    for (int i = blockIdx.x; i < n; i += gridDim.x) {
+        const int kv = a.fetch_list[3 * (int64_t)i + 0];
+        const int blk = a.fetch_list[3 * (int64_t)i + 1];
+        const int slot = a.fetch_list[3 * (int64_t)i + 2];
+        uint16_t* hot = (uint16_t*)a.hot + ((int64_t)kv * a.slots + slot) * pe;
+        uint16_t* pool = (uint16_t*)a.pool + (((int64_t)a.t_layer * a.nb + blk) * a.n_kv + kv) * pe;
+        const int64_t e = (int64_t)tok * a.d + 8 * ch;
+        const int8_t vld = a.pool_valid[(int64_t)kv * a.nb + blk];
+        const int vb = a.vbo ? a.vbo[blk] : -1;
+        if (vld == 0 && vb >= 0) {
+            const uint16_t* st = (const uint16_t*)a.vpool + (int64_t)vb * a.v_sb +
+                                 (int64_t)kv * a.v_sh + (int64_t)tok * a.v_st + 8 * ch;
+            const uint4 x = *reinterpret_cast<const uint4*>(st);
+            *reinterpret_cast<uint4*>(hot + e) = x;
+            *reinterpret_cast<uint4*>(pool + e) = x;
+            __syncthreads();
+            if (tid == 0) a.pool_valid[(int64_t)kv * a.nb + blk] = 1;
+        } else {
+            *reinterpret_cast<uint4*>(hot + e) = *reinterpret_cast<const uint4*>(pool + e);
+        }
+    }
+}
+
+}  // namespace amass
+
+using namespace amass;
+
+extern "C" int amass_tier_gather_plan(const amass_tier_plan_args* a, void* stream) {
+    if (!a) return AMASS_ERR_NULL;
+    if (!a->page_table || !a->page_cnt || !a->block_table || !a->seq_lens || !a->page2slot ||
+        !a->slot2page || !a->lru_clock || !a->clock || !a->miss_pages || !a->miss_cnt ||
+        !a->victim_slots || !a->overflow || !a->fetch_list || !a->fetch_cnt || !a->first_pos)
+        return AMASS_ERR_NULL;
+    if (a->n_req < 0 || a->n_kv < 1 || a->nb < 1 || a->slots < 1 || a->max_pages < 1 ||
+        a->page < 1 || a->fcap < 1)
+        return AMASS_ERR_GEOMETRY;
+    if (a->slots > TP_MAXS || a->n_req > TP_MAXREQ) return AMASS_ERR_CAPACITY;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(tier_clock_kernel, dim3(1), dim3(64), 0, s, a->clock, a->fetch_cnt);
+    int rc = check_launch();
+    if (rc || a->n_req == 0) return rc;
+    hipLaunchKernelGGL(miss_diff_kernel, dim3(a->n_kv, a->n_req), dim3(MD_THREADS), 0, s, *a);
+    rc = check_launch();
+    if (rc) return rc;
+    hipLaunchKernelGGL(victims_kernel, dim3(a->n_kv), dim3(TP_THREADS), 0, s, *a);
+    return check_launch();
+}
+
+extern "C" int amass_tier_fetch(const amass_tier_fetch_args* a, void* stream) {
+    if (!a) return AMASS_ERR_NULL;
+    if (!a->fetch_list || !a->fetch_cnt || !a->hot || !a->pool || !a->pool_valid)
+        return AMASS_ERR_NULL;
+    if (a->page * a->d != 16 * 128 || a->n_kv < 1 || a->nb < 1 || a->slots < 1 || a->fcap < 1 ||
+        a->grid < 1)
+        return AMASS_ERR_GEOMETRY;
+    if (a->vbo && !a->vpool) return AMASS_ERR_NULL;
+    hipLaunchKernelGGL(fetch_kernel, dim3(a->grid), dim3(256), 0, (hipStream_t)stream, *a);
+    return check_launch();
+}

@@ -1,0 +1,245 @@
+/*
+ * amass_hip.h -- C-ABI of the MI355X (gfx950) decode-time sparse-attention hot path.
+ *
+ * One shared library (libamass_hip.so) built with hipcc for gfx950.  Every entry point
+ * takes a POD argument struct (device pointers, element strides, geometry) plus a
+ * hipStream_t passed as void*, launches on that stream, never allocates device memory,
+ * never synchronises the host, and returns an int status (AMASS_OK = 0, negative on
+ * invalid geometry / HIP error).  Nothing throws across this boundary.  Launches are
+ * fixed-shape given (n_req, max_pages, ...) so a caller may capture them in a HIP graph.
+ *
+ * Element types: "bf16"/"fp16" arguments are raw 16-bit storage (void*), int8 codes are
+ * int8_t, scores fp32, tables int32.  Strides are in ELEMENTS of the pointed-to type.
+ *
+ * Each entry point names the reference interface it replaces (file:line inside the
+ * Js-Hwang1/amass-kv source tree, src/amass/...).
+ */
+#ifndef AMASS_HIP_H
+#define AMASS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AMASS_ABI_VERSION 1
+
+/* ---- status codes ---------------------------------------------------------------- */
+#define AMASS_OK               0
+#define AMASS_ERR_NULL        -1  /* a required pointer is NULL                      */
+#define AMASS_ERR_GEOMETRY    -2  /* unsupported / inconsistent shape               */
+#define AMASS_ERR_UNSUPPORTED -3  /* valid request, not implemented for this config */
+#define AMASS_ERR_LAUNCH      -4  /* kernel launch failed (hipGetLastError)         */
+#define AMASS_ERR_HIP         -5  /* other HIP runtime error                        */
+#define AMASS_ERR_CAPACITY    -6  /* a fixed capacity (LDS, scratch) is exceeded    */
+
+/* ---- quad (Gaussian-MGF quadratic) page score ------------------------------------- */
+/* Replaces the quad score of selection/quad_score.py:110-139 (Triton golden) and
+ * selection/quad_score_cuda.py:1724-1794 (hand-CUDA launcher).  Per (request, kv-head
+ * kh, page p < n_sel_hi[r]) and group head g:
+ *   qh_k = (V_code[:,k] * V_scale[k]) . q_g ;  quad = s^2/(2P) * sum_k sig2_k qh_k^2
+ *   qmu  = s * (mu_code * mu_scale) . q_g  ;  S_g = qmu + quad
+ * combine 0 ("max"): score[r,kh,p] = max_g S_g ; combine 1 ("nrm"): score_h[r,kh,g,p]=S_g.
+ * q is quantised per q-head to two int8 limbs (qi = rn(q/qs), qs = max|q|/16383,
+ * hi = rn(qi/128), lo = qi - 128 hi) and the d-contractions are exact int32 sums. */
+typedef struct amass_quad_score_args {
+    const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
+    const int8_t*  mu;       int64_t mu_sb;          /* (NB,n_kv,d) int8, block stride  */
+    const void*    mu_scale; int64_t mus_sb;         /* (NB,n_kv) fp16                  */
+    const int8_t*  v;        int64_t v_sb;           /* (NB,n_kv,d,r') int8 | (..,r'/2) int4 */
+    const void*    v_scale;  int64_t vs_sb;          /* (NB,n_kv,r') fp16               */
+    const void*    sig2;     int64_t sg_sb;          /* (NB,n_kv,r') fp16               */
+    const int32_t* block_table; int64_t bt_st;       /* (R,max_blocks) int32            */
+    const int32_t* n_sel_hi;                         /* (R,) int32                      */
+    float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32 (combine 0)    */
+    float*         score_h;  int64_t sh_sr, sh_sh, sh_sg; /* (R,n_kv,G,MP) (combine 1)  */
+    int32_t*       comb_out; /* optional (R,n_kv,MP,G,r'+1) exact int32 sums; NULL = off */
+    float          scale;    /* s = 1/sqrt(d) */
+    int32_t n_req, n_kv, G, d, page, rank, v_bits, max_pages, combine;
+} amass_quad_score_args;
+int amass_quad_score(const amass_quad_score_args* a, void* stream);
+
+/* ---- r8 (rank-r int8 low-rank per-key LSE) page score ----------------------------- */
+/* Replaces selection/score.py:123-148 (Triton golden) and selection/score_cuda.py:888-913.
+ *   q~[g,k] = (Vk_code[:,k] Vk_scale[k]) . q_g ; tok[g,t] = s * c_scale[t] * (c_code[t,:] . q~[g])
+ *   S_g = s * mu.q_g + logsumexp_{t : 16p+t < seq_len} tok[g,t] ; score = max_g S_g
+ * comb_out (optional) receives the exact int32 sums sum_d qi*code for the r columns and mu. */
+typedef struct amass_r8_score_args {
+    const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
+    const int8_t*  mu;       int64_t mu_sb;          /* (NB,n_kv,d) int8                */
+    const void*    mu_scale; int64_t mus_sb;         /* (NB,n_kv) fp16                  */
+    const int8_t*  vk;       int64_t vk_sb;          /* (NB,n_kv,d,r) int8 | (..,r/2) int4 */
+    const void*    vk_scale; int64_t vks_sb;         /* (NB,n_kv,r) fp16                */
+    const int8_t*  c;        int64_t c_sb;           /* (NB,n_kv,page,r) int8 | (..,r/2) */
+    const void*    c_scale;  int64_t cs_sb;          /* (NB,n_kv,page) fp16             */
+    const int32_t* block_table; int64_t bt_st;
+    const int32_t* seq_lens;                         /* (R,) int32                      */
+    const int32_t* n_sel_hi;                         /* (R,) int32                      */
+    float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32                */
+    int32_t*       comb_out; /* optional (R,n_kv,MP,G,r+1) exact int32 sums; NULL = off */
+    float          scale;
+    int32_t n_req, n_kv, G, d, page, rank, vk_bits, c_bits, max_pages;
+} amass_r8_score_args;
+int amass_r8_score(const amass_r8_score_args* a, void* stream);
+
+/* ---- per-step derived page parameters --------------------------------------------- */
+/* Replaces selection/select.py:30-54 (_derive_params_kernel / derive_page_params):
+ *   n_pages = ceil(sl/page); n_sel_hi = n_pages - window; S = n_sel_hi - sink;
+ *   b = min(max(ceil_fp64(budget*S), 1), max(S, 1)). */
+typedef struct amass_derive_args {
+    const int32_t* seq_lens;
+    int32_t*       n_pages;
+    int32_t*       n_sel_hi;
+    int32_t*       b_fix;
+    double         budget;
+    int32_t n_req, page, window_pages, sink_pages;
+} amass_derive_args;
+int amass_derive_params(const amass_derive_args* a, void* stream);
+
+/* ---- nrm GQA combine --------------------------------------------------------------- */
+/* Replaces selection/quad_score.py:276-315,384-399 (_nrm_hmax/_nrm_combine) and
+ * selection/quad_score_cuda.py:1446-1547 (nrm_combine_kernel):
+ *   hmax_g = max_{p<n_sel_hi} S_g[p] ; score[p] = sum_g exp(S_g[p] - hmax_g). */
+typedef struct amass_nrm_args {
+    const float*   score_h;  int64_t sh_sr, sh_sh, sh_sg;
+    float*         score;    int64_t sc_sr, sc_sh;
+    const int32_t* n_sel_hi;
+    int32_t n_req, n_kv, G, max_pages;
+} amass_nrm_args;
+int amass_nrm_combine(const amass_nrm_args* a, void* stream);
+
+/* ---- page selection (top-b / coverage nucleus) ------------------------------------- */
+/* Replaces selection/select.py:60-116 (_topb_select_kernel) and selection/select_cuda.py:
+ * 370-391 (topb_select_cuda); the coverage mode specifies per-(request, kv-head) the
+ * nucleus that backend/_selection_bridge.py:117-133 (_nucleus_b) computes per request.
+ * Selectable region [sink, n_sel_hi); sinks, window and tail are always kept; if the
+ * selectable region has <= 1 page every page is kept.  Output: ascending logical page ids
+ * in page_table[r,kh,0:cnt), -1 in [cnt, max_pages), page_cnt[r,kh] = cnt.
+ *   mode 0 (top-b):    b = b_fix[r] pages of the selectable region.
+ *   mode 1 (coverage): page masses w (score_kind 0: w = exp(score - max score), score_kind 1:
+ *                      w = score) in 2^-32 fixed point; need = ceil(coverage * total) -
+ *                      sink mass; b = fewest top pages whose mass reaches need (>= 1).
+ *   tie_mode 0: exactly b pages, ties at the b-th score broken to the lower page index.
+ *   tie_mode 1: keep every page with score >= the b-th score (reference threshold rule).
+ * If score_h != NULL the nrm combine runs first and writes its result into score. */
+typedef struct amass_select_args {
+    float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) in (or out if nrm)  */
+    const float*   score_h;  int64_t sh_sr, sh_sh, sh_sg; /* optional nrm input          */
+    const int32_t* n_pages;
+    const int32_t* n_sel_hi;
+    const int32_t* b_fix;
+    int32_t*       page_table; int64_t pt_sr, pt_sh; /* (R,n_kv,MP) int32               */
+    int32_t*       page_cnt;   int64_t pc_sr;        /* (R,n_kv) int32                  */
+    int32_t*       n_sel_out;  /* optional (R,n_kv): selectable pages chosen; NULL = off */
+    double         coverage;
+    int32_t n_req, n_kv, G, max_pages, sink_pages, mode, tie_mode, score_kind;
+} amass_select_args;
+int amass_topb_select(const amass_select_args* a, void* stream);      /* forces mode 0 */
+int amass_coverage_select(const amass_select_args* a, void* stream);  /* forces mode 1 */
+
+/* ---- sparse / dense paged decode attention ----------------------------------------- */
+/* Replaces attention/decode.py:247-304 + attention/merge.py:21-50 (Triton split-K decode
+ * and LSE merge) and attention/decode_cuda.py:1376-1501 (hand-CUDA split / fused).
+ * Per (request r, kv-head kh) attend the pages page_table[r,kh,0:page_cnt) (dense = 1:
+ * every page 0..ceil(sl/page)) with an online softmax; tokens >= seq_len are masked.
+ * path 1: split-K partials (m_part,l_part,acc_part (R,n_kv,split,G[,d]) fp32 contiguous)
+ * then LSE merge; path 2: one fused launch merging page stripes through LDS; path 0: auto.
+ * v_src 0: V from the resident paged cache; v_src 1: mem-v tier, V per page from the hot
+ * buffer (complete page resident in page2slot), else the staged pool (vbo[blk] >= 0,
+ * addressed through v/v_sb/v_st/v_sh), else the pinned host pool (UVA) -- the address
+ * select of tier/decode_mem.py:78-166 and attention/decode.py:179-226. */
+typedef struct amass_decode_args {
+    const void*    q;  int64_t q_st, q_hs;             /* (T,H,d) bf16                  */
+    const void*    k;  int64_t k_sb, k_st, k_sh;       /* K (NB,page,n_kv,d) bf16 view  */
+    const void*    v;  int64_t v_sb, v_st, v_sh;       /* V view (resident or staged)   */
+    const int32_t* block_table; int64_t bt_st;
+    const int32_t* seq_lens;
+    const int32_t* page_table;  int64_t pt_sr, pt_sh;
+    const int32_t* page_cnt;    int64_t pc_sr;
+    float*         m_part;
+    float*         l_part;
+    float*         acc_part;
+    void*          out; int64_t o_st, o_hs;            /* (T,H,d) bf16                  */
+    const void*    hot;        /* tier: (L,n_kv,S,page,d) bf16 base of THIS layer (n_kv,S,page,d) */
+    const int32_t* page2slot;  /* tier: (n_kv,NB) of this layer                          */
+    const int32_t* vbo;        /* tier: (NB,) staging block or -1                        */
+    const void*    pool;       /* tier: pinned pool device pointer (L,NB,n_kv,page,d)    */
+    int32_t t_layer, t_nb, t_slots;
+    float   scale;
+    int32_t n_req, n_kv, G, d, page, split, pps_min, path, dense, v_src;
+} amass_decode_args;
+int amass_sparse_decode(const amass_decode_args* a, void* stream);
+int amass_dense_paged_decode(const amass_decode_args* a, void* stream); /* forces dense=1 */
+
+/* ---- mem-v tier ------------------------------------------------------------------ */
+/* Replaces tier/residency.py:385-407 (gather_plan: _miss_diff_kernel +
+ * _select_victims_kernel).  Per (request, kv-head) every selected COMPLETE page is a hit
+ * (resident: its LRU clock is touched) or a miss; per kv-head the distinct new misses, in
+ * (request, position) order, take the least-recently-used slots not touched this step
+ * (ties -> lower slot), evicting their old pages; installed misses are appended to the
+ * flat fetch list (kv, blk, slot).  clock is advanced by one on device first. */
+typedef struct amass_tier_plan_args {
+    const int32_t* page_table; int64_t pt_sr, pt_sh;
+    const int32_t* page_cnt;   int64_t pc_sr;
+    const int32_t* block_table; int64_t bt_st;
+    const int32_t* seq_lens;
+    int32_t* page2slot;      /* (n_kv,NB) this layer   */
+    int32_t* slot2page;      /* (n_kv,S) this layer    */
+    int32_t* lru_clock;      /* (n_kv,S) this layer    */
+    int32_t* clock;          /* (1,)                   */
+    int32_t* miss_pages;     /* (R,n_kv,MP) scratch    */
+    int32_t* miss_cnt;       /* (R,n_kv)               */
+    int32_t* victim_slots;   /* (R,n_kv,MP)            */
+    int32_t* overflow;       /* (1,) latch             */
+    int32_t* fetch_list;     /* (FCAP,3)               */
+    int32_t* fetch_cnt;      /* (1,)                   */
+    int32_t* first_pos;      /* (n_kv,NB) scratch, INT32_MAX at rest (dedup) */
+    int32_t n_req, n_kv, nb, slots, max_pages, page, fcap;
+} amass_tier_plan_args;
+int amass_tier_gather_plan(const amass_tier_plan_args* a, void* stream);
+
+/* Replaces tier/residency.py:196-248,409-436 (_fetch_flat_kernel / gather_fetch): copy
+ * each (kv, blk, slot) of the flat fetch list into the hot buffer from the pinned pool if
+ * pool_valid, else from the staged pool (vbo >= 0, with write-through to the pinned pool
+ * and pool_valid set), else from the pinned pool.  Pure 16-bit copies. */
+typedef struct amass_tier_fetch_args {
+    const int32_t* fetch_list;
+    const int32_t* fetch_cnt;
+    void*          hot;        /* (n_kv,S,page,d) this layer */
+    void*          pool;       /* pinned pool device pointer (L,NB,n_kv,page,d) */
+    const void*    vpool; int64_t v_sb, v_st, v_sh;   /* staged pool view of this layer */
+    const int32_t* vbo;
+    int8_t*        pool_valid; /* (n_kv,NB) this layer */
+    int32_t t_layer, nb, n_kv, slots, page, d, fcap, grid;
+} amass_tier_fetch_args;
+int amass_tier_fetch(const amass_tier_fetch_args* a, void* stream);
+
+/* Replaces tier/decode_mem.py:169-222 (mem_decode_ptrsel): the decode with v_src = 1. */
+int amass_tier_decode(const amass_decode_args* a, void* stream);
+
+/* Copy-engine gather of pinned pages into hot slots (tier/dma.py:77-140, residency.py:
+ * 438-525): n runs of (dst, src, dpitch, spitch, width_bytes, height) issued as 2-D
+ * host-to-device copies on `stream` (a side stream). */
+typedef struct amass_copy_run {
+    void* dst; const void* src; int64_t dpitch, spitch, width, height;
+} amass_copy_run;
+int amass_tier_dma(const amass_copy_run* runs, int32_t n, void* stream);
+
+/* Pinned, device-mapped host memory (tier/pool.py:65-79,104-151 MappedHostVPool):
+ * hipHostMalloc(hipHostMallocMapped) + hipHostGetDevicePointer. */
+int amass_host_pool_alloc(size_t bytes, void** host_ptr, void** dev_ptr);
+int amass_host_pool_free(void* host_ptr);
+
+/* ---- introspection (host only, no GPU needed) --------------------------------------- */
+int         amass_abi_version(void);
+size_t      amass_abi_struct_size(int which); /* 0 quad,1 r8,2 derive,3 nrm,4 select,
+                                                 5 decode,6 plan,7 fetch,8 copy_run */
+const char* amass_status_string(int status);
+int         amass_last_hip_error(void);      /* last hipError_t seen by the library */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AMASS_HIP_H */

@@ -1,0 +1,132 @@
+"""GPU parity of the sparse / dense paged decode against the fp64 oracle.
+
+Bar (BASELINE): outputs within 2e-2 absolute / 1e-2 relative of the fp64 softmax
+attention.  Covers split-K + merge, the fused single pass, the dense baseline, G = 4 / 8,
+partial last pages whose unused slots hold NaN (must be masked), padded rows (zero
+output), empty and single-page selections.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.decode as odec
+import oracle.select as osel
+from amass.attention import ensure_stage_b_buffers
+from amass.attention.decode import ResidentVSource, dense_paged_decode, sparse_paged_decode_batched
+from amass.bench.synth import make_case
+from helpers import announce, npf, npi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ATOL, RTOL = 2e-2, 1e-2
+
+
+class _St:
+    pass
+
+
+def _case(B, G, seed, partial=True):
+    case = make_case(B=B, ctx=(200, 3000), n_kv=8, G=G, heavy=0.0, table="perm", seed=seed)
+    sl = case.seq_lens.clone()
+    if partial:
+        sl = sl - torch.arange(B, dtype=torch.int32) % 13   # ragged partial last pages
+        sl = torch.clamp(sl, min=1)
+        # poison the unused token slots of every request's last page
+        for r in range(B):
+            n = int(sl[r])
+            last = (n - 1) // 16
+            blk = int(case.block_table[r, last])
+            t0 = n - last * 16
+            if t0 < 16:
+                case.kv_cache[blk, :, t0:] = float("nan")
+    case.seq_lens = sl.to(torch.int32)
+    return case
+
+
+def _selection(case, frac, seed, empty_unit=False):
+    B, n_kv, MP = case.q.shape[0], case.n_kv, case.max_pages
+    gen = torch.Generator().manual_seed(seed)
+    sc = torch.randn(B, n_kv, MP, generator=gen).numpy()
+    npg, nsh, bfix = osel.derive(case.seq_lens.numpy(), frac, 16, 1, 1)
+    tab, cnt, _ = osel.select(sc, npg, nsh, bfix, sink=1, max_pages=MP, mode=0)
+    if empty_unit:
+        cnt[0, 0] = 0
+        tab[0, 0, :] = -1
+    return tab, cnt
+
+
+def _st(case, tab, cnt):
+    st = _St()
+    st.max_reqs, st.n_kv, st.G, st.D = case.q.shape[0], case.n_kv, case.G, case.d
+    st.page_table = torch.from_numpy(tab).to(DEV)
+    st.page_cnt = torch.from_numpy(cnt).to(DEV)
+    ensure_stage_b_buffers(st, DEV)
+    return st
+
+
+def _np_inputs(case):
+    return (npf(case.q), npf(case.kv_cache[:, 0]), npf(case.kv_cache[:, 1]),
+            npi(case.block_table), npi(case.seq_lens))
+
+
+@pytest.mark.parametrize("G", [4, 8])
+@pytest.mark.parametrize("path", ["split", "fused"])
+@pytest.mark.parametrize("frac", [0.05, 0.5])
+def test_sparse_decode(G, path, frac):
+    announce(f"sparse decode G={G} path={path} frac={frac}")
+    case = _case(5, G, seed=G * 10 + int(frac * 100))
+    tab, cnt = _selection(case, frac, seed=1, empty_unit=True)
+    q, K, V, bt, sl = _np_inputs(case)
+    ref = odec.attend(q, K, V, bt, sl, tab, cnt, scale=case.scale, G=G)
+    kv = case.kv_cache.to(DEV)
+    st = _st(case, tab, cnt)
+    out = torch.full((5, 8 * G, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    sparse_paged_decode_batched(case.q.to(DEV), kv, case.block_table.to(DEV),
+                                case.seq_lens.to(DEV), st, out, ResidentVSource(kv),
+                                scale=case.scale, path=path)
+    torch.cuda.synchronize()
+    got = npf(out)
+    assert np.isfinite(got).all()
+    assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
+    # the empty unit (req 0, kv-head 0) writes zeros
+    assert np.all(got[0, :G] == 0)
+
+
+@pytest.mark.parametrize("G", [4, 8])
+@pytest.mark.parametrize("path", ["split", "fused"])
+def test_dense_decode(G, path):
+    announce(f"dense decode G={G} path={path}")
+    case = _case(4, G, seed=40 + G)
+    q, K, V, bt, sl = _np_inputs(case)
+    ref = odec.attend(q, K, V, bt, sl, scale=case.scale, G=G, dense=True)
+    kv = case.kv_cache.to(DEV)
+    st = _St()
+    st.max_reqs, st.n_kv, st.G, st.D = 4, 8, G, 128
+    ensure_stage_b_buffers(st, DEV)
+    out = torch.zeros((4, 8 * G, 128), dtype=torch.bfloat16, device=DEV)
+    dense_paged_decode(case.q.to(DEV), kv, case.block_table.to(DEV), case.seq_lens.to(DEV),
+                       st, out, scale=case.scale, path=path)
+    torch.cuda.synchronize()
+    got = npf(out)
+    assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
+
+
+def test_split_equals_fused_and_padded_rows():
+    announce("split vs fused, padded rows")
+    case = _case(4, 4, seed=77, partial=False)
+    case.seq_lens[3] = 0
+    tab, cnt = _selection(case, 0.2, seed=2)
+    cnt[3] = 0
+    tab[3] = -1
+    kv = case.kv_cache.to(DEV)
+    st = _st(case, tab, cnt)
+    outs = []
+    for path in ("split", "fused"):
+        out = torch.full((4, 32, 128), 7.0, dtype=torch.bfloat16, device=DEV)
+        sparse_paged_decode_batched(case.q.to(DEV), kv, case.block_table.to(DEV),
+                                    case.seq_lens.to(DEV), st, out, ResidentVSource(kv),
+                                    scale=case.scale, path=path)
+        outs.append(npf(out))
+    torch.cuda.synchronize()
+    assert np.all(outs[0][3] == 0) and np.all(outs[1][3] == 0)
+    assert np.allclose(outs[0], outs[1], atol=1e-2, rtol=1e-2)

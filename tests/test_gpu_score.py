@@ -1,0 +1,137 @@
+"""GPU parity of the quad and r8 page-score kernels against the CPU oracle.
+
+Bar: the int32 d-contractions (comb_out) are bit-exact against int64 brute force; quad
+scores within |d| <= 1e-3 * max(|ref|, 1) of the fp64 oracle with unquantised q (the
+Triton reference semantics, BASELINE tolerance 1e-3 relative) and within 2e-5 of the
+oracle that uses the 2-limb q code; nrm-combined scores within 1e-4 relative; r8 scores
+within 1e-3 likewise.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.score as osc
+import oracle.select as osel
+from amass.bench.synth import build_quad_state, build_r8_state, make_case
+from amass.selection import derive_page_params, nrm_combine, r8_score
+from amass.selection.quad_score import quad_score_launch
+from helpers import announce, npf, npi, rel_close, to_device, case_to
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _quad_setup(rank, v_bits, G, combine, seed=0, B=3):
+    case = make_case(B=B, ctx=(300, 1400), n_kv=8, G=G, heavy=0.05, table="perm", seed=seed)
+    st = build_quad_state(case, rank=rank, v_bits=v_bits, combine=combine, budget=0.05)
+    to_device(st, DEV)
+    case_to(case, DEV)
+    derive_page_params(st, case.seq_lens, B)
+    return case, st
+
+
+def _oracle_inputs(case, st):
+    mu, mus, V, Vs, sg, _ = st.layer_state(0)
+    return dict(q=npf(case.q), mu=npi(mu), mu_scale=npf(mus), V=npi(V), V_scale=npf(Vs),
+                sig2=npf(sg), block_table=npi(case.block_table), n_sel_hi=npi(st.n_sel_hi))
+
+
+@pytest.mark.parametrize("rank,v_bits", [(2, 8), (4, 8), (8, 8), (2, 4), (4, 4), (8, 4)])
+@pytest.mark.parametrize("G", [4, 8])
+def test_quad_comb_exact_and_scores(rank, v_bits, G):
+    announce(f"quad rank={rank} v_bits={v_bits} G={G}")
+    case, st = _quad_setup(rank, v_bits, G, "max")
+    B, MP = case.q.shape[0], st.max_pages
+    npg, nsh, bfix = osel.derive(npi(case.seq_lens), st.budget, 16, 1, 1)
+    assert np.array_equal(npi(st.n_pages), npg) and np.array_equal(npi(st.n_sel_hi), nsh)
+    assert np.array_equal(npi(st.b_fix), bfix)
+    comb = torch.zeros(B, 8, MP, G, rank + 1, dtype=torch.int32, device=DEV)
+    st.score.fill_(float("nan"))
+    quad_score_launch(st, 0, case.q, case.block_table, B, case.scale, comb_out=comb)
+    torch.cuda.synchronize()
+    o = _oracle_inputs(case, st)
+    ref_comb = osc.quad_comb(o["q"], o["mu"], o["V"], o["block_table"], o["n_sel_hi"], G=G,
+                             v_bits=v_bits, max_pages=MP)
+    got = npi(comb).astype(np.int64)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n]), f"comb mismatch req {r}"
+    kw = dict(scale=case.scale, page=16, G=G, v_bits=v_bits, max_pages=MP)
+    ref_f = osc.quad_score(**o, **kw, combine="max", q_mode="float")
+    ref_l = osc.quad_score(**o, **kw, combine="max", q_mode="limbs")
+    sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert rel_close(sc[r, :, :n], ref_f[r, :, :n], 1) <= 1e-3
+        assert rel_close(sc[r, :, :n], ref_l[r, :, :n], 1) <= 2e-5
+
+
+@pytest.mark.parametrize("rank,v_bits", [(8, 8), (2, 4)])
+def test_quad_nrm(rank, v_bits):
+    announce(f"quad nrm rank={rank} v_bits={v_bits}")
+    case, st = _quad_setup(rank, v_bits, 4, "nrm", seed=3)
+    B, MP = case.q.shape[0], st.max_pages
+    quad_score_launch(st, 0, case.q, case.block_table, B, case.scale)
+    nrm_combine(st, B)
+    torch.cuda.synchronize()
+    o = _oracle_inputs(case, st)
+    ref_h = osc.quad_score(**o, scale=case.scale, page=16, G=4, v_bits=v_bits, max_pages=MP,
+                           combine="nrm", q_mode="float")
+    sh = npf(st.score_h)
+    nsh = npi(st.n_sel_hi)
+    for r in range(B):
+        n = int(nsh[r])
+        assert rel_close(sh[r, :, :, :n], ref_h[r, :, :, :n], 1) <= 1e-3
+    # nrm of the GPU's own per-head scores: fp64 oracle vs the fp32 kernel
+    ref_n = osc.nrm_combine(sh.astype(np.float64), nsh)
+    sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert rel_close(sc[r, :, :n], ref_n[r, :, :n], 1) <= 1e-5
+
+
+def test_quad_padded_rows_untouched():
+    """Rows with seq_len 0 (n_sel_hi < 0) write nothing."""
+    announce("quad padded rows")
+    case = make_case(B=2, ctx=(200, 400), n_kv=8, G=4, seed=5)
+    st = build_quad_state(case, rank=2, v_bits=8, combine="max", max_reqs=3)
+    to_device(st, DEV)
+    case_to(case, DEV)
+    sl = torch.cat([case.seq_lens, torch.zeros(1, dtype=torch.int32, device=DEV)])
+    bt = torch.cat([case.block_table, case.block_table[:1]])
+    q = torch.cat([case.q, case.q[:1]])
+    derive_page_params(st, sl, 3)
+    st.score.fill_(123.0)
+    quad_score_launch(st, 0, q, bt, 3, case.scale)
+    torch.cuda.synchronize()
+    assert bool((st.score[2] == 123.0).all())
+
+
+@pytest.mark.parametrize("vk_bits,c_bits", [(8, 8), (4, 4), (8, 4)])
+@pytest.mark.parametrize("G", [4, 8])
+def test_r8_comb_exact_and_scores(vk_bits, c_bits, G):
+    announce(f"r8 vk={vk_bits} c={c_bits} G={G}")
+    case = make_case(B=3, ctx=(300, 1400), n_kv=8, G=G, seed=11)
+    st = build_r8_state(case, vk_bits=vk_bits, c_bits=c_bits)
+    to_device(st, DEV)
+    case_to(case, DEV)
+    B, MP = 3, st.max_pages
+    derive_page_params(st, case.seq_lens, B)
+    comb = torch.zeros(B, 8, MP, G, 9, dtype=torch.int32, device=DEV)
+    r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
+    torch.cuda.synchronize()
+    mu, mus, Vk, Vks, c, cs, _ = st.layer_state(0)
+    nsh = npi(st.n_sel_hi)
+    ref_comb = osc.r8_comb(npf(case.q), npi(mu), npi(Vk), npi(case.block_table), nsh, G=G,
+                           vk_bits=vk_bits, max_pages=MP)
+    got = npi(comb).astype(np.int64)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
+    ref = osc.r8_score(npf(case.q), npi(mu), npf(mus), npi(Vk), npf(Vks), npi(c), npf(cs),
+                       npi(case.block_table), npi(case.seq_lens), nsh, scale=case.scale,
+                       page=16, G=G, vk_bits=vk_bits, c_bits=c_bits, max_pages=MP)
+    sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3

@@ -1,0 +1,148 @@
+"""GPU parity of derive / top-b / coverage selection against the CPU oracle.
+
+Bar: given the same scores, page_table, page_cnt and the chosen count are bit-exact for
+both tie rules (lower page index; the reference's keep-all-ties threshold), both nucleus
+mass kinds, forced ties, padded rows, short sequences, b >= S, and up to 8192 pages.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.select as osel
+from amass.selection import QuadState, coverage_select, derive_page_params, topb_select
+from amass.selection.select import select_pages
+from helpers import announce, npf, npi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _state(R, MP, G=4, n_kv=8, budget=0.05, combine="max"):
+    st = QuadState(DEV, num_layers=1, num_blocks=4, n_kv=n_kv, G=G, head_dim=128, page=16,
+                   max_reqs=R, max_pages=MP, rank=2, budget=budget, combine=combine)
+    return st
+
+
+def _seq_lens(R, MP, gen, special=True):
+    sl = torch.randint(16, MP * 16 + 1, (R,), generator=gen).to(torch.int32)
+    if special and R >= 4:
+        sl[0] = 0            # padded row
+        sl[1] = 20           # 2 pages: S <= 1 -> keep all
+        sl[2] = MP * 16      # full
+        sl[3] = 3 * 16 + 5   # partial tail page
+    return sl
+
+
+def _scores(R, n_kv, MP, gen, ties: bool, kind: int):
+    if kind == 1:
+        sc = torch.rand(R, n_kv, MP, generator=gen) * 4.0
+    else:
+        sc = torch.randn(R, n_kv, MP, generator=gen) * 3.0
+    if ties:
+        sc = torch.round(sc * 4) / 4            # many exact ties
+    return sc
+
+
+def _run(st, R, mode, tie, kind, cov, gen, ties, MP):
+    sl = _seq_lens(R, MP, gen)
+    sl_d = sl.to(DEV)
+    derive_page_params(st, sl_d, R)
+    sc = _scores(R, st.n_kv, MP, gen, ties, kind)
+    st.score.copy_(sc.to(DEV))
+    st.page_table.fill_(-7)
+    st.combine = "nrm" if kind == 1 else "max"
+    if mode == 0:
+        topb_select(st, R, tie_mode=["index", "all"][tie])
+    else:
+        coverage_select(st, R, cov, tie_mode=["index", "all"][tie])
+    torch.cuda.synchronize()
+    npg, nsh, bfix = npi(st.n_pages), npi(st.n_sel_hi), npi(st.b_fix)
+    ref_tab, ref_cnt, ref_nsel = osel.select(sc.numpy(), npg, nsh, bfix, sink=1, max_pages=MP,
+                                             mode=mode, coverage=cov, tie_mode=tie,
+                                             score_kind=kind)
+    got_tab, got_cnt, got_nsel = npi(st.page_table), npi(st.page_cnt), npi(st.n_sel)
+    assert np.array_equal(got_cnt, ref_cnt)
+    assert np.array_equal(got_tab, ref_tab)
+    if tie == 0:
+        assert np.array_equal(got_nsel, ref_nsel)
+    return got_cnt
+
+
+@pytest.mark.parametrize("tie", [0, 1])
+@pytest.mark.parametrize("ties", [False, True])
+@pytest.mark.parametrize("MP", [37, 1024])
+def test_topb(tie, ties, MP):
+    announce(f"topb tie={tie} ties={ties} MP={MP}")
+    gen = torch.Generator().manual_seed(100 + MP + tie)
+    R = 6
+    st = _state(R, MP, budget=0.07)
+    _run(st, R, 0, tie, 0, 1.0, gen, ties, MP)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("tie", [0, 1])
+@pytest.mark.parametrize("cov", [0.5, 0.95, 1.0])
+@pytest.mark.parametrize("ties", [False, True])
+def test_coverage(kind, tie, cov, ties):
+    announce(f"coverage kind={kind} tie={tie} cov={cov} ties={ties}")
+    gen = torch.Generator().manual_seed(int(cov * 100) + 7 * kind + tie)
+    R, MP = 6, 700
+    st = _state(R, MP)
+    _run(st, R, 1, tie, kind, cov, gen, ties, MP)
+
+
+def test_budget_one_keeps_all():
+    announce("budget 1.0")
+    gen = torch.Generator().manual_seed(3)
+    R, MP = 4, 300
+    st = _state(R, MP, budget=1.0)
+    cnt = _run(st, R, 0, 0, 0, 1.0, gen, False, MP)
+    npg = npi(st.n_pages)
+    for r in range(R):
+        assert (cnt[r] == max(npg[r], 0)).all()
+
+
+def test_long_context_8192_pages():
+    announce("topb + coverage at MP=8192")
+    gen = torch.Generator().manual_seed(9)
+    R, MP = 2, 8192
+    st = _state(R, MP, G=8, budget=0.02)
+    _run(st, R, 0, 0, 0, 1.0, gen, False, MP)
+    _run(st, R, 1, 0, 1, 0.95, gen, False, MP)
+
+
+def test_nrm_fused_into_select():
+    """select_pages with score_h: st.score equals the standalone nrm combine and the
+    selection equals the oracle's on that score."""
+    announce("nrm fused select")
+    gen = torch.Generator().manual_seed(21)
+    R, MP, G = 5, 513, 4
+    st = _state(R, MP, G=G, combine="nrm")
+    st.coverage = 0.9
+    sl = _seq_lens(R, MP, gen).to(DEV)
+    derive_page_params(st, sl, R)
+    st.score_h.copy_((torch.randn(R, 8, G, MP, generator=gen) * 2).to(DEV))
+    select_pages(st, R, score_h=st.score_h)
+    torch.cuda.synchronize()
+    got_score = npf(st.score)
+    got_tab = npi(st.page_table)
+    from amass.selection import nrm_combine
+    st.score.fill_(0)
+    nrm_combine(st, R)
+    torch.cuda.synchronize()
+    nsh = npi(st.n_sel_hi)
+    ref_score = npf(st.score)
+    for r in range(R):
+        n = max(int(nsh[r]), 0)
+        assert np.array_equal(got_score[r, :, :n], ref_score[r, :, :n])
+    ref_tab, _, _ = osel.select(got_score, npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                                max_pages=MP, mode=1, coverage=0.9, tie_mode=0, score_kind=1)
+    assert np.array_equal(got_tab, ref_tab)
+
+
+def test_config0_known_answer():
+    """Config 0: B=1, ctx 4096, fixed 5% budget -> S = 254, b = 13."""
+    st = _state(1, 256, budget=0.05)
+    derive_page_params(st, torch.tensor([4096], dtype=torch.int32, device=DEV), 1)
+    torch.cuda.synchronize()
+    assert int(st.n_pages[0]) == 256 and int(st.n_sel_hi[0]) == 255 and int(st.b_fix[0]) == 13
