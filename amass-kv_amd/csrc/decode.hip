@@ -220,7 +220,8 @@ __global__ __launch_bounds__(SPLIT_WAVES * WAVE) void decode_split_kernel(const 
     WaveState st;
     init_state(st);
     attend_run(a, r, kh, sl, j0, j1, 1, lane, qb, st);
-    const float lt = st.l + __shfl_xor(st.l, 16, WAVE) + __shfl_xor(st.l, 32, WAVE);
+    float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
+    lt += __shfl_xor(lt, 32, WAVE);
     const int64_t base = (((int64_t)r * a.n_kv + kh) * a.split + sp) * a.G;
     if (lane < a.G) {
         a.m_part[base + lane] = st.m;
@@ -282,7 +283,8 @@ __global__ __launch_bounds__(FUSED_WAVES * WAVE) void decode_fused_kernel(const 
         load_q(a, r, kh, lane, qb);
         attend_run(a, r, kh, sl, w, cnt, FUSED_WAVES, lane, qb, st);
     }
-    const float lt = st.l + __shfl_xor(st.l, 16, WAVE) + __shfl_xor(st.l, 32, WAVE);
+    float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
+    lt += __shfl_xor(lt, 32, WAVE);
     if (lane < a.G) {
         sm_m[w][lane] = st.m;
         sm_l[w][lane] = lt;
