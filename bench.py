@@ -50,19 +50,26 @@ def graph_of(fn, reps=1):
     return g
 
 
-def time_graph(g, steps, warmup, reps=1):
-    """Average ms per call of a graph holding `reps` calls (events on the replay stream)."""
+def time_graph(g, steps, warmup, reps=1, batches=7):
+    """Median over `batches` of the average ms per call of `steps` back-to-back replays of
+    a graph holding `reps` calls (one event pair per batch on the replay stream) -- the
+    reference's median-of-batches graph timing (bench/timing.py:71-117)."""
+    import statistics
+
     import torch
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(steps):
-        g.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / (steps * reps)
+    out = []
+    for _ in range(batches):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) / (steps * reps))
+    return statistics.median(out)
 
 
 def quad_score_bytes(st, n_req, G):

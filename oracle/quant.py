@@ -4,7 +4,9 @@ q_limbs   -- the 2-limb int8 query code of the reference's int kernels
              (selection/quad_score_cuda.py:902-935, selection/score_cuda.py:182-215):
              qs = max(amax|q|, 1e-12)/16383, qi = rn(q/qs) in [-16383, 16383],
              hi = rn(qi/128) in [-127, 127], lo = qi - 128 hi  (so 128 hi + lo == qi).
-             The divide is IEEE fp32 (the reference compiles with --use_fast_math).
+             The reference divides with --use_fast_math; this build fixes the rounding as
+             m = max(amax, 1e-12), qs = m/16383 and inv = 16383/m (IEEE fp32 divides) and
+             qi = rn(fp32(q * inv)).
 quant     -- summary codes (selection/build.py:297-301): lvl = 2^(bits-1)-1,
              s = max(amax/lvl, 1e-8) fp32, code = clip(rint(x/s), -lvl, lvl).
 pack_i4   -- selection/build.py:304-312: byte = lo nibble (even column) | hi << 4.
@@ -26,9 +28,10 @@ def bf16_round(x) -> np.ndarray:
 def q_limbs(q):
     """q (..., d) -> (qi int64, hi int64, lo int64, qs float32) per the reference recipe."""
     q = np.asarray(q, np.float32)
-    amax = np.abs(q).max(axis=-1)
-    qs = (np.maximum(amax, F32(1e-12)) / F32(16383)).astype(np.float32)
-    qi = np.clip(np.rint(q / qs[..., None]), -16383, 16383).astype(np.int64)
+    m = np.maximum(np.abs(q).max(axis=-1), F32(1e-12)).astype(np.float32)
+    qs = (m / F32(16383)).astype(np.float32)
+    inv = (F32(16383) / m).astype(np.float32)
+    qi = np.clip(np.rint((q * inv[..., None]).astype(np.float32)), -16383, 16383).astype(np.int64)
     hi = np.clip(np.rint(qi.astype(np.float32) * F32(0.0078125)), -127, 127).astype(np.int64)
     lo = np.clip(qi - 128 * hi, -127, 127)
     return qi, hi, lo, qs
