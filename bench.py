@@ -147,6 +147,8 @@ def main():
     ap.add_argument("--boost", default="sigma", choices=["sigma", "keynorm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path has no "
@@ -164,6 +166,14 @@ def main():
     from amass.selection.select import select_pages
 
     dev = "cuda"
+    if args.copy_calibration:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 256 MiB device copies done")
+        del src, dst
     t0 = time.time()
     case = config_case(1, seed=args.seed, device=dev, boost=args.boost)
     log(f"inputs generated ({time.time() - t0:.1f}s)")
