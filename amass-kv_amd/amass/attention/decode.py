@@ -88,6 +88,9 @@ def _decode_args(q, k, vsource, block_table, seq_lens, st, out, scale, n_req, *,
     if not dense:
         table = st.page_table if table is None else table
         cnt = st.page_cnt if cnt is None else cnt
+    if path != "fused" and getattr(st, "m_part", None) is None:
+        raise ValueError("split-K partials missing: call ensure_stage_b_buffers(st, device) "
+                         "once before decoding (outside any graph capture)")
     tf = vsource.tier_fields()
     return DecodeArgs(
         q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),

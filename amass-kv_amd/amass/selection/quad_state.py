@@ -86,3 +86,17 @@ class QuadState:
         """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer``."""
         return (self.quad_mu[layer], self.mu_scale[layer], self.quad_V[layer],
                 self.V_scale[layer], self.quad_sig2[layer], self.quad_tag[layer])
+
+    def load_reference(self, layer: int, mu, mu_scale, V, V_scale, sig2) -> None:
+        """Write one layer's summaries given in the reference layout
+        (``selection/quad_state.py:36-151``: quad_V (NB, n_kv, d, r'[/2]))."""
+        dev = self.quad_mu.device
+        self.quad_mu[layer].copy_(torch.as_tensor(mu).to(dev))
+        self.mu_scale[layer].copy_(torch.as_tensor(mu_scale).to(dev))
+        self.quad_V[layer].copy_(torch.as_tensor(V).to(dev))
+        self.V_scale[layer].copy_(torch.as_tensor(V_scale).to(dev))
+        self.quad_sig2[layer].copy_(torch.as_tensor(sig2).to(dev))
+
+    def reference_V(self, layer: int) -> torch.Tensor:
+        """quad_V of ``layer`` in the reference layout (NB, n_kv, d, r'[/2])."""
+        return self.quad_V[layer]

@@ -118,9 +118,11 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 }
 
 // ---------------------------------------------------------------- order keys
-// fp32 -> order-preserving uint32 (ascending float order == ascending uint order)
+// fp32 -> order-preserving uint32 (ascending float order == ascending uint order).
+// -0.0 maps to the key of +0.0: the two compare equal, so they tie (lower index wins).
 __device__ __forceinline__ uint32_t f2u(float f) {
     uint32_t u = __float_as_uint(f);
+    u = (u == 0x80000000u) ? 0u : u;
     uint32_t mask = (uint32_t)(-(int32_t)(u >> 31)) | 0x80000000u;
     return u ^ mask;
 }

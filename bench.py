@@ -148,7 +148,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a plain 256 MiB device copy (HBM counter calibration)")
+                    help="also run a plain 256 MiB read + 256 MiB write kernel (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path has no "
@@ -170,7 +170,7 @@ def main():
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).normal_()
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.neg(src, out=dst)     # one elementwise kernel: reads 256 MiB, writes 256 MiB
         torch.cuda.synchronize()
         log("copy calibration: 3 x 256 MiB device copies done")
         del src, dst

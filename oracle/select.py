@@ -43,8 +43,9 @@ def derive(seq_lens, budget: float, page: int, window: int, sink: int):
 
 
 def f2u(x):
-    """fp32 -> order-preserving uint32 keys."""
+    """fp32 -> order-preserving uint32 keys (-0.0 shares +0.0's key: they compare equal)."""
     u = np.asarray(x, np.float32).view(np.uint32)
+    u = np.where(u == np.uint32(0x80000000), np.uint32(0), u)
     mask = np.where(u >> 31, np.uint32(0xFFFFFFFF), np.uint32(0x80000000))
     return u ^ mask
 

@@ -8,6 +8,8 @@ import pytest
 
 from amass import _hip
 
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
                       "include", "amass_hip.h")
 
@@ -84,3 +86,15 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_hip, "_LIB", None)
     with pytest.raises(_hip.AmassError, match="missing"):
         _hip.load_library(str(tmp_path / "nope.so"))
+
+
+def test_product_never_imports_the_oracle():
+    """The shipped package has no CPU fallback: nothing under amass-kv_amd imports oracle."""
+    import re
+    pkg = os.path.join(ROOT, "amass-kv_amd")
+    pat = re.compile(r"^\s*(from\s+oracle\b|import\s+oracle\b)", re.M)
+    for dp, _dn, fns in os.walk(pkg):
+        for fn in fns:
+            if fn.endswith((".py", ".hip", ".h", ".cpp")):
+                with open(os.path.join(dp, fn)) as f:
+                    assert not pat.search(f.read()), os.path.join(dp, fn)

@@ -40,6 +40,8 @@ def _scores(R, n_kv, MP, gen, ties: bool, kind: int):
         sc = torch.randn(R, n_kv, MP, generator=gen) * 3.0
     if ties:
         sc = torch.round(sc * 4) / 4            # many exact ties
+        sc[..., 5::11] = -0.0                   # -0.0 and +0.0 compare equal: one tie class
+        sc[..., 9::13] = 0.0
     return sc
 
 
