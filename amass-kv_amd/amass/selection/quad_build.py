@@ -3,7 +3,8 @@
 Restates selection/quad_build.py:56-198 of the reference: the same page-gram eigh as the
 r8 builder (:mod:`amass.selection.build`), storing the top-r' eigenvalues ``sig2`` instead
 of the per-key coordinates.  Per (block, kv-head): quad_mu/mu_scale = int8 page mean,
-quad_V/V_scale = Vk = dc^T U8 / S8 quantised per column (int8 or packed int4),
+quad_V/V_scale = Vk = dc^T U8 / S8 quantised per column (int8 or packed int4, stored
+in the column-major kernel layout),
 quad_sig2 = fp16(S2r), quad_tag = leading TAGW channels of the page's last key.
 """
 from __future__ import annotations
@@ -12,6 +13,7 @@ import torch
 
 from .build import (CHUNK, _page_eigh, _quant_mu, _quant_vk, _refresh, _tail_blocks,
                     finalized_blocks)
+from .quad_state import v_to_device
 
 
 def quad_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> None:
@@ -20,7 +22,7 @@ def quad_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> N
     v_code, v_s = _quant_vk(Vk, st.v_grain, st.v_bits)
     st.quad_mu[layer, blocks] = mu_code
     st.mu_scale[layer, blocks] = mu_s
-    st.quad_V[layer, blocks] = v_code
+    st.quad_V[layer, blocks] = v_to_device(v_code, st.v_bits)
     st.V_scale[layer, blocks] = v_s
     st.quad_sig2[layer, blocks] = S2r.to(st.quad_sig2.dtype)
     st.quad_tag[layer, blocks] = Kp_flat[:, st.page - 1, :, :st.tagw].to(st.quad_tag.dtype)

@@ -24,6 +24,9 @@ def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadSc
         raise ValueError("block_table must be int32 with unit column stride")
     if block_table.shape[1] < st.max_pages - st.window_pages:
         raise ValueError("block_table narrower than the scored page range")
+    if V.stride(3) != 1 or V.stride(2) != V.shape[3] or V.stride(1) != V.shape[2] * V.shape[3] \
+            or mu.stride(2) != 1 or mu.stride(1) != mu.shape[2]:
+        raise ValueError("quad_V / quad_mu must be contiguous inside each block")
     nrm = st.combine == "nrm"
     sh = st.score_h
     return QuadScoreArgs(

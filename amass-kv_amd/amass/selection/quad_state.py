@@ -1,23 +1,60 @@
 """QuadState -- persistent buffers of the quad (Gaussian-MGF quadratic) selector.
 
-Same tensors, dtypes and layout as the reference (``selection/quad_state.py:36-151``):
+The tensors, dtypes and shapes of the reference (``selection/quad_state.py:36-151``),
+except that quad_V is stored column-major per (block, kv-head):
 
   quad_mu    (L, NB, n_kv, d)       int8   + mu_scale  (L, NB, n_kv)      fp16
-  quad_V     (L, NB, n_kv, d, r')   int8   + V_scale   (L, NB, n_kv, r')  fp16 (per column)
-             int4: (L, NB, n_kv, d, r'/2), byte = lo nibble (even column) | hi << 4
+  quad_V     (L, NB, n_kv, r', d)   int8   + V_scale   (L, NB, n_kv, r')  fp16 (per column)
+             int4: (L, NB, n_kv, r', d/2), byte j = code[j] | code[j + d/2] << 4
+             (the reference keeps (.., d, r') with two columns per int4 byte)
   quad_sig2  (L, NB, n_kv, r')      fp16   eigenvalues of the page's centred key scatter
   quad_tag   (L, NB, n_kv, TAGW)    bf16   NaN-init content tag
 
+Column-major V lets the gfx950 score kernel feed each 16-byte load straight into an
+int8 matrix-core instruction (16 consecutive d of one column of one page), and makes
+the two K-halves of a column one 128-byte line.  ``v_to_device`` / ``v_to_reference``
+convert between the two layouts; ``load_reference`` and ``reference_V`` use them.
+
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
-(R, n_kv, G, MP) and hmax (R, n_kv, G).  The physical-block-keyed slabs put all n_kv
-heads of a page next to each other (8 KB for r'=8 int8 V), which is what lets one
-gfx950 wave read a whole page's summaries with coalesced 16-byte loads.
+(R, n_kv, G, MP) and hmax (R, n_kv, G).
 """
 from __future__ import annotations
 
 import torch
 
 from .state import TAGW
+
+
+def _unpack_pairs(packed: torch.Tensor) -> torch.Tensor:
+    b = packed.view(torch.uint8).to(torch.int32)
+    lo, hi = b & 0xF, (b >> 4) & 0xF
+    lo = torch.where(lo >= 8, lo - 16, lo)
+    hi = torch.where(hi >= 8, hi - 16, hi)
+    return lo, hi
+
+
+def v_to_device(v_ref: torch.Tensor, v_bits: int) -> torch.Tensor:
+    """Reference quad_V (..., d, r') int8 or (..., d, r'/2) packed int4 (lo nibble = even
+    column) -> the kernel layout (..., r', d) int8 or (..., r', d/2) packed halves."""
+    if v_bits == 8:
+        return v_ref.transpose(-1, -2).contiguous()
+    lo, hi = _unpack_pairs(v_ref)                       # columns 2c, 2c+1
+    code = torch.stack([lo, hi], dim=-1).flatten(-2)    # (..., d, r')
+    code = code.transpose(-1, -2)                       # (..., r', d)
+    half = code.shape[-1] // 2
+    packed = (code[..., :half] & 0xF) | ((code[..., half:] & 0xF) << 4)
+    return packed.to(torch.uint8).view(torch.int8).contiguous()
+
+
+def v_to_reference(v_dev: torch.Tensor, v_bits: int) -> torch.Tensor:
+    """Inverse of :func:`v_to_device`."""
+    if v_bits == 8:
+        return v_dev.transpose(-1, -2).contiguous()
+    lo, hi = _unpack_pairs(v_dev)                       # d = j, j + d/2
+    code = torch.cat([lo, hi], dim=-1)                  # (..., r', d)
+    code = code.transpose(-1, -2)                       # (..., d, r')
+    packed = (code[..., 0::2] & 0xF) | ((code[..., 1::2] & 0xF) << 4)
+    return packed.to(torch.uint8).view(torch.int8).contiguous()
 
 
 class QuadState:
@@ -55,10 +92,10 @@ class QuadState:
         self.device = device
         i8, f16, bf16 = torch.int8, torch.float16, torch.bfloat16
         i32, f32, f64 = torch.int32, torch.float32, torch.float64
-        rv = r // 2 if v_bits == 4 else r
+        dv = D // 2 if v_bits == 4 else D
         self.quad_mu = torch.zeros(L, NB, n_kv, D, device=device, dtype=i8)
         self.mu_scale = torch.zeros(L, NB, n_kv, device=device, dtype=f16)
-        self.quad_V = torch.zeros(L, NB, n_kv, D, rv, device=device, dtype=i8)
+        self.quad_V = torch.zeros(L, NB, n_kv, r, dv, device=device, dtype=i8)
         self.V_scale = torch.zeros(L, NB, n_kv, r, device=device, dtype=f16)
         self.quad_sig2 = torch.zeros(L, NB, n_kv, r, device=device, dtype=f16)
         self.quad_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=device, dtype=bf16)
@@ -83,7 +120,7 @@ class QuadState:
                        + self.V_scale[0].numel() + self.quad_tag[0].numel()))
 
     def layer_state(self, layer: int):
-        """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer``."""
+        """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer`` (V column-major)."""
         return (self.quad_mu[layer], self.mu_scale[layer], self.quad_V[layer],
                 self.V_scale[layer], self.quad_sig2[layer], self.quad_tag[layer])
 
@@ -93,10 +130,10 @@ class QuadState:
         dev = self.quad_mu.device
         self.quad_mu[layer].copy_(torch.as_tensor(mu).to(dev))
         self.mu_scale[layer].copy_(torch.as_tensor(mu_scale).to(dev))
-        self.quad_V[layer].copy_(torch.as_tensor(V).to(dev))
+        self.quad_V[layer].copy_(v_to_device(torch.as_tensor(V).to(dev), self.v_bits))
         self.V_scale[layer].copy_(torch.as_tensor(V_scale).to(dev))
         self.quad_sig2[layer].copy_(torch.as_tensor(sig2).to(dev))
 
     def reference_V(self, layer: int) -> torch.Tensor:
         """quad_V of ``layer`` in the reference layout (NB, n_kv, d, r'[/2])."""
-        return self.quad_V[layer]
+        return v_to_reference(self.quad_V[layer], self.v_bits)

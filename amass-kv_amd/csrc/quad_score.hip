@@ -1,29 +1,44 @@
 // Quad (Gaussian-MGF quadratic) page score for gfx950.
 //
 // Math per (request r, kv-head h, page p < n_sel_hi[r]) and GQA head g
-// (reference: selection/quad_score.py:35-107, selection/quad_score_cuda.py:10-17):
+// (reference: selection/quad_score.py:7-24,35-107, selection/quad_score_cuda.py:10-17):
 //   qh_k = (V_code[:,k] * V_scale[k]) . q_g        k < r'
 //   quad = s^2 / (2P) * sum_k sig2_k * qh_k^2
 //   qmu  = s * (mu_code * mu_scale) . q_g
 //   S_g  = qmu + quad ; score = max_g S_g ("max") or S_g -> score_h ("nrm")
 //
-// Design.  A wave owns 8 "units" of 8 lanes; a unit is one (page, kv-head) summary
-// record and each lane holds 16 consecutive d rows of it, so a wave reads whole
-// (page, 8-head) slabs of the physical-block-keyed layout with 16-byte loads (one
-// contiguous 8 KB slab per page at r'=8 int8, n_kv=8).  q is quantised once per wave to
-// two int8 limbs (qi = rn(q/qs), qs = max|q|/16383, hi = rn(qi/128), lo = qi-128hi;
-// the reference recipe of selection/quad_score_cuda.py:902-935 with an IEEE divide) and
-// every d-contraction is an exact int32 sum from v_dot4_i32_i8: the V rows are stored
-// (d, r') so each lane byte-transposes its rows into d-contiguous words with v_perm_b32
-// (int4 codes are fed biased, nib^8 in [0,15], and the bias is removed exactly with
-// 8*sum(qi)).  The 8 lanes of a unit reduce with three DPP adds; the fp32 epilogue
-// runs on lane g of the unit.  Pure VALU + VMEM: the contraction per record is G x
-// (r'+1) dot products of length d, far below an MFMA tile.
-#include "score_common.h"
+// Design.  The d-contractions of a page are a small int8 matrix product,
+// [2G query limbs x d] x [d x (r'+1) columns], so they run on the matrix cores:
+// v_mfma_i32_16x16x64_i8 with M = the 2G limb rows of one kv-head's queries, N = 16
+// pages of a tile and K = 64 d per instruction.  q is quantised once per wave to two
+// int8 limbs (qi = rn(q*inv), inv = 16383/max|q|, hi = rn(qi/128), lo = qi - 128hi;
+// the recipe of selection/quad_score_cuda.py:902-935 with IEEE divides) and every
+// contraction is an exact int32 sum: comb = 128 * (hi . x) + (lo . x).
+//
+// Layout.  quad_V is stored column-major per (block, kv-head): (r', d) int8, so the 16
+// bytes a lane feeds to one MFMA (16 consecutive d of one column of one page) are one
+// dwordx4 load, and the two K-steps of a column read one whole 128-byte line.  int4 V is
+// (r', d/2) with byte j = code[j] | code[j + d/2] << 4: shifting the low nibble up and
+// masking gives 16 * code as a signed byte for d = j (K-step 0) and d = j + 64 (K-step
+// 1) with two ALU ops per word, and the result is divided by 16 exactly.  mu, mu_scale,
+// V_scale and sig2 keep the reference layout (selection/quad_state.py:36-151).
+//
+// Lanes.  lane = 16 kg + n: column n of the MFMA is page n of the tile, kg the 16-d
+// group of each K-step (d = 64 t + 16 kg + s for slot s).  A wave owns one (request,
+// kv-head) and strides over its 16-page tiles; each tile is two load groups (columns
+// [0, r'/2) + mu, then [r'/2, r') + scales), double-buffered so one group streams in
+// while the other is multiplied.  Result rows 4kg..4kg+3 of lane (kg, n) are limbs
+// (hi, lo) of g = 2kg and 2kg+1, so the fp32 epilogue runs on every lane with 2kg < G.
+// Workgroups are placed so that the n_kv heads of one (request, page range) run on one
+// XCD together: they share the 128-byte lines of V_scale / sig2 / mu_scale in its L2.
+#include "common.h"
 
 namespace amass {
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
 constexpr int QS_WAVES = 4;
+constexpr int QS_TILE = 16;     // pages per MFMA tile
 
 struct QuadParams {
     const uint16_t* q; int64_t q_st, q_hs;
@@ -38,217 +53,385 @@ struct QuadParams {
     float* score_h; int64_t sh_sr, sh_sh, sh_sg;
     int32_t* comb_out;
     float scale;
-    int n_req, n_kv, d, page, max_pages;
-    int hpt, ppt;  // heads per tile (min(n_kv,8)), pages per tile (8/hpt)
+    int n_req, n_kv, G, page, max_pages;
+    int zsplit;     // workgroups per (request, kv-head)
+    int units;      // n_req * zsplit
 };
 
-// One page tile's raw loads (double-buffered across the page loop).
-template <int NV4>
-struct QuadPage {
-    uint32_t raw[4 * NV4];
-    uint32_t mu[4];
-    uint32_t vs[4], sg[4];
+__device__ __forceinline__ i32x4_t ld16(const int8_t* p) {
+    return *reinterpret_cast<const i32x4_t*>(p);
+}
+
+__device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// V columns of one load group: int8 -> 2 loads (K-steps) per column, int4 -> 1.
+template <int VB>
+constexpr int loads_per_col() { return VB == 8 ? 2 : 1; }
+
+// fp16 scales of n consecutive columns (n = 1, 2, 4) as up to two dwords
+template <int N>
+__device__ __forceinline__ uint2 load_halves(const uint16_t* p) {
+    if constexpr (N == 4) return *reinterpret_cast<const uint2*>(p);
+    else if constexpr (N == 2) return uint2{*reinterpret_cast<const uint32_t*>(p), 0u};
+    else return uint2{(uint32_t)*p, 0u};
+}
+
+template <int RP, int VB>
+struct QuadGroupA {                       // columns [0, RP/2), mu and their scales
+    static constexpr int NC = RP / 2;
+    i32x4_t v[NC * loads_per_col<VB>()];
+    i32x4_t mu[2];
+    uint2 vs, sg;                         // fp16 V_scale / sig2 of columns [0, RP/2)
     uint32_t mus;
-    int page;
-    bool valid;
+};
+template <int RP, int VB>
+struct QuadGroupB {                       // columns [RP/2, RP) and their scales
+    static constexpr int NC = RP - RP / 2;
+    i32x4_t v[NC * loads_per_col<VB>()];
+    uint2 vs, sg;
 };
 
-template <int RP, int NV4>
-__device__ __forceinline__ void quad_load(const QuadParams& p, int req, int h, int nsh, int pg,
-                                          int poff, int64_t vh_off, int64_t mh_off,
-                                          QuadPage<NV4>& t) {
-    int page = pg * p.ppt + poff;
-    t.valid = page < nsh;
-    if (!t.valid) page = nsh - 1;
-    t.page = page;
-    const int64_t blk = p.bt[(int64_t)req * p.bt_st + page];
-    const uint4* vsrc = reinterpret_cast<const uint4*>(p.v + blk * p.v_sb + vh_off);
+// Byte offset of column c inside a (block, head) V record; lane offset 16 kg added by
+// the caller.
+template <int VB>
+constexpr int col_bytes() { return VB == 8 ? 128 : 64; }
+
+template <int RP, int VB>
+__device__ __forceinline__ void load_a(const QuadParams& p, const int8_t* vrec,
+                                       const int8_t* murec, int64_t blk, int h,
+                                       QuadGroupA<RP, VB>& a) {
 #pragma unroll
-    for (int i = 0; i < NV4; ++i) {
-        const uint4 u = vsrc[i];
-        t.raw[4 * i] = u.x; t.raw[4 * i + 1] = u.y; t.raw[4 * i + 2] = u.z; t.raw[4 * i + 3] = u.w;
+    for (int c = 0; c < QuadGroupA<RP, VB>::NC; ++c) {
+        if constexpr (VB == 8) {
+            a.v[2 * c] = ld16(vrec + c * 128);
+            a.v[2 * c + 1] = ld16(vrec + c * 128 + 64);
+        } else {
+            a.v[c] = ld16(vrec + c * 64);
+        }
     }
-    const uint4 m4 = *reinterpret_cast<const uint4*>(p.mu + blk * p.mu_sb + mh_off);
-    t.mu[0] = m4.x; t.mu[1] = m4.y; t.mu[2] = m4.z; t.mu[3] = m4.w;
-    const uint16_t* vsp = p.vs + blk * p.vs_sb + (int64_t)h * RP;
-    const uint16_t* sgp = p.sg + blk * p.sg_sb + (int64_t)h * RP;
-    if constexpr (RP == 8) {
-        const uint4 a = *reinterpret_cast<const uint4*>(vsp);
-        const uint4 b = *reinterpret_cast<const uint4*>(sgp);
-        t.vs[0] = a.x; t.vs[1] = a.y; t.vs[2] = a.z; t.vs[3] = a.w;
-        t.sg[0] = b.x; t.sg[1] = b.y; t.sg[2] = b.z; t.sg[3] = b.w;
-    } else if constexpr (RP == 4) {
-        const uint2 a = *reinterpret_cast<const uint2*>(vsp);
-        const uint2 b = *reinterpret_cast<const uint2*>(sgp);
-        t.vs[0] = a.x; t.vs[1] = a.y; t.sg[0] = b.x; t.sg[1] = b.y;
+    a.mu[0] = ld16(murec);
+    a.mu[1] = ld16(murec + 64);
+    a.vs = load_halves<RP / 2>(p.vs + blk * p.vs_sb + (int64_t)h * RP);
+    a.sg = load_halves<RP / 2>(p.sg + blk * p.sg_sb + (int64_t)h * RP);
+    a.mus = p.mus[blk * p.mus_sb + h];
+}
+
+template <int RP, int VB>
+__device__ __forceinline__ void load_b(const QuadParams& p, const int8_t* vrec, int64_t blk,
+                                       int h, QuadGroupB<RP, VB>& b) {
+    constexpr int C0 = RP / 2;
+#pragma unroll
+    for (int c = 0; c < QuadGroupB<RP, VB>::NC; ++c) {
+        if constexpr (VB == 8) {
+            b.v[2 * c] = ld16(vrec + (C0 + c) * 128);
+            b.v[2 * c + 1] = ld16(vrec + (C0 + c) * 128 + 64);
+        } else {
+            b.v[c] = ld16(vrec + (C0 + c) * 64);
+        }
+    }
+    b.vs = load_halves<RP - C0>(p.vs + blk * p.vs_sb + (int64_t)h * RP + C0);
+    b.sg = load_halves<RP - C0>(p.sg + blk * p.sg_sb + (int64_t)h * RP + C0);
+}
+
+// MFMA over one column: int8 -> two K-steps; int4 -> both K-steps from one word set.
+template <int VB>
+__device__ __forceinline__ i32x4_t col_mfma(const i32x4_t (&qa)[2], const i32x4_t* x) {
+    i32x4_t acc = {0, 0, 0, 0};
+    if constexpr (VB == 8) {
+        acc = mfma_i8(qa[0], x[0], acc);
+        acc = mfma_i8(qa[1], x[1], acc);
     } else {
-        t.vs[0] = *reinterpret_cast<const uint32_t*>(vsp);
-        t.sg[0] = *reinterpret_cast<const uint32_t*>(sgp);
+        const i32x4_t m = {(int)0xF0F0F0F0u, (int)0xF0F0F0F0u, (int)0xF0F0F0F0u,
+                           (int)0xF0F0F0F0u};
+        acc = mfma_i8(qa[0], (x[0] << 4) & m, acc);
+        acc = mfma_i8(qa[1], x[0] & m, acc);
     }
-    t.mus = p.mus[blk * p.mus_sb + h];
+    return acc;
 }
 
-__device__ __forceinline__ float half_at(const uint32_t* w, int i) {
-    return fp16_to_f32((uint16_t)((w[i >> 1] >> (16 * (i & 1))) & 0xFFFF));
+// Combined int32 d-contractions of g = 2kg (x) and 2kg+1 (y) from one MFMA result.
+template <int VB>
+__device__ __forceinline__ void comb2(i32x4_t acc, int& x, int& y) {
+    x = acc[0] * 128 + acc[1];
+    y = acc[2] * 128 + acc[3];
+    if constexpr (VB == 4) { x >>= 4; y >>= 4; }   // exact: both are multiples of 16
 }
 
-template <int RP, int VB, int G, bool NRM, int NV4>
-__device__ __forceinline__ void quad_compute(const QuadParams& p, const QuadPage<NV4>& t,
-                                             const uint32_t (&qh)[G][4],
-                                             const uint32_t (&ql)[G][4], float qsg, int qsumg,
-                                             int req, int h, int sub, int gown, float qcoef) {
-    uint32_t w[RP][4];
-    unpack_v<RP, VB>(t.raw, w);
-    int cs[RP + 1];
+__device__ __forceinline__ float half_of(uint2 w, int k) {
+    const uint32_t d = (k >> 1) ? w.y : w.x;
+    return fp16_to_f32((uint16_t)((d >> (16 * (k & 1))) & 0xFFFFu));
+}
+
+// Running fp32 epilogue of one tile for g = 2kg + e: the quad sum in column order and
+// the mu term (the same operations, in the same order, as one pass over all columns).
+struct QuadAcc {
+    float quad[2];
+    float qmu[2];
+};
+
+template <int NC, int VB>
+__device__ __forceinline__ void cols_epilogue(const i32x4_t (&qa)[2], const i32x4_t* v,
+                                              uint2 vs, uint2 sg, float qs0, float qs1,
+                                              QuadAcc& acc, int32_t* co, int co_g, bool co_on,
+                                              int col0) {
 #pragma unroll
-    for (int k = 0; k <= RP; ++k) {
-        const uint32_t* x = (k < RP) ? w[k < RP ? k : 0] : t.mu;
-        int v[G];
+    for (int c = 0; c < NC; ++c) {
+        int x[2];
+        comb2<VB>(col_mfma<VB>(qa, &v[c * loads_per_col<VB>()]), x[0], x[1]);
+        const float vsc = half_of(vs, c), sgc = half_of(sg, c);
 #pragma unroll
-        for (int g = 0; g < G; ++g) v[g] = dot16_2limb(qh[g], ql[g], x[0], x[1], x[2], x[3]);
-        cs[k] = unit8_reduce_col<G>(v, sub);
+        for (int e = 0; e < 2; ++e) {
+            const float qhk = (float)x[e] * (e ? qs1 : qs0) * vsc;
+            acc.quad[e] += sgc * qhk * qhk;
+        }
+        if (co_on) {
+            co[col0 + c] = x[0];
+            co[co_g + col0 + c] = x[1];
+        }
     }
-    if constexpr (VB == 4) {
+}
+
+// comb_out row of (request, head, page, g = 2kg); the row of g + 1 follows at +RP+1.
+template <int RP>
+__device__ __forceinline__ int32_t* comb_row(const QuadParams& p, int req, int h, int page,
+                                             int kg) {
+    return p.comb_out + (((int64_t)req * p.n_kv + h) * p.max_pages + page) * (p.G * (RP + 1)) +
+           (int64_t)(2 * kg) * (RP + 1);
+}
+
+template <int RP, int VB, bool COMB>
+__device__ __forceinline__ void tile_start(const QuadParams& p, const i32x4_t (&qa)[2],
+                                           const QuadGroupA<RP, VB>& a, float qs0, float qs1,
+                                           QuadAcc& acc, int req, int h, int page, bool valid,
+                                           int kg) {
+    constexpr int CA = RP / 2;
+    const bool co_on = COMB && valid && 2 * kg < p.G;
+    const bool co1 = 2 * kg + 1 < p.G;
+    int32_t* co = co_on ? comb_row<RP>(p, req, h, page, kg) : nullptr;
+    acc.quad[0] = acc.quad[1] = 0.f;
+    cols_epilogue<CA, VB>(qa, a.v, a.vs, a.sg, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on, 0);
+    i32x4_t m = {0, 0, 0, 0};
+    m = mfma_i8(qa[0], a.mu[0], m);
+    m = mfma_i8(qa[1], a.mu[1], m);
+    const int cmu[2] = {m[0] * 128 + m[1], m[2] * 128 + m[3]};
+    const float musf = fp16_to_f32((uint16_t)a.mus);
 #pragma unroll
-        for (int k = 0; k < RP; ++k) cs[k] -= 8 * qsumg;
+    for (int e = 0; e < 2; ++e) acc.qmu[e] = (float)cmu[e] * (e ? qs1 : qs0) * musf * p.scale;
+    if (co_on) {
+        co[RP] = cmu[0];
+        if (co1) co[2 * RP + 1] = cmu[1];
     }
-    float quad = 0.f;
+}
+
+template <int RP, int VB, bool NRM, bool COMB>
+__device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (&qa)[2],
+                                            const QuadGroupB<RP, VB>& b, QuadAcc& acc, int req,
+                                            int h, int page, bool valid, int kg, float qs0,
+                                            float qs1, float qcoef) {
+    constexpr int CA = RP / 2;
+    const bool co_on = COMB && valid && 2 * kg < p.G;
+    const bool co1 = 2 * kg + 1 < p.G;
+    int32_t* co = co_on ? comb_row<RP>(p, req, h, page, kg) : nullptr;
+    cols_epilogue<RP - CA, VB>(qa, b.v, b.vs, b.sg, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on,
+                               CA);
+    float S[2];
 #pragma unroll
-    for (int k = 0; k < RP; ++k) {
-        const float qhk = (float)cs[k] * qsg * half_at(t.vs, k);
-        quad += half_at(t.sg, k) * qhk * qhk;
-    }
-    const float musf = fp16_to_f32((uint16_t)t.mus);
-    const float qmu = (float)cs[RP] * qsg * musf * p.scale;
-    const float S = qmu + qcoef * quad;
-    // lanes sub and sub^1 (G=4), sub^{1,2} (G=2) ... hold the same g: one writes
-    constexpr int DUP = 8 / G;     // lanes per g inside the unit
-    const bool writer = (sub & (DUP - 1)) == 0;
+    for (int e = 0; e < 2; ++e) S[e] = acc.qmu[e] + qcoef * acc.quad[e];
+    const int g0 = 2 * kg, g1 = 2 * kg + 1;
     if constexpr (NRM) {
-        if (t.valid && writer)
-            p.score_h[(int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh + (int64_t)gown * p.sh_sg +
-                      t.page] = S;
+        // score_h row of g0 (g1 is the next row); the base is wave-uniform
+        const int64_t row = (int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh;
+        const int off = g0 * (int)p.sh_sg + page;
+        if (valid && g0 < p.G) p.score_h[row + off] = S[0];
+        if (valid && g1 < p.G) p.score_h[row + off + (int)p.sh_sg] = S[1];
     } else {
-        const float Sm = unit8_maxf(S);
-        if (t.valid && sub == 0)
-            p.score[(int64_t)req * p.sc_sr + (int64_t)h * p.sc_sh + t.page] = Sm;
-    }
-    if (p.comb_out != nullptr && t.valid && writer) {
-        int32_t* co = p.comb_out +
-                      (((int64_t)req * p.n_kv + h) * p.max_pages + t.page) * (G * (RP + 1)) +
-                      gown * (RP + 1);
-#pragma unroll
-        for (int k = 0; k <= RP; ++k) co[k] = cs[k];
+        float m = g0 < p.G ? (g1 < p.G ? fmaxf(S[0], S[1]) : S[0]) : -INFINITY;
+        if (p.G > 2) m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+        if (p.G > 4) m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+        if (valid && kg == 0)
+            p.score[(int64_t)req * p.sc_sr + (int64_t)h * p.sc_sh + page] = m;
     }
 }
 
-template <int RP, int VB, int G, bool NRM>
-__global__ __launch_bounds__(QS_WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(G >= 8 ? 2 : 3)))
+// COMB: also write the int32 contractions to comb_out (a test entry; the production
+// instance has no extra stores in its loop, which keeps the load wait counts exact).
+template <int RP, int VB, bool NRM, bool COMB>
+__global__ __launch_bounds__(QS_WAVES * WAVE)
 void quad_score_kernel(const QuadParams p) {
-    constexpr int RV = RP * VB / 8;     // bytes per d row
-    constexpr int NV4 = RV;             // 16-byte loads per lane (16 rows * RV / 16)
+    constexpr int VREC = RP * col_bytes<VB>();      // V bytes per (block, head)
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int req = blockIdx.z;
-    const int hb = blockIdx.y;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, kg = lane >> 4;
+    // XCD-aware placement: workgroup b runs on XCD b % 8; the n_kv heads of a unit u
+    // (request, page range) are consecutive workgroups of one XCD.
+    const int b = blockIdx.x;
+    const int local = b >> 3;
+    const int h = local % p.n_kv;
+    const int u = (local / p.n_kv) * 8 + (b & 7);
+    if (u >= p.units) return;
+    const int req = u / p.zsplit, z = u % p.zsplit;
     const int nsh = p.nsh[req];
-    const int j = lane >> 3, sub = lane & 7;
-    const int h = hb * p.hpt + (j % p.hpt);
-    const int poff = j / p.hpt;
-    const int npg = (nsh + p.ppt - 1) / p.ppt;
-    const int wstride = gridDim.x * QS_WAVES;
-    int pg = blockIdx.x * QS_WAVES + wave;
-    if (pg >= npg) return;
+    const int ntile = (nsh + QS_TILE - 1) / QS_TILE;
+    const int wstride = p.zsplit * QS_WAVES;
+    const int t0 = z * QS_WAVES + wave;
+    if (t0 >= ntile) return;
+    const int cnt = (ntile - t0 + wstride - 1) / wstride;
 
-    const int64_t vh_off = (int64_t)h * p.d * RV + (int64_t)sub * 16 * RV;
-    const int64_t mh_off = (int64_t)h * p.d + 16 * sub;
-    QuadPage<NV4> ta, tb;
-    quad_load<RP, NV4>(p, req, h, nsh, pg, poff, vh_off, mh_off, ta);
-
-    // ---- query limbs for this lane's kv-head group (once per wave) --------------------
-    uint32_t qh[G][4], ql[G][4];
-    float qsg = 0.f;
-    int qsumg = 0;
-    const int gown = unit_g<G>(sub);
+    // ---- query limbs: lane row m = n holds limb (n & 1) of g = n >> 1 -------------------
+    const int qg = n >> 1;
+    const bool qlive = qg < p.G;
+    uint32_t qw[2][8];          // bf16 pairs, d = 64 t + 16 kg + 2 i (+1)
+    {
+        const int gq = qlive ? qg : p.G - 1;       // unconditional loads, zeroed below
+        const uint16_t* qrow = p.q + (int64_t)req * p.q_st + (int64_t)(h * p.G + gq) * p.q_hs;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float qs;
-        int qsum;
-        quantize_q16(p.q + (int64_t)req * p.q_st + (int64_t)(h * G + g) * p.q_hs + 16 * sub,
-                     qh[g], ql[g], qs, qsum);
-        if (g == gown) { qsg = qs; qsumg = qsum; }
+        for (int t = 0; t < 2; ++t) {
+            const uint4 x0 = *reinterpret_cast<const uint4*>(qrow + 64 * t + 16 * kg);
+            const uint4 x1 = *reinterpret_cast<const uint4*>(qrow + 64 * t + 16 * kg + 8);
+            qw[t][0] = x0.x; qw[t][1] = x0.y; qw[t][2] = x0.z; qw[t][3] = x0.w;
+            qw[t][4] = x1.x; qw[t][5] = x1.y; qw[t][6] = x1.z; qw[t][7] = x1.w;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qw[t][i] = qlive ? qw[t][i] : 0u;
+        }
     }
+
+    // tile addressing: lane n owns page 16 tile + n; clamped pages load valid data and
+    // are never written
+    auto page_of = [&](int tile) { return tile * QS_TILE + n; };
+    auto block_of = [&](int page) -> int64_t {
+        const int pc = page < nsh ? page : nsh - 1;
+        return (int64_t)p.bt[(int64_t)req * p.bt_st + pc];
+    };
+    const int64_t vhead = (int64_t)h * VREC + 16 * kg;
+    const int64_t mhead = (int64_t)h * 128 + 16 * kg;
+
+    int tile = t0;
+    int64_t blk = block_of(page_of(tile));
+    QuadGroupA<RP, VB> ga;
+    QuadGroupB<RP, VB> gb;
+    load_a<RP, VB>(p, p.v + blk * p.v_sb + vhead, p.mu + blk * p.mu_sb + mhead, blk, h, ga);
+    const int tnext0 = cnt > 1 ? tile + wstride : tile;
+    int64_t blk_next = block_of(page_of(tnext0));
+    // issue order A, next block id, B -- the order the loop keeps, so the loop's wait
+    // counts hold on entry as well
+    __builtin_amdgcn_sched_barrier(0);
+    load_b<RP, VB>(p, p.v + blk * p.v_sb + vhead, blk, h, gb);
+
+    // |bf16| orders like its magnitude bits: take the max as integers
+    uint32_t amax = 0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            amax = max(amax, max(qw[t][i] & 0x7FFFu, (qw[t][i] >> 16) & 0x7FFFu));
+    float mx = __uint_as_float(amax << 16);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+    mx = fmaxf(mx, 1e-12f);
+    const float qs = mx / 16383.0f;            // correctly rounded divides
+    const float inv = 16383.0f / mx;
+    const int limb = n & 1;
+    i32x4_t qa[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * wi + j;
+                const uint32_t wv = qw[t][e >> 1];
+                const float fv = (e & 1) ? bf16hi(wv) : bf16lo(wv);
+                int qi = (int)rintf(__fmul_rn(fv, inv));
+                qi = max(-16383, min(16383, qi));
+                int hi = (int)rintf((float)qi * 0.0078125f);
+                hi = max(-127, min(127, hi));
+                const int v = limb ? qi - 128 * hi : hi;
+                word |= ((uint32_t)(v & 0xFF)) << (8 * j);
+            }
+            qa[t][wi] = (int)word;
+        }
+    }
+    const float qs0 = __shfl(qs, 4 * kg, WAVE);        // lane 4kg: row 4kg = g 2kg
+    const float qs1 = __shfl(qs, 4 * kg + 2, WAVE);
     const float qcoef = p.scale * p.scale / (2.0f * (float)p.page);
 
-    // ---- page loop, two register stages: steady-state loads are unconditional so the
-    // wait counts stay exact and page i+1 streams in while page i is reduced ------------
-    const int n = (npg - pg + wstride - 1) / wstride;
-    int i = 0;
-    for (; i + 2 < n; i += 2) {
-        quad_load<RP, NV4>(p, req, h, nsh, pg + (i + 1) * wstride, poff, vh_off, mh_off, tb);
-        quad_compute<RP, VB, G, NRM, NV4>(p, ta, qh, ql, qsg, qsumg, req, h, sub, gown, qcoef);
-        quad_load<RP, NV4>(p, req, h, nsh, pg + (i + 2) * wstride, poff, vh_off, mh_off, ta);
-        quad_compute<RP, VB, G, NRM, NV4>(p, tb, qh, ql, qsg, qsumg, req, h, sub, gown, qcoef);
+    // ---- tile loop: group A of tile i+1 streams in while group B of tile i is used,
+    // and group B of tile i+1 while group A of tile i+1 is used.  Every load in the
+    // steady state is unconditional so the wait counts stay exact. -----------------------
+    QuadAcc acc;
+    for (int i = 0; i + 1 < cnt; ++i) {
+        const int page = page_of(tile);
+        const bool valid = page < nsh;
+        tile_start<RP, VB, COMB>(p, qa, ga, qs0, qs1, acc, req, h, page, valid, kg);
+        // keep the refill of a buffer after its last use (bounds the live registers)
+        __builtin_amdgcn_sched_barrier(0);
+        const int64_t bn = blk_next;
+        load_a<RP, VB>(p, p.v + bn * p.v_sb + vhead, p.mu + bn * p.mu_sb + mhead, bn, h, ga);
+        const int tn2 = (i + 2 < cnt) ? tile + 2 * wstride : tile + wstride;
+        blk_next = block_of(page_of(tn2));
+        tile_finish<RP, VB, NRM, COMB>(p, qa, gb, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b<RP, VB>(p, p.v + bn * p.v_sb + vhead, bn, h, gb);
+        tile += wstride;
     }
-    if (i + 1 < n) {
-        quad_load<RP, NV4>(p, req, h, nsh, pg + (i + 1) * wstride, poff, vh_off, mh_off, tb);
-        quad_compute<RP, VB, G, NRM, NV4>(p, ta, qh, ql, qsg, qsumg, req, h, sub, gown, qcoef);
-        quad_compute<RP, VB, G, NRM, NV4>(p, tb, qh, ql, qsg, qsumg, req, h, sub, gown, qcoef);
-    } else {
-        quad_compute<RP, VB, G, NRM, NV4>(p, ta, qh, ql, qsg, qsumg, req, h, sub, gown, qcoef);
-    }
+    const int page = page_of(tile);
+    const bool valid = page < nsh;
+    tile_start<RP, VB, COMB>(p, qa, ga, qs0, qs1, acc, req, h, page, valid, kg);
+    tile_finish<RP, VB, NRM, COMB>(p, qa, gb, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
 }
 
-// One resident round: as many workgroups as the kernel's occupancy lets every CU hold
-// at once (queried once per kernel instance), split over (request, head block); each wave
-// then strides over its request's page tiles.
+// Workgroups per CU the kernel can keep resident (queried once per instance).
 template <typename K>
-static int resident_wgs(K kernel, int threads) {
-    static int cached = 0;
+static int resident_per_cu(K kernel, int threads, int& cus) {
+    static int cached = 0, cached_cus = 0;
     if (cached == 0) {
-        int dev = 0, cus = 0, per_cu = 0;
+        int dev = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-            per_cu < 1)
-            return 1024;
-        cached = per_cu * cus;
+            hipDeviceGetAttribute(&cached_cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) !=
+                hipSuccess ||
+            per_cu < 1) {
+            cus = 256;
+            return 2;
+        }
+        cached = per_cu;
     }
+    cus = cached_cus;
     return cached;
 }
 
-static int quad_zsplit(int resident, int n_req, int hb, int tiles) {
-    const int per = n_req * hb;
-    int z = (resident + per - 1) / per;
-    const int zmax = (tiles + QS_WAVES * 2 - 1) / (QS_WAVES * 2);  // >= 2 tiles per wave
+// One resident round of workgroups over (request, kv-head) pairs, at most enough that
+// every wave gets a tile.
+static int quad_zsplit(int resident, int pairs, int tiles) {
+    int z = (resident + pairs - 1) / pairs;
+    const int zmax = (tiles + QS_WAVES - 1) / QS_WAVES;
     z = z < zmax ? z : zmax;
     return z < 1 ? 1 : z;
 }
 
-template <int RP, int VB, int G, bool NRM>
-static int launch_quad_k(const QuadParams& p, dim3 grid, int tiles, hipStream_t s) {
-    auto k = quad_score_kernel<RP, VB, G, NRM>;
-    grid.x = quad_zsplit(resident_wgs(k, QS_WAVES * WAVE), p.n_req, grid.y, tiles);
-    hipLaunchKernelGGL(k, grid, dim3(QS_WAVES * WAVE), 0, s, p);
+template <int RP, int VB, bool NRM, bool COMB>
+static int launch_quad_k(QuadParams p, int tiles, hipStream_t s) {
+    auto k = quad_score_kernel<RP, VB, NRM, COMB>;
+    int cus = 0;
+    const int per_cu = resident_per_cu(k, QS_WAVES * WAVE, cus);
+    p.zsplit = quad_zsplit(per_cu * cus, p.n_req * p.n_kv, tiles);
+    p.units = p.n_req * p.zsplit;
+    const int upad = (p.units + 7) / 8 * 8;
+    hipLaunchKernelGGL(k, dim3(upad * p.n_kv), dim3(QS_WAVES * WAVE), 0, s, p);
     return check_launch();
 }
 
-template <int RP, int VB, int G>
-static int launch_quad_g(const QuadParams& p, bool nrm, dim3 grid, int tiles, hipStream_t s) {
-    return nrm ? launch_quad_k<RP, VB, G, true>(p, grid, tiles, s)
-               : launch_quad_k<RP, VB, G, false>(p, grid, tiles, s);
-}
-
 template <int RP, int VB>
-static int launch_quad_rv(const QuadParams& p, int G, bool nrm, dim3 grid, int tiles,
-                          hipStream_t s) {
-    switch (G) {
-        case 1: return launch_quad_g<RP, VB, 1>(p, nrm, grid, tiles, s);
-        case 2: return launch_quad_g<RP, VB, 2>(p, nrm, grid, tiles, s);
-        case 4: return launch_quad_g<RP, VB, 4>(p, nrm, grid, tiles, s);
-        case 8: return launch_quad_g<RP, VB, 8>(p, nrm, grid, tiles, s);
-        default: return AMASS_ERR_GEOMETRY;
-    }
+static int launch_quad_rv(const QuadParams& p, bool nrm, int tiles, hipStream_t s) {
+    if (p.comb_out != nullptr)
+        return nrm ? launch_quad_k<RP, VB, true, true>(p, tiles, s)
+                   : launch_quad_k<RP, VB, false, true>(p, tiles, s);
+    return nrm ? launch_quad_k<RP, VB, true, false>(p, tiles, s)
+               : launch_quad_k<RP, VB, false, false>(p, tiles, s);
 }
 
 }  // namespace amass
@@ -263,8 +446,8 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     if (a->combine == 0 && !a->score) return AMASS_ERR_NULL;
     if (a->combine == 1 && !a->score_h) return AMASS_ERR_NULL;
     if (a->combine != 0 && a->combine != 1) return AMASS_ERR_GEOMETRY;
-    if (a->d != 128 || a->n_req < 0 || a->max_pages < 1) return AMASS_ERR_GEOMETRY;
-    if (!(a->n_kv >= 1 && (8 % a->n_kv == 0 || a->n_kv % 8 == 0))) return AMASS_ERR_GEOMETRY;
+    if (a->d != 128 || a->n_req < 0 || a->max_pages < 1 || a->n_kv < 1) return AMASS_ERR_GEOMETRY;
+    if (a->G < 1 || a->G > 8) return AMASS_ERR_GEOMETRY;
     if (a->v_bits != 8 && a->v_bits != 4) return AMASS_ERR_GEOMETRY;
     if (a->rank != 2 && a->rank != 4 && a->rank != 8) return AMASS_ERR_UNSUPPORTED;
     if (a->n_req == 0) return AMASS_OK;
@@ -281,26 +464,23 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     p.score_h = a->score_h; p.sh_sr = a->sh_sr; p.sh_sh = a->sh_sh; p.sh_sg = a->sh_sg;
     p.comb_out = a->comb_out;
     p.scale = a->scale;
-    p.n_req = a->n_req; p.n_kv = a->n_kv; p.d = a->d; p.page = a->page;
+    p.n_req = a->n_req; p.n_kv = a->n_kv; p.G = a->G; p.page = a->page;
     p.max_pages = a->max_pages;
-    p.hpt = a->n_kv < 8 ? a->n_kv : 8;
-    p.ppt = 8 / p.hpt;
-    const int hb = a->n_kv / p.hpt;
-    const int tiles = (a->max_pages + p.ppt - 1) / p.ppt;
-    dim3 grid(1, hb, a->n_req);
+    p.zsplit = 1; p.units = a->n_req;
+    const int tiles = (a->max_pages + QS_TILE - 1) / QS_TILE;
     hipStream_t s = (hipStream_t)stream;
     const bool nrm = a->combine == 1;
     if (a->v_bits == 8) {
         switch (a->rank) {
-            case 2: return launch_quad_rv<2, 8>(p, a->G, nrm, grid, tiles, s);
-            case 4: return launch_quad_rv<4, 8>(p, a->G, nrm, grid, tiles, s);
-            case 8: return launch_quad_rv<8, 8>(p, a->G, nrm, grid, tiles, s);
+            case 2: return launch_quad_rv<2, 8>(p, nrm, tiles, s);
+            case 4: return launch_quad_rv<4, 8>(p, nrm, tiles, s);
+            case 8: return launch_quad_rv<8, 8>(p, nrm, tiles, s);
         }
     } else {
         switch (a->rank) {
-            case 2: return launch_quad_rv<2, 4>(p, a->G, nrm, grid, tiles, s);
-            case 4: return launch_quad_rv<4, 4>(p, a->G, nrm, grid, tiles, s);
-            case 8: return launch_quad_rv<8, 4>(p, a->G, nrm, grid, tiles, s);
+            case 2: return launch_quad_rv<2, 4>(p, nrm, tiles, s);
+            case 4: return launch_quad_rv<4, 4>(p, nrm, tiles, s);
+            case 8: return launch_quad_rv<8, 4>(p, nrm, tiles, s);
         }
     }
     return AMASS_ERR_UNSUPPORTED;

@@ -109,7 +109,8 @@ def cpu_baseline(case, st, budget_s=15.0):
 
     f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
     i = lambda t: t.detach().cpu().numpy()          # noqa: E731
-    mu, mus, V, Vs, sg, _ = st.layer_state(0)
+    mu, mus, _, Vs, sg, _ = st.layer_state(0)
+    V = st.reference_V(0)
     host = dict(q=f(case.q), mu=i(mu), mus=f(mus), V=i(V), Vs=f(Vs), sg=f(sg),
                 bt=i(case.block_table), sl=i(case.seq_lens), K=f(case.kv_cache[:, 0]),
                 Vc=f(case.kv_cache[:, 1]), npg=i(st.n_pages), nsh=i(st.n_sel_hi),

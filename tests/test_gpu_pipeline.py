@@ -34,7 +34,8 @@ def _step(st, case, out, path="auto"):
 def _check(case, st, out, *, mode, cov, kind):
     B, MP, G = case.q.shape[0], st.max_pages, case.G
     nsh = npi(st.n_sel_hi)
-    mu, mus, V, Vs, sg, _ = st.layer_state(0)
+    mu, mus, _, Vs, sg, _ = st.layer_state(0)
+    V = st.reference_V(0)
     ref_h = osc.quad_score(npf(case.q), npi(mu), npf(mus), npi(V), npf(Vs), npf(sg),
                            npi(case.block_table), nsh, scale=case.scale, page=16, G=G,
                            v_bits=st.v_bits, max_pages=MP, combine="nrm")

@@ -31,7 +31,8 @@ def _quad_setup(rank, v_bits, G, combine, seed=0, B=3):
 
 
 def _oracle_inputs(case, st):
-    mu, mus, V, Vs, sg, _ = st.layer_state(0)
+    mu, mus, _, Vs, sg, _ = st.layer_state(0)
+    V = st.reference_V(0)
     return dict(q=npf(case.q), mu=npi(mu), mu_scale=npf(mus), V=npi(V), V_scale=npf(Vs),
                 sig2=npf(sg), block_table=npi(case.block_table), n_sel_hi=npi(st.n_sel_hi))
 
