@@ -36,8 +36,7 @@ def _fields(spec: str):
 
 class QuadScoreArgs(C.Structure):
     _fields_ = _fields(
-        "q:p q_st:i64 q_hs:i64 mu:p mu_sb:i64 mu_scale:p mus_sb:i64 v:p v_sb:i64 "
-        "v_scale:p vs_sb:i64 sig2:p sg_sb:i64 block_table:p bt_st:i64 n_sel_hi:p "
+        "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 n_sel_hi:p "
         "score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 comb_out:p "
         "scale:f32 n_req:i32 n_kv:i32 G:i32 d:i32 page:i32 rank:i32 v_bits:i32 "
         "max_pages:i32 combine:i32")

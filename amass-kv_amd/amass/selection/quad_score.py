@@ -16,24 +16,21 @@ from .select import derive_page_params, select_pages
 
 
 def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadScoreArgs:
-    mu, mu_s, V, V_s, sig2, _ = st.layer_state(layer)
-    require_cuda(q, block_table, mu)
+    rec = st.quad_rec[layer]
+    require_cuda(q, block_table, rec)
     if q.dtype != torch.bfloat16 or q.stride(2) != 1:
         raise ValueError("q must be bf16 (T, H, d) with unit stride on d")
     if block_table.dtype != torch.int32 or block_table.stride(1) != 1:
         raise ValueError("block_table must be int32 with unit column stride")
     if block_table.shape[1] < st.max_pages - st.window_pages:
         raise ValueError("block_table narrower than the scored page range")
-    if V.stride(3) != 1 or V.stride(2) != V.shape[3] or V.stride(1) != V.shape[2] * V.shape[3] \
-            or mu.stride(2) != 1 or mu.stride(1) != mu.shape[2]:
-        raise ValueError("quad_V / quad_mu must be contiguous inside each block")
+    if rec.stride(2) != 1 or rec.stride(1) != rec.shape[2]:
+        raise ValueError("quad_rec must hold each block's n_kv records contiguously")
     nrm = st.combine == "nrm"
     sh = st.score_h
     return QuadScoreArgs(
         q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),
-        mu=ptr(mu), mu_sb=mu.stride(0), mu_scale=ptr(mu_s), mus_sb=mu_s.stride(0),
-        v=ptr(V), v_sb=V.stride(0), v_scale=ptr(V_s), vs_sb=V_s.stride(0),
-        sig2=ptr(sig2), sg_sb=sig2.stride(0),
+        rec=ptr(rec), rec_sb=rec.stride(0),
         block_table=ptr(block_table), bt_st=block_table.stride(0),
         n_sel_hi=ptr(st.n_sel_hi),
         score=ptr(st.score), sc_sr=st.score.stride(0), sc_sh=st.score.stride(1),

@@ -1,19 +1,25 @@
 """QuadState -- persistent buffers of the quad (Gaussian-MGF quadratic) selector.
 
-The tensors, dtypes and shapes of the reference (``selection/quad_state.py:36-151``),
-except that quad_V is stored column-major per (block, kv-head):
+The reference (``selection/quad_state.py:36-151``) keeps five slabs per layer; this
+build packs them into one contiguous record per (block, kv-head) and exposes the
+reference's names as views into it:
 
-  quad_mu    (L, NB, n_kv, d)       int8   + mu_scale  (L, NB, n_kv)      fp16
-  quad_V     (L, NB, n_kv, r', d)   int8   + V_scale   (L, NB, n_kv, r')  fp16 (per column)
-             int4: (L, NB, n_kv, r', d/2), byte j = code[j] | code[j + d/2] << 4
-             (the reference keeps (.., d, r') with two columns per int4 byte)
-  quad_sig2  (L, NB, n_kv, r')      fp16   eigenvalues of the page's centred key scatter
-  quad_tag   (L, NB, n_kv, TAGW)    bf16   NaN-init content tag
+  quad_rec   (L, NB, n_kv, REC)     int8   REC = r' * CB + 192 bytes:
+    quad_V     (L, NB, n_kv, r', CB)  int8  column-major: column k holds CB bytes;
+               int8 CB = d (byte j = code[j]); int4 CB = d/2, byte j = code[j] | code[j+d/2] << 4
+               (the reference keeps (.., d, r') with two columns per int4 byte)
+    quad_mu    (L, NB, n_kv, d)       int8  page-mean codes
+    V_scale    (L, NB, n_kv, r')      fp16  per column            (fp16 half 0 of the meta)
+    quad_sig2  (L, NB, n_kv, r')      fp16  eigenvalues of the page's centred key scatter
+                                            (half 8)
+    mu_scale   (L, NB, n_kv)          fp16  (half 16; halves r'..7, r'+8..15, 17..31 zero)
+  quad_tag   (L, NB, n_kv, TAGW)    bf16   NaN-init content tag (separate)
 
-Column-major V lets the gfx950 score kernel feed each 16-byte load straight into an
-int8 matrix-core instruction (16 consecutive d of one column of one page), and makes
-the two K-halves of a column one 128-byte line.  ``v_to_device`` / ``v_to_reference``
-convert between the two layouts; ``load_reference`` and ``reference_V`` use them.
+One record means one base address per (page, kv-head) and one DRAM neighbourhood: the
+gfx950 score kernel feeds each 16-byte load of a V column straight into an int8
+matrix-core instruction, and reads the scales with one more 16-byte load per lane
+instead of five scattered small ones.  ``v_to_device`` / ``v_to_reference`` convert V
+between the two layouts; ``load_reference`` and ``reference_V`` use them.
 
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
 (R, n_kv, G, MP) and hmax (R, n_kv, G).
@@ -92,12 +98,18 @@ class QuadState:
         self.device = device
         i8, f16, bf16 = torch.int8, torch.float16, torch.bfloat16
         i32, f32, f64 = torch.int32, torch.float32, torch.float64
-        dv = D // 2 if v_bits == 4 else D
-        self.quad_mu = torch.zeros(L, NB, n_kv, D, device=device, dtype=i8)
-        self.mu_scale = torch.zeros(L, NB, n_kv, device=device, dtype=f16)
-        self.quad_V = torch.zeros(L, NB, n_kv, r, dv, device=device, dtype=i8)
-        self.V_scale = torch.zeros(L, NB, n_kv, r, device=device, dtype=f16)
-        self.quad_sig2 = torch.zeros(L, NB, n_kv, r, device=device, dtype=f16)
+        if r > 8 or D != 128:
+            raise ValueError("the packed quad record holds r' <= 8 columns of d = 128")
+        cb = D // 2 if v_bits == 4 else D
+        vb = r * cb
+        self.rec_bytes = vb + D + 64
+        self.quad_rec = torch.zeros(L, NB, n_kv, self.rec_bytes, device=device, dtype=i8)
+        meta = self.quad_rec[..., vb + D:].view(f16)                   # (L, NB, n_kv, 32)
+        self.quad_V = self.quad_rec[..., :vb].unflatten(-1, (r, cb))
+        self.quad_mu = self.quad_rec[..., vb:vb + D]
+        self.V_scale = meta[..., 0:r]
+        self.quad_sig2 = meta[..., 8:8 + r]
+        self.mu_scale = meta[..., 16]
         self.quad_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=device, dtype=bf16)
         self.quad_c = self.c_scale = self.quad_resid = None
         self.score = torch.empty(R, n_kv, MP, device=device, dtype=f32)
@@ -115,9 +127,7 @@ class QuadState:
         self.budget64 = torch.tensor([self.budget], device=device, dtype=f64)
 
     def bytes_per_layer(self) -> int:
-        return (self.quad_mu[0].numel() + self.quad_V[0].numel()
-                + 2 * (self.quad_sig2[0].numel() + self.mu_scale[0].numel()
-                       + self.V_scale[0].numel() + self.quad_tag[0].numel()))
+        return self.quad_rec[0].numel() + 2 * self.quad_tag[0].numel()
 
     def layer_state(self, layer: int):
         """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer`` (V column-major)."""

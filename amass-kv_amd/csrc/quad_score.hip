@@ -15,22 +15,24 @@
 // the recipe of selection/quad_score_cuda.py:902-935 with IEEE divides) and every
 // contraction is an exact int32 sum: comb = 128 * (hi . x) + (lo . x).
 //
-// Layout.  quad_V is stored column-major per (block, kv-head): (r', d) int8, so the 16
-// bytes a lane feeds to one MFMA (16 consecutive d of one column of one page) are one
-// dwordx4 load, and the two K-steps of a column read one whole 128-byte line.  int4 V is
-// (r', d/2) with byte j = code[j] | code[j + d/2] << 4: shifting the low nibble up and
-// masking gives 16 * code as a signed byte for d = j (K-step 0) and d = j + 64 (K-step
-// 1) with two ALU ops per word, and the result is divided by 16 exactly.  mu, mu_scale,
-// V_scale and sig2 keep the reference layout (selection/quad_state.py:36-151).
+// Layout.  One record per (block, kv-head) (AMASS_QUAD_REC_BYTES): quad_V column-major
+// (r' columns of CB bytes), then the 128 mu codes, then 64 bytes of fp16 scales
+// (V_scale at half 0, sig2 at half 8, mu_scale at half 16).  The 16 bytes a lane feeds
+// to one MFMA (16 consecutive d of one column of one page) are one dwordx4 load, the two
+// K-steps of a column read one whole 128-byte line, and the page's scales are one more
+// 16-byte load per lane spread over the tile's four lane groups and exchanged with
+// ds_bpermute.  int4 V (CB = 64) has byte j = code[j] | code[j + 64] << 4: shifting the
+// low nibble up and masking gives 16 * code as a signed byte for d = j (K-step 0) and
+// d = j + 64 (K-step 1) with two ALU ops per word; the sums are divided by 16 exactly.
 //
 // Lanes.  lane = 16 kg + n: column n of the MFMA is page n of the tile, kg the 16-d
 // group of each K-step (d = 64 t + 16 kg + s for slot s).  A wave owns one (request,
 // kv-head) and strides over its 16-page tiles; each tile is two load groups (columns
-// [0, r'/2) + mu, then [r'/2, r') + scales), double-buffered so one group streams in
+// [0, r'/2) + mu + scales, then [r'/2, r')), double-buffered so one group streams in
 // while the other is multiplied.  Result rows 4kg..4kg+3 of lane (kg, n) are limbs
 // (hi, lo) of g = 2kg and 2kg+1, so the fp32 epilogue runs on every lane with 2kg < G.
 // Workgroups are placed so that the n_kv heads of one (request, page range) run on one
-// XCD together: they share the 128-byte lines of V_scale / sig2 / mu_scale in its L2.
+// XCD together, reading neighbouring records of the same blocks through one L2.
 #include "common.h"
 
 namespace amass {
@@ -42,11 +44,7 @@ constexpr int QS_TILE = 16;     // pages per MFMA tile
 
 struct QuadParams {
     const uint16_t* q; int64_t q_st, q_hs;
-    const int8_t* mu; int64_t mu_sb;
-    const uint16_t* mus; int64_t mus_sb;
-    const int8_t* v; int64_t v_sb;
-    const uint16_t* vs; int64_t vs_sb;
-    const uint16_t* sg; int64_t sg_sb;
+    const int8_t* rec; int64_t rec_sb;
     const int32_t* bt; int64_t bt_st;
     const int32_t* nsh;
     float* score; int64_t sc_sr, sc_sh;
@@ -66,73 +64,79 @@ __device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// V columns of one load group: int8 -> 2 loads (K-steps) per column, int4 -> 1.
-template <int VB>
-constexpr int loads_per_col() { return VB == 8 ? 2 : 1; }
-
-// fp16 scales of n consecutive columns (n = 1, 2, 4) as up to two dwords
-template <int N>
-__device__ __forceinline__ uint2 load_halves(const uint16_t* p) {
-    if constexpr (N == 4) return *reinterpret_cast<const uint2*>(p);
-    else if constexpr (N == 2) return uint2{*reinterpret_cast<const uint32_t*>(p), 0u};
-    else return uint2{(uint32_t)*p, 0u};
-}
+// bytes per V column / loads per column (int8: two K-steps; int4: one word set)
+template <int VB> constexpr int col_bytes() { return VB == 8 ? 128 : 64; }
+template <int VB> constexpr int loads_per_col() { return VB == 8 ? 2 : 1; }
+template <int RP, int VB> constexpr int rec_bytes() { return RP * col_bytes<VB>() + 192; }
 
 template <int RP, int VB>
-struct QuadGroupA {                       // columns [0, RP/2), mu and their scales
+struct QuadGroupA {                       // columns [0, RP/2), mu, the page's scales
     static constexpr int NC = RP / 2;
     i32x4_t v[NC * loads_per_col<VB>()];
     i32x4_t mu[2];
-    uint2 vs, sg;                         // fp16 V_scale / sig2 of columns [0, RP/2)
-    uint32_t mus;
+    i32x4_t meta;                         // 16 bytes kg of the 64-byte scale block
 };
 template <int RP, int VB>
-struct QuadGroupB {                       // columns [RP/2, RP) and their scales
+struct QuadGroupB {                       // columns [RP/2, RP)
     static constexpr int NC = RP - RP / 2;
     i32x4_t v[NC * loads_per_col<VB>()];
-    uint2 vs, sg;
 };
 
-// Byte offset of column c inside a (block, head) V record; lane offset 16 kg added by
-// the caller.
-template <int VB>
-constexpr int col_bytes() { return VB == 8 ? 128 : 64; }
+// fp16 scales of one page, gathered to every lane of the page
+struct PageScales {
+    uint32_t vs[4], sg[4];                // halves k of V_scale / sig2
+    uint32_t mus;                         // mu_scale in the low half
+};
 
+// `lr` = the lane's record (block record + head * REC + 16 kg)
 template <int RP, int VB>
-__device__ __forceinline__ void load_a(const QuadParams& p, const int8_t* vrec,
-                                       const int8_t* murec, int64_t blk, int h,
-                                       QuadGroupA<RP, VB>& a) {
+__device__ __forceinline__ void load_a(const int8_t* lr, QuadGroupA<RP, VB>& a) {
+    constexpr int CB = col_bytes<VB>();
 #pragma unroll
     for (int c = 0; c < QuadGroupA<RP, VB>::NC; ++c) {
         if constexpr (VB == 8) {
-            a.v[2 * c] = ld16(vrec + c * 128);
-            a.v[2 * c + 1] = ld16(vrec + c * 128 + 64);
+            a.v[2 * c] = ld16(lr + c * CB);
+            a.v[2 * c + 1] = ld16(lr + c * CB + 64);
         } else {
-            a.v[c] = ld16(vrec + c * 64);
+            a.v[c] = ld16(lr + c * CB);
         }
     }
-    a.mu[0] = ld16(murec);
-    a.mu[1] = ld16(murec + 64);
-    a.vs = load_halves<RP / 2>(p.vs + blk * p.vs_sb + (int64_t)h * RP);
-    a.sg = load_halves<RP / 2>(p.sg + blk * p.sg_sb + (int64_t)h * RP);
-    a.mus = p.mus[blk * p.mus_sb + h];
+    a.mu[0] = ld16(lr + RP * CB);
+    a.mu[1] = ld16(lr + RP * CB + 64);
+    a.meta = ld16(lr + RP * CB + 128);
 }
 
 template <int RP, int VB>
-__device__ __forceinline__ void load_b(const QuadParams& p, const int8_t* vrec, int64_t blk,
-                                       int h, QuadGroupB<RP, VB>& b) {
+__device__ __forceinline__ void load_b(const int8_t* lr, QuadGroupB<RP, VB>& b) {
+    constexpr int CB = col_bytes<VB>();
     constexpr int C0 = RP / 2;
 #pragma unroll
     for (int c = 0; c < QuadGroupB<RP, VB>::NC; ++c) {
         if constexpr (VB == 8) {
-            b.v[2 * c] = ld16(vrec + (C0 + c) * 128);
-            b.v[2 * c + 1] = ld16(vrec + (C0 + c) * 128 + 64);
+            b.v[2 * c] = ld16(lr + (C0 + c) * CB);
+            b.v[2 * c + 1] = ld16(lr + (C0 + c) * CB + 64);
         } else {
-            b.v[c] = ld16(vrec + (C0 + c) * 64);
+            b.v[c] = ld16(lr + (C0 + c) * CB);
         }
     }
-    b.vs = load_halves<RP - C0>(p.vs + blk * p.vs_sb + (int64_t)h * RP + C0);
-    b.sg = load_halves<RP - C0>(p.sg + blk * p.sg_sb + (int64_t)h * RP + C0);
+}
+
+// lane n (kg 0) holds V_scale, lane n + 16 (kg 1) sig2, lane n + 32 (kg 2) mu_scale
+template <int RP>
+__device__ __forceinline__ PageScales gather_scales(i32x4_t meta, int n) {
+    PageScales s;
+    constexpr int NW = (RP + 1) / 2;      // dwords holding r' halves
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s.vs[i] = i < NW ? (uint32_t)__shfl(meta[i], n, WAVE) : 0u;
+        s.sg[i] = i < NW ? (uint32_t)__shfl(meta[i], n + 16, WAVE) : 0u;
+    }
+    s.mus = (uint32_t)__shfl(meta[0], n + 32, WAVE);
+    return s;
+}
+
+__device__ __forceinline__ float half_at(const uint32_t (&w)[4], int k) {
+    return fp16_to_f32((uint16_t)((w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu));
 }
 
 // MFMA over one column: int8 -> two K-steps; int4 -> both K-steps from one word set.
@@ -159,11 +163,6 @@ __device__ __forceinline__ void comb2(i32x4_t acc, int& x, int& y) {
     if constexpr (VB == 4) { x >>= 4; y >>= 4; }   // exact: both are multiples of 16
 }
 
-__device__ __forceinline__ float half_of(uint2 w, int k) {
-    const uint32_t d = (k >> 1) ? w.y : w.x;
-    return fp16_to_f32((uint16_t)((d >> (16 * (k & 1))) & 0xFFFFu));
-}
-
 // Running fp32 epilogue of one tile for g = 2kg + e: the quad sum in column order and
 // the mu term (the same operations, in the same order, as one pass over all columns).
 struct QuadAcc {
@@ -173,14 +172,14 @@ struct QuadAcc {
 
 template <int NC, int VB>
 __device__ __forceinline__ void cols_epilogue(const i32x4_t (&qa)[2], const i32x4_t* v,
-                                              uint2 vs, uint2 sg, float qs0, float qs1,
-                                              QuadAcc& acc, int32_t* co, int co_g, bool co_on,
-                                              int col0) {
+                                              const PageScales& sc, int col0, float qs0,
+                                              float qs1, QuadAcc& acc, int32_t* co, int co_g,
+                                              bool co_on) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         int x[2];
         comb2<VB>(col_mfma<VB>(qa, &v[c * loads_per_col<VB>()]), x[0], x[1]);
-        const float vsc = half_of(vs, c), sgc = half_of(sg, c);
+        const float vsc = half_at(sc.vs, col0 + c), sgc = half_at(sc.sg, col0 + c);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const float qhk = (float)x[e] * (e ? qs1 : qs0) * vsc;
@@ -203,20 +202,20 @@ __device__ __forceinline__ int32_t* comb_row(const QuadParams& p, int req, int h
 
 template <int RP, int VB, bool COMB>
 __device__ __forceinline__ void tile_start(const QuadParams& p, const i32x4_t (&qa)[2],
-                                           const QuadGroupA<RP, VB>& a, float qs0, float qs1,
-                                           QuadAcc& acc, int req, int h, int page, bool valid,
-                                           int kg) {
+                                           const QuadGroupA<RP, VB>& a, const PageScales& sc,
+                                           float qs0, float qs1, QuadAcc& acc, int req, int h,
+                                           int page, bool valid, int kg) {
     constexpr int CA = RP / 2;
     const bool co_on = COMB && valid && 2 * kg < p.G;
     const bool co1 = 2 * kg + 1 < p.G;
     int32_t* co = co_on ? comb_row<RP>(p, req, h, page, kg) : nullptr;
     acc.quad[0] = acc.quad[1] = 0.f;
-    cols_epilogue<CA, VB>(qa, a.v, a.vs, a.sg, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on, 0);
+    cols_epilogue<CA, VB>(qa, a.v, sc, 0, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on);
     i32x4_t m = {0, 0, 0, 0};
     m = mfma_i8(qa[0], a.mu[0], m);
     m = mfma_i8(qa[1], a.mu[1], m);
     const int cmu[2] = {m[0] * 128 + m[1], m[2] * 128 + m[3]};
-    const float musf = fp16_to_f32((uint16_t)a.mus);
+    const float musf = fp16_to_f32((uint16_t)(sc.mus & 0xFFFFu));
 #pragma unroll
     for (int e = 0; e < 2; ++e) acc.qmu[e] = (float)cmu[e] * (e ? qs1 : qs0) * musf * p.scale;
     if (co_on) {
@@ -227,25 +226,31 @@ __device__ __forceinline__ void tile_start(const QuadParams& p, const i32x4_t (&
 
 template <int RP, int VB, bool NRM, bool COMB>
 __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (&qa)[2],
-                                            const QuadGroupB<RP, VB>& b, QuadAcc& acc, int req,
-                                            int h, int page, bool valid, int kg, float qs0,
-                                            float qs1, float qcoef) {
+                                            const QuadGroupB<RP, VB>& b, const PageScales& sc,
+                                            QuadAcc& acc, int req, int h, int page, bool valid,
+                                            int kg, float qs0, float qs1, float qcoef) {
     constexpr int CA = RP / 2;
     const bool co_on = COMB && valid && 2 * kg < p.G;
     const bool co1 = 2 * kg + 1 < p.G;
     int32_t* co = co_on ? comb_row<RP>(p, req, h, page, kg) : nullptr;
-    cols_epilogue<RP - CA, VB>(qa, b.v, b.vs, b.sg, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on,
-                               CA);
+    cols_epilogue<RP - CA, VB>(qa, b.v, sc, CA, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on);
     float S[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) S[e] = acc.qmu[e] + qcoef * acc.quad[e];
     const int g0 = 2 * kg, g1 = 2 * kg + 1;
     if constexpr (NRM) {
-        // score_h row of g0 (g1 is the next row); the base is wave-uniform
         const int64_t row = (int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh;
-        const int off = g0 * (int)p.sh_sg + page;
-        if (valid && g0 < p.G) p.score_h[row + off] = S[0];
-        if (valid && g1 < p.G) p.score_h[row + off + (int)p.sh_sg] = S[1];
+        if (p.G <= 4) {
+            // lanes kg 2,3 take g 1,3 from lanes kg 0,1: one store per lane
+            const float odd = __shfl_xor(S[1], 32, WAVE);
+            const int g = kg < 2 ? 2 * kg : 2 * kg - 3;
+            const float v = kg < 2 ? S[0] : odd;
+            if (valid && g < p.G) p.score_h[row + g * (int)p.sh_sg + page] = v;
+        } else {
+            const int off = g0 * (int)p.sh_sg + page;
+            if (valid && g0 < p.G) p.score_h[row + off] = S[0];
+            if (valid && g1 < p.G) p.score_h[row + off + (int)p.sh_sg] = S[1];
+        }
     } else {
         float m = g0 < p.G ? (g1 < p.G ? fmaxf(S[0], S[1]) : S[0]) : -INFINITY;
         if (p.G > 2) m = fmaxf(m, __shfl_xor(m, 16, WAVE));
@@ -260,7 +265,7 @@ __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (
 template <int RP, int VB, bool NRM, bool COMB>
 __global__ __launch_bounds__(QS_WAVES * WAVE)
 void quad_score_kernel(const QuadParams p) {
-    constexpr int VREC = RP * col_bytes<VB>();      // V bytes per (block, head)
+    constexpr int REC = rec_bytes<RP, VB>();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kg = lane >> 4;
@@ -300,24 +305,26 @@ void quad_score_kernel(const QuadParams p) {
     // tile addressing: lane n owns page 16 tile + n; clamped pages load valid data and
     // are never written
     auto page_of = [&](int tile) { return tile * QS_TILE + n; };
-    auto block_of = [&](int page) -> int64_t {
+    auto lane_blk = [&](int tile) -> int64_t {
+        const int page = page_of(tile);
         const int pc = page < nsh ? page : nsh - 1;
         return (int64_t)p.bt[(int64_t)req * p.bt_st + pc];
     };
-    const int64_t vhead = (int64_t)h * VREC + 16 * kg;
-    const int64_t mhead = (int64_t)h * 128 + 16 * kg;
+    // the loop carries block ids, not record pointers: carried pointers made the
+    // compiler double the load buffers and copy them at the loop head
+    const int64_t rhead = (int64_t)h * REC + 16 * kg;
+    auto lane_rec = [&](int64_t blk) { return p.rec + blk * p.rec_sb + rhead; };
 
     int tile = t0;
-    int64_t blk = block_of(page_of(tile));
+    const int8_t* lr = lane_rec(lane_blk(tile));
     QuadGroupA<RP, VB> ga;
     QuadGroupB<RP, VB> gb;
-    load_a<RP, VB>(p, p.v + blk * p.v_sb + vhead, p.mu + blk * p.mu_sb + mhead, blk, h, ga);
-    const int tnext0 = cnt > 1 ? tile + wstride : tile;
-    int64_t blk_next = block_of(page_of(tnext0));
+    load_a<RP, VB>(lr, ga);
+    int64_t bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
     // issue order A, next block id, B -- the order the loop keeps, so the loop's wait
     // counts hold on entry as well
     __builtin_amdgcn_sched_barrier(0);
-    load_b<RP, VB>(p, p.v + blk * p.v_sb + vhead, blk, h, gb);
+    load_b<RP, VB>(lr, gb);
 
     // |bf16| orders like its magnitude bits: take the max as integers
     uint32_t amax = 0;
@@ -365,22 +372,24 @@ void quad_score_kernel(const QuadParams p) {
     for (int i = 0; i + 1 < cnt; ++i) {
         const int page = page_of(tile);
         const bool valid = page < nsh;
-        tile_start<RP, VB, COMB>(p, qa, ga, qs0, qs1, acc, req, h, page, valid, kg);
+        const PageScales sc = gather_scales<RP>(ga.meta, n);
+        tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, kg);
         // keep the refill of a buffer after its last use (bounds the live registers)
         __builtin_amdgcn_sched_barrier(0);
-        const int64_t bn = blk_next;
-        load_a<RP, VB>(p, p.v + bn * p.v_sb + vhead, p.mu + bn * p.mu_sb + mhead, bn, h, ga);
-        const int tn2 = (i + 2 < cnt) ? tile + 2 * wstride : tile + wstride;
-        blk_next = block_of(page_of(tn2));
-        tile_finish<RP, VB, NRM, COMB>(p, qa, gb, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
+        const int8_t* ln = lane_rec(bn_next);
+        load_a<RP, VB>(ln, ga);
+        bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
+        tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1,
+                                       qcoef);
         __builtin_amdgcn_sched_barrier(0);
-        load_b<RP, VB>(p, p.v + bn * p.v_sb + vhead, bn, h, gb);
+        load_b<RP, VB>(ln, gb);
         tile += wstride;
     }
     const int page = page_of(tile);
     const bool valid = page < nsh;
-    tile_start<RP, VB, COMB>(p, qa, ga, qs0, qs1, acc, req, h, page, valid, kg);
-    tile_finish<RP, VB, NRM, COMB>(p, qa, gb, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
+    const PageScales sc = gather_scales<RP>(ga.meta, n);
+    tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, kg);
+    tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
 }
 
 // Workgroups per CU the kernel can keep resident (queried once per instance).
@@ -440,9 +449,7 @@ using namespace amass;
 
 extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     if (!a) return AMASS_ERR_NULL;
-    if (!a->q || !a->mu || !a->mu_scale || !a->v || !a->v_scale || !a->sig2 ||
-        !a->block_table || !a->n_sel_hi)
-        return AMASS_ERR_NULL;
+    if (!a->q || !a->rec || !a->block_table || !a->n_sel_hi) return AMASS_ERR_NULL;
     if (a->combine == 0 && !a->score) return AMASS_ERR_NULL;
     if (a->combine == 1 && !a->score_h) return AMASS_ERR_NULL;
     if (a->combine != 0 && a->combine != 1) return AMASS_ERR_GEOMETRY;
@@ -450,14 +457,14 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     if (a->G < 1 || a->G > 8) return AMASS_ERR_GEOMETRY;
     if (a->v_bits != 8 && a->v_bits != 4) return AMASS_ERR_GEOMETRY;
     if (a->rank != 2 && a->rank != 4 && a->rank != 8) return AMASS_ERR_UNSUPPORTED;
+    // 16-byte loads: the records (and so the block stride) must be 16-byte aligned
+    if ((((uintptr_t)a->rec) & 15) != 0 || (a->rec_sb & 15) != 0) return AMASS_ERR_GEOMETRY;
+    if (a->rec_sb < (int64_t)a->n_kv * AMASS_QUAD_REC_BYTES(a->rank, a->v_bits))
+        return AMASS_ERR_GEOMETRY;
     if (a->n_req == 0) return AMASS_OK;
     QuadParams p;
     p.q = (const uint16_t*)a->q; p.q_st = a->q_st; p.q_hs = a->q_hs;
-    p.mu = a->mu; p.mu_sb = a->mu_sb;
-    p.mus = (const uint16_t*)a->mu_scale; p.mus_sb = a->mus_sb;
-    p.v = a->v; p.v_sb = a->v_sb;
-    p.vs = (const uint16_t*)a->v_scale; p.vs_sb = a->vs_sb;
-    p.sg = (const uint16_t*)a->sig2; p.sg_sb = a->sg_sb;
+    p.rec = a->rec; p.rec_sb = a->rec_sb;
     p.bt = a->block_table; p.bt_st = a->bt_st;
     p.nsh = a->n_sel_hi;
     p.score = a->score; p.sc_sr = a->sc_sr; p.sc_sh = a->sc_sh;

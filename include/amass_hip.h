@@ -43,14 +43,21 @@ extern "C" {
  *   qmu  = s * (mu_code * mu_scale) . q_g  ;  S_g = qmu + quad
  * combine 0 ("max"): score[r,kh,p] = max_g S_g ; combine 1 ("nrm"): score_h[r,kh,g,p]=S_g.
  * q is quantised per q-head to two int8 limbs (qi = rn(q/qs), qs = max|q|/16383,
- * hi = rn(qi/128), lo = qi - 128 hi) and the d-contractions are exact int32 sums. */
+ * hi = rn(qi/128), lo = qi - 128 hi) and the d-contractions are exact int32 sums.
+ *
+ * Summary record.  The reference's five per-(block, kv-head) slabs (quad_mu, mu_scale,
+ * quad_V, V_scale, quad_sig2) are packed into one contiguous record per (block, kv-head)
+ * of AMASS_QUAD_REC_BYTES(rank, v_bits) bytes, n_kv records per block:
+ *   [0, r'*CB)          quad_V column-major: column k = CB bytes; int8 CB = d = 128
+ *                       (byte j = code[j]); int4 CB = 64 (byte j = code[j] | code[j+64] << 4)
+ *   [r'*CB, +128)       quad_mu int8 codes (d)
+ *   [r'*CB+128, +64)    fp16: V_scale[0..r') at half 0, sig2[0..r') at half 8,
+ *                       mu_scale at half 16, the rest zero
+ * rec points at block 0 of the layer, rec_sb is the block stride in bytes. */
+#define AMASS_QUAD_REC_BYTES(rank, v_bits) ((rank) * ((v_bits) == 8 ? 128 : 64) + 192)
 typedef struct amass_quad_score_args {
     const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
-    const int8_t*  mu;       int64_t mu_sb;          /* (NB,n_kv,d) int8, block stride  */
-    const void*    mu_scale; int64_t mus_sb;         /* (NB,n_kv) fp16                  */
-    const int8_t*  v;        int64_t v_sb;           /* (NB,n_kv,d,r') int8 | (..,r'/2) int4 */
-    const void*    v_scale;  int64_t vs_sb;          /* (NB,n_kv,r') fp16               */
-    const void*    sig2;     int64_t sg_sb;          /* (NB,n_kv,r') fp16               */
+    const int8_t*  rec;      int64_t rec_sb;         /* (NB,n_kv,REC) summary records   */
     const int32_t* block_table; int64_t bt_st;       /* (R,max_blocks) int32            */
     const int32_t* n_sel_hi;                         /* (R,) int32                      */
     float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32 (combine 0)    */
