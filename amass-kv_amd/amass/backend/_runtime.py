@@ -1,0 +1,101 @@
+"""Backend runtime: the one AmassConfig, the Stage-A / Stage-B dispatch, layer lookup.
+
+The reference keeps these singletons and adapters in ``backend/_runtime.py:1-303``:
+register() stores the config, the metadata builder owns the per-layer state, and the
+attention impl calls the select / decode functions with the layer-index-free signature
+``(q, kv_cache, block_table, seq_lens, st, n_req, scale, cfg)``.  On this build there is
+one implementation of every kernel (libamass_hip.so); nothing here falls back to
+another kernel family -- an unsupported configuration is refused up front and the
+impl then leaves the step to the stock vLLM attention, as the reference does for every
+path it does not handle (``backend/attn.py:45-59``).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+from ..config import AmassConfig
+
+_config: Optional[AmassConfig] = None
+
+PAGE = 16          # page size the kernels are built for (reference: cfg page = 16)
+HEAD_DIM = 128     # head dim the kernels are built for
+
+
+def set_config(cfg: Optional[AmassConfig]) -> None:
+    global _config
+    _config = cfg
+
+
+def get_config() -> Optional[AmassConfig]:
+    return _config
+
+
+def unsupported_reason(cfg: Optional[AmassConfig], *, head_size: int, block_size: int,
+                       G: int) -> Optional[str]:
+    """Why this build's decode path does not serve a layer (None = it does)."""
+    if cfg is None:
+        return "no AmassConfig registered"
+    if cfg.variant != "fast":
+        return (f"variant {cfg.variant!r}: the tier's write path (staging / flush) is not "
+                "part of this build, so mem variants keep the stock attention")
+    if cfg.score == "clse":
+        return "score='clse' is not built on this backend (use score='quad' or 'r8')"
+    if head_size != HEAD_DIM or block_size != PAGE:
+        return f"head_size {head_size} / block_size {block_size} (built for 128 / 16)"
+    if not 1 <= G <= 8:
+        return f"GQA group {G} (built for 1..8)"
+    return None
+
+
+def make_state(cfg: AmassConfig, device, *, num_layers: int, num_blocks: int, n_kv: int,
+               G: int, max_reqs: int, max_pages: int):
+    """The persistent Stage-A state for ``cfg.score`` (reference builder.py:161-205)."""
+    from ..attention.decode import ensure_stage_b_buffers
+    from ..selection import QuadState, R8State
+    budget = cfg.budget if cfg.budget is not None else 0.1
+    common = dict(num_layers=num_layers, num_blocks=num_blocks, n_kv=n_kv, G=G,
+                  head_dim=HEAD_DIM, page=PAGE, max_reqs=max_reqs, max_pages=max_pages,
+                  budget=budget, sink_pages=cfg.sink_pages, window_pages=cfg.window_pages)
+    if cfg.score == "quad":
+        st = QuadState(device, rank=cfg.quad_rank, v_bits=cfg.quad_v_bits,
+                       combine=cfg.quad_combine, **common)
+    else:
+        st = R8State(device, rank=cfg.r8_rank, **common)
+    # budget None -> the per-(request, kv-head) coverage nucleus; else fixed top-b
+    st.coverage = cfg.coverage if cfg.budget is None else None
+    st.scale = None
+    ensure_stage_b_buffers(st, device)
+    return st
+
+
+def layer_index(st, kv_cache) -> int:
+    """Physical layer of ``kv_cache`` (the builder keys its data_ptr at allocation)."""
+    layer_of = getattr(st, "_layer_of", None)
+    if layer_of is None:
+        raise RuntimeError("amass: state has no layer map (the builder did not bind it)")
+    lidx = layer_of.get(kv_cache.data_ptr())
+    if lidx is None:
+        raise RuntimeError(f"amass: kv_cache {kv_cache.data_ptr():#x} is not a layer the "
+                           "builder bound")
+    return lidx
+
+
+def select(q, kv_cache, block_table, seq_lens, st, n_req: int, scale: float,
+           cfg: AmassConfig) -> None:
+    """Stage A for one layer: score + (nrm) + top-b / coverage -> st.page_table,
+    st.page_cnt.  ``derive=False``: the builder derived this step's page params."""
+    from ..selection import QuadState, select_pages_quad, select_pages_r8
+    lidx = layer_index(st, kv_cache)
+    if isinstance(st, QuadState):
+        select_pages_quad(st, lidx, q, block_table, seq_lens, n_req, scale, derive=False)
+    else:
+        select_pages_r8(st, lidx, q, block_table, seq_lens, n_req, scale, derive=False)
+
+
+def decode_dispatch(q, kv_cache, block_table, seq_lens, st, out, vsource, scale: float,
+                    cfg: AmassConfig) -> None:
+    """Stage B: sparse paged decode over st.page_table (split-K or fused, chosen by the
+    library from the batch shape)."""
+    from ..attention.decode import sparse_paged_decode_batched
+    sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out, vsource,
+                                scale=scale)

@@ -72,6 +72,25 @@ def time_graph(g, steps, warmup, reps=1, batches=7):
     return statistics.median(out)
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config1.txt")
+
+
+def profiled_traffic():
+    """HBM bytes per launch measured by rocprofv3 (FETCH_SIZE / WRITE_SIZE, calibrated
+    against a kernel of known size) for the config-1 kernels: the `traffic <kernel>
+    <bytes>` lines of profiles/hbm_traffic_config1.txt, or {} when it is absent."""
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic":
+                    out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
+
+
 def quad_score_bytes(st, n_req, G):
     """Algorithmic HBM bytes of one quad-score launch: per scored (page, kv-head) record
     d*r'*vb/8 (V) + d (mu) + 2r' (V_scale) + 2r' (sig2) + 2 (mu_scale), plus the block
@@ -231,11 +250,18 @@ def main():
         "sparse_decode": dict(us=round(us_att, 2), bytes=b_att,
                               gbs=round(b_att / us_att / 1e3, 1)),
     }
+    traffic = profiled_traffic()
+    for k, v in kernels.items():
+        v["traffic"] = traffic.get(k)
     dom = max(kernels, key=lambda k: kernels[k]["us"])
     dk = kernels[dom]
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(dk["bytes"] / dk["us"] / 1e3, 1),
             "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(dk["bytes"] / (dk["us"] * 1e-6) / PEAK_HBM, 4), "traffic": None}
+            "frac": round(dk["bytes"] / (dk["us"] * 1e-6) / PEAK_HBM, 4),
+            "traffic": traffic.get(dom),
+            "traffic_source": "profiles/hbm_traffic_config1.txt: rocprofv3 FETCH_SIZE x2.000 "
+                              "+ WRITE_SIZE x1.000 (scales from a 256 MiB neg kernel)"
+            if dom in traffic else None}
     total_bytes = b_score + b_sel + b_att
     res = {
         "metric": "sparse decode attn us/layer + HBM GB/s at B=32 ctx16k; speedup vs dense paged",

@@ -1,0 +1,187 @@
+"""vLLM-ROCm plugin boundary on a vLLM stand-in (CPU): registration and backend
+wrapping (reference backend/register.py:26-86), the impl's pure-decode gate
+(backend/attn.py:31-82), graph-support declaration (backend/builder.py:81-88) and the
+builder's lazy state, summary refresh gate and derive gating (builder.py:252-459).
+Kernel calls are replaced by recorders; the GPU path is covered by test_gpu_backend."""
+import types
+
+import pytest
+import torch
+
+import fake_vllm
+from amass import AmassConfig
+from amass.backend import _runtime, attn, builder, register
+
+
+@pytest.fixture
+def vllm(monkeypatch):
+    saved = fake_vllm.install()
+    orig = fake_vllm.RocmPlatform.__dict__["get_attn_backend_cls"]
+    monkeypatch.setattr(register, "_APPLIED", False)
+    monkeypatch.setattr(register, "_WRAPPED", {})
+    monkeypatch.delenv("AMASS_DISABLE", raising=False)
+    monkeypatch.delenv("AMASS_CONFIG", raising=False)
+    yield fake_vllm
+    fake_vllm.RocmPlatform.get_attn_backend_cls = orig
+    _runtime.set_config(None)
+    fake_vllm.uninstall(saved)
+
+
+FAST = dict(variant="fast", score="quad", quad_rank=8, quad_v_bits=8, budget=None,
+            coverage=0.95)
+
+
+def _backend(vllm, **cfg):
+    register.register(dict(FAST, **cfg))
+    path = vllm.RocmPlatform.get_attn_backend_cls(None, 128, torch.bfloat16, "auto", 16)
+    return path, register._resolve(path)
+
+
+def test_register_wraps_the_platform_backend(vllm):
+    path, be = _backend(vllm)
+    assert path == "amass.backend.register.Amass_TritonAttentionBackend"
+    assert issubclass(be, vllm.TritonAttentionBackend) and be.get_name() == "TRITON_ATTN"
+    impl, bld = be.get_impl_cls(), be.get_builder_cls()
+    assert issubclass(impl, attn.AmassAttentionImplMixin)
+    assert issubclass(impl, vllm.TritonAttentionImpl)
+    assert issubclass(bld, builder.AmassMetadataBuilderMixin)
+    assert issubclass(bld, vllm.TritonAttentionMetadataBuilder)
+    # the same class comes back on every selection; MLA is left alone
+    assert vllm.RocmPlatform.get_attn_backend_cls(None, 128, None, "auto", 16) == path
+    assert vllm.RocmPlatform.get_attn_backend_cls(None, 128, None, "auto", 16,
+                                                  use_mla=True) == vllm.MLA_PATH
+    assert _runtime.get_config() == AmassConfig(**FAST)
+
+
+def test_disable_env_makes_register_inert(vllm, monkeypatch):
+    monkeypatch.setenv("AMASS_DISABLE", "1")
+    register.register(FAST)
+    assert vllm.RocmPlatform.get_attn_backend_cls(None, 128, None, "auto", 16) == \
+        vllm.TRITON_PATH
+    assert _runtime.get_config() is None
+
+
+@pytest.mark.parametrize("cfg,want", [
+    ({}, "UNIFORM_SINGLE_TOKEN_DECODE"),
+    ({"force_eager": True}, "NEVER"),
+    ({"variant": "mem-v"}, "NEVER"),
+    ({"score": "clse"}, "NEVER"),
+    ({"score": "r8"}, "UNIFORM_SINGLE_TOKEN_DECODE"),
+])
+def test_cudagraph_support(vllm, cfg, want):
+    _, be = _backend(vllm, **cfg)
+    vc = vllm.vllm_config(num_gpu_blocks=0, layers={})
+    got = be.get_builder_cls().get_cudagraph_support(vc, vllm.kv_spec())
+    assert got.name == want
+
+
+def test_unserved_geometry_keeps_stock(vllm):
+    _, be = _backend(vllm)
+    vc = vllm.vllm_config(num_gpu_blocks=0, layers={})
+    assert be.get_builder_cls().get_cudagraph_support(
+        vc, vllm.kv_spec(head_size=64)).name == "NEVER"
+
+
+def _impl(be, n_q=32, n_kv=8):
+    return be.get_impl_cls()(n_q, 128, 0.088, n_kv)
+
+
+def test_impl_delegates_everything_but_pure_decode(vllm, monkeypatch):
+    _, be = _backend(vllm)
+    calls = []
+    monkeypatch.setattr(_runtime, "select", lambda *a: calls.append(("select", a)))
+    monkeypatch.setattr(_runtime, "decode_dispatch", lambda *a: calls.append(("decode", a)))
+    monkeypatch.setattr(attn, "ResidentVSource", lambda kv: ("vsrc", kv))
+    impl = _impl(be)
+    kv = torch.zeros(4, 2, 16, 8, 128)
+    q = torch.zeros(3, 32, 128)
+    out = torch.zeros(3, 32 * 128)
+    st = types.SimpleNamespace()
+    sl, bt = torch.tensor([5, 9, 17]), torch.zeros(3, 4, dtype=torch.int32)
+    decode = vllm.Metadata(seq_lens=sl, block_table=bt, max_query_len=1, causal=True,
+                           amass=st)
+    for md in (vllm.Metadata(**dict(vars(decode), max_query_len=7)),      # prefill
+               vllm.Metadata(**dict(vars(decode), amass=None)),           # no state
+               vllm.Metadata(**dict(vars(decode), causal=False)),
+               vllm.Metadata(**dict(vars(decode), use_cascade=True))):
+        assert impl.forward(None, q, None, None, kv, md, output=out) is out
+    assert impl.calls == ["stock"] * 4 and not calls
+    impl.sliding_window = (128, 0)
+    impl.forward(None, q, None, None, kv, decode, output=out)
+    impl.sliding_window = (-1, -1)
+    impl.kv_cache_dtype = "fp8"
+    impl.forward(None, q, None, None, kv, decode, output=out)
+    impl.kv_cache_dtype = "auto"
+    assert impl.calls == ["stock"] * 6 and not calls
+    assert impl.forward(None, q, None, None, kv, decode, output=out) is out
+    assert [c[0] for c in calls] == ["select", "decode"]
+    sel, dec = calls[0][1], calls[1][1]
+    assert sel[0] is q and sel[1] is kv and sel[4] is st and sel[5] == 3 and sel[6] == 0.088
+    assert dec[5].shape == (3, 32, 128) and dec[6] == ("vsrc", kv)
+    assert impl.calls == ["stock"] * 6
+
+
+def _cam(sl, bt, max_q=1):
+    return types.SimpleNamespace(seq_lens=sl, block_table_tensor=bt, max_query_len=max_q,
+                                 seq_lens_cpu_upper_bound=sl.clone())
+
+
+def test_builder_lazy_state_refresh_gate_and_derive(vllm, monkeypatch):
+    _, be = _backend(vllm)
+    rec = []
+    import amass.selection as sel
+    monkeypatch.setattr(sel, "derive_page_params", lambda st, sl, n: rec.append("derive"))
+    monkeypatch.setattr(sel, "quad_build_bulk", lambda *a: rec.append(("bulk", a[4], a[5])))
+    monkeypatch.setattr(sel, "quad_build_delta", lambda *a: rec.append(("delta", a[4], a[5])))
+    monkeypatch.setattr(sel, "quad_build_tail",
+                        lambda *a: rec.append(("tail", a[5].tolist())))
+    kv = {f"l{i}": torch.zeros(40, 2, 16, 8, 128, dtype=torch.bfloat16) for i in range(2)}
+    vc = vllm.vllm_config(num_gpu_blocks=0, layers=kv, max_num_seqs=4, max_model_len=512)
+    b = be.get_builder_cls()(vllm.kv_spec(), list(kv), vc, "cpu")
+    bt = torch.arange(8, dtype=torch.int32).view(2, 4)
+    md = b.build(0, _cam(torch.tensor([33, 40]), bt))
+    assert not hasattr(md, "amass") and not rec                 # cache not allocated yet
+    vc.cache_config.num_gpu_blocks = 40
+    md = b.build(0, _cam(torch.tensor([33, 40]), bt))
+    st = md.amass
+    assert type(st).__name__ == "QuadState" and st.L == 2 and st.NB == 40
+    assert st.coverage == 0.95 and st.r == 8 and st.max_pages == 32 and st.max_reqs == 4
+    assert st._layer_of == {kv["l0"].data_ptr(): 0, kv["l1"].data_ptr(): 1}
+    assert rec == [("bulk", 2, 2), "derive"]
+    rec.clear()
+    b.build(0, _cam(torch.tensor([34, 41]), bt))               # steady, no boundary
+    assert rec == []
+    b.build(0, _cam(torch.tensor([35, 42]), bt))
+    assert rec == []
+    want = []
+    for _ in range(29):                                           # reach 64 / 71
+        cur = b._amass_prev + 1
+        crossed = [i for i in range(2) if int(cur[i]) % 16 == 0]
+        want += [("tail", crossed)] if crossed else []
+        want += ["derive"] if any(int(c) % 16 == 1 for c in cur) else []
+        b.build(0, _cam(cur, bt))
+    assert rec == want and ("tail", [0]) in rec and ("tail", [1]) in rec
+    rec.clear()
+    b.build(0, _cam(torch.tensor([65, 72]), bt))                 # 65 % 16 == 1 -> derive
+    assert rec == ["derive"]
+    rec.clear()
+    b.build(0, _cam(torch.tensor([100, 3]), bt))                 # composition change
+    assert rec == [("delta", 2, 6), "derive"]
+    rec.clear()
+    md = b.build(0, _cam(torch.tensor([100, 3]), bt, max_q=5))   # prefill: no state
+    assert not hasattr(md, "amass") and rec == []
+
+
+def test_builder_skips_refresh_during_capture(vllm, monkeypatch):
+    _, be = _backend(vllm, score="r8", budget=0.05)
+    rec = []
+    import amass.selection as sel
+    monkeypatch.setattr(sel, "derive_page_params", lambda st, sl, n: rec.append("derive"))
+    monkeypatch.setattr(sel, "r8_build_bulk", lambda *a: rec.append("bulk"))
+    kv = {"l0": torch.zeros(20, 2, 16, 8, 128, dtype=torch.bfloat16)}
+    vc = vllm.vllm_config(num_gpu_blocks=20, layers=kv, max_model_len=256)
+    b = be.get_builder_cls()(vllm.kv_spec(), list(kv), vc, "cpu")
+    md = b.build_for_cudagraph_capture(_cam(torch.tensor([1, 1]),
+                                            torch.zeros(2, 16, dtype=torch.int32)))
+    assert type(md.amass).__name__ == "R8State" and md.amass.coverage is None
+    assert rec == ["derive"]
