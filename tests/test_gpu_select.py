@@ -2,7 +2,8 @@
 
 Bar: given the same scores, page_table, page_cnt and the chosen count are bit-exact for
 both tie rules (lower page index; the reference's keep-all-ties threshold), both nucleus
-mass kinds, forced ties, padded rows, short sequences, b >= S, and up to 8192 pages.
+mass kinds, forced ties (+0.0 / -0.0 included), padded rows, short sequences, b >= S, and
+up to 16384 pages (the largest page count the selection accepts).
 """
 import numpy as np
 import pytest
@@ -111,6 +112,16 @@ def test_long_context_8192_pages():
     st = _state(R, MP, G=8, budget=0.02)
     _run(st, R, 0, 0, 0, 1.0, gen, False, MP)
     _run(st, R, 1, 0, 1, 0.95, gen, False, MP)
+
+
+def test_max_pages_16384():
+    """The largest page count the selection accepts (scores staged in LDS)."""
+    announce("topb + coverage at MP=16384")
+    gen = torch.Generator().manual_seed(10)
+    R, MP = 2, 16384
+    st = _state(R, MP, G=4, budget=0.02)
+    _run(st, R, 0, 0, 0, 1.0, gen, False, MP)
+    _run(st, R, 1, 0, 1, 0.95, gen, True, MP)
 
 
 def test_nrm_fused_into_select():
