@@ -24,8 +24,8 @@ def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadSc
         raise ValueError("block_table must be int32 with unit column stride")
     if block_table.shape[1] < st.max_pages - st.window_pages:
         raise ValueError("block_table narrower than the scored page range")
-    if rec.stride(2) != 1 or rec.stride(1) != rec.shape[2]:
-        raise ValueError("quad_rec must hold each block's n_kv records contiguously")
+    if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
+        raise ValueError("quad_rec must hold each block's records contiguously")
     nrm = st.combine == "nrm"
     sh = st.score_h
     return QuadScoreArgs(

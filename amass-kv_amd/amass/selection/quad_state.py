@@ -1,25 +1,27 @@
 """QuadState -- persistent buffers of the quad (Gaussian-MGF quadratic) selector.
 
 The reference (``selection/quad_state.py:36-151``) keeps five slabs per layer; this
-build packs them into one contiguous record per (block, kv-head) and exposes the
-reference's names as views into it:
+build packs them into one block-keyed buffer and exposes the reference's names as views
+into it.  Per (layer, block), REC = r' * CB + 192 bytes per kv head:
 
-  quad_rec   (L, NB, n_kv, REC)     int8   REC = r' * CB + 192 bytes:
-    quad_V     (L, NB, n_kv, r', CB)  int8  column-major: column k holds CB bytes;
+  quad_rec   (L, NB, n_kv * REC)  int8, per block:
+    n_kv records of VM = r' * CB + 128 bytes, head h at h * VM:
+      quad_V   (L, NB, n_kv, r', CB) int8  column-major: column k holds CB bytes;
                int8 CB = d (byte j = code[j]); int4 CB = d/2, byte j = code[j] | code[j+d/2] << 4
                (the reference keeps (.., d, r') with two columns per int4 byte)
-    quad_mu    (L, NB, n_kv, d)       int8  page-mean codes
-    V_scale    (L, NB, n_kv, r')      fp16  per column            (fp16 half 0 of the meta)
-    quad_sig2  (L, NB, n_kv, r')      fp16  eigenvalues of the page's centred key scatter
-                                            (half 8)
-    mu_scale   (L, NB, n_kv)          fp16  (half 16; halves r'..7, r'+8..15, 17..31 zero)
-  quad_tag   (L, NB, n_kv, TAGW)    bf16   NaN-init content tag (separate)
+      quad_mu  (L, NB, n_kv, d)      int8  page-mean codes
+    then n_kv scale blocks of 64 bytes (fp16 halves), head h at n_kv * VM + 64 h:
+      V_scale  (L, NB, n_kv, r')     half 0..r'-1
+      quad_sig2(L, NB, n_kv, r')     half 8..8+r'-1 (eigenvalues of the centred key scatter)
+      mu_scale (L, NB, n_kv)         half 16; the other halves are zero
+  quad_tag   (L, NB, n_kv, TAGW)  bf16  NaN-init content tag (separate)
 
-One record means one base address per (page, kv-head) and one DRAM neighbourhood: the
-gfx950 score kernel feeds each 16-byte load of a V column straight into an int8
-matrix-core instruction, and reads the scales with one more 16-byte load per lane
-instead of five scattered small ones.  ``v_to_device`` / ``v_to_reference`` convert V
-between the two layouts; ``load_reference`` and ``reference_V`` use them.
+Every V / mu record is whole 128-byte lines and a block's n_kv records are contiguous,
+so the gfx950 score kernel (one wave per kv head of a block, all on one CU) streams whole
+lines, feeds each 16-byte load of a V column straight into an int8 matrix-core
+instruction, and reads a page's scales with one more 16-byte load per lane.
+``v_to_device`` / ``v_to_reference`` convert V between this and the reference layout;
+``load_reference`` and ``reference_V`` use them.
 
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
 (R, n_kv, G, MP) and hmax (R, n_kv, G).
@@ -102,11 +104,13 @@ class QuadState:
             raise ValueError("the packed quad record holds r' <= 8 columns of d = 128")
         cb = D // 2 if v_bits == 4 else D
         vb = r * cb
-        self.rec_bytes = vb + D + 64
-        self.quad_rec = torch.zeros(L, NB, n_kv, self.rec_bytes, device=device, dtype=i8)
-        meta = self.quad_rec[..., vb + D:].view(f16)                   # (L, NB, n_kv, 32)
-        self.quad_V = self.quad_rec[..., :vb].unflatten(-1, (r, cb))
-        self.quad_mu = self.quad_rec[..., vb:vb + D]
+        vm = vb + D                                       # V + mu bytes per head
+        self.rec_bytes = vm + 64                          # + the head's scale block
+        self.quad_rec = torch.zeros(L, NB, n_kv * self.rec_bytes, device=device, dtype=i8)
+        recs = self.quad_rec[..., :n_kv * vm].unflatten(-1, (n_kv, vm))
+        meta = self.quad_rec[..., n_kv * vm:].unflatten(-1, (n_kv, 64)).view(f16)
+        self.quad_V = recs[..., :vb].unflatten(-1, (r, cb))
+        self.quad_mu = recs[..., vb:]
         self.V_scale = meta[..., 0:r]
         self.quad_sig2 = meta[..., 8:8 + r]
         self.mu_scale = meta[..., 16]

@@ -15,31 +15,31 @@
 // the recipe of selection/quad_score_cuda.py:902-935 with IEEE divides) and every
 // contraction is an exact int32 sum: comb = 128 * (hi . x) + (lo . x).
 //
-// Layout.  One record per (block, kv-head) (AMASS_QUAD_REC_BYTES): quad_V column-major
-// (r' columns of CB bytes), then the 128 mu codes, then 64 bytes of fp16 scales
-// (V_scale at half 0, sig2 at half 8, mu_scale at half 16).  The 16 bytes a lane feeds
-// to one MFMA (16 consecutive d of one column of one page) are one dwordx4 load, the two
-// K-steps of a column read one whole 128-byte line, and the page's scales are one more
-// 16-byte load per lane spread over the tile's four lane groups and exchanged with
-// ds_bpermute.  int4 V (CB = 64) has byte j = code[j] | code[j + 64] << 4: shifting the
-// low nibble up and masking gives 16 * code as a signed byte for d = j (K-step 0) and
-// d = j + 64 (K-step 1) with two ALU ops per word; the sums are divided by 16 exactly.
+// Layout.  Per block, the n_kv heads' records [quad_V column-major (r' columns of CB
+// bytes) | 128 mu codes], then the n_kv heads' 64-byte fp16 scale blocks (V_scale at
+// half 0, sig2 at half 8, mu_scale at half 16) -- AMASS_QUAD_REC_BYTES per head.  The 16
+// bytes a lane feeds to one MFMA (16 consecutive d of one column of one page) are one
+// dwordx4 load, the two K-steps of a column read one whole 128-byte line, every V / mu
+// record is whole 128-byte lines, and a page's scales are one more 16-byte load per lane
+// spread over the tile's four lane groups and exchanged with ds_bpermute.  int4 V
+// (CB = 64) has byte j = code[j] | code[j + 64] << 4: shifting the low nibble up and
+// masking gives 16 * code as a signed byte for d = j (K-step 0) and d = j + 64 (K-step
+// 1) with two ALU ops per word; the sums are divided by 16 exactly.
 //
 // Lanes.  lane = 16 kg + n: column n of the MFMA is page n of the tile, kg the 16-d
-// group of each K-step (d = 64 t + 16 kg + s for slot s).  A wave owns one (request,
-// kv-head) and strides over its 16-page tiles; each tile is two load groups (columns
+// group of each K-step (d = 64 t + 16 kg + s for slot s).  A workgroup holds one wave per
+// kv head (up to 8) of one request and all its waves walk the same 16-page tiles, so a
+// block's records are read by one CU together; each tile is two load groups (columns
 // [0, r'/2) + mu + scales, then [r'/2, r')), double-buffered so one group streams in
 // while the other is multiplied.  Result rows 4kg..4kg+3 of lane (kg, n) are limbs
 // (hi, lo) of g = 2kg and 2kg+1, so the fp32 epilogue runs on every lane with 2kg < G.
-// Workgroups are placed so that the n_kv heads of one (request, page range) run on one
-// XCD together, reading neighbouring records of the same blocks through one L2.
 #include "common.h"
 
 namespace amass {
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int QS_WAVES = 4;
+constexpr int QS_MAXW = 8;      // waves (kv heads) per workgroup
 constexpr int QS_TILE = 16;     // pages per MFMA tile
 
 struct QuadParams {
@@ -52,7 +52,8 @@ struct QuadParams {
     int32_t* comb_out;
     float scale;
     int n_req, n_kv, G, page, max_pages;
-    int zsplit;     // workgroups per (request, kv-head)
+    int hw;         // kv heads (waves) per workgroup
+    int zsplit;     // workgroups per (request, head group)
     int units;      // n_req * zsplit
 };
 
@@ -67,7 +68,7 @@ __device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
 // bytes per V column / loads per column (int8: two K-steps; int4: one word set)
 template <int VB> constexpr int col_bytes() { return VB == 8 ? 128 : 64; }
 template <int VB> constexpr int loads_per_col() { return VB == 8 ? 2 : 1; }
-template <int RP, int VB> constexpr int rec_bytes() { return RP * col_bytes<VB>() + 192; }
+template <int RP, int VB> constexpr int vm_bytes() { return RP * col_bytes<VB>() + 128; }
 
 template <int RP, int VB>
 struct QuadGroupA {                       // columns [0, RP/2), mu, the page's scales
@@ -88,9 +89,9 @@ struct PageScales {
     uint32_t mus;                         // mu_scale in the low half
 };
 
-// `lr` = the lane's record (block record + head * REC + 16 kg)
+// `lr` = the lane's record (block + head * VM + 16 kg); `moff` = its scale block - lr
 template <int RP, int VB>
-__device__ __forceinline__ void load_a(const int8_t* lr, QuadGroupA<RP, VB>& a) {
+__device__ __forceinline__ void load_a(const int8_t* lr, QuadGroupA<RP, VB>& a, int moff) {
     constexpr int CB = col_bytes<VB>();
 #pragma unroll
     for (int c = 0; c < QuadGroupA<RP, VB>::NC; ++c) {
@@ -103,7 +104,7 @@ __device__ __forceinline__ void load_a(const int8_t* lr, QuadGroupA<RP, VB>& a) 
     }
     a.mu[0] = ld16(lr + RP * CB);
     a.mu[1] = ld16(lr + RP * CB + 64);
-    a.meta = ld16(lr + RP * CB + 128);
+    a.meta = ld16(lr + moff);
 }
 
 template <int RP, int VB>
@@ -263,24 +264,20 @@ __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (
 // COMB: also write the int32 contractions to comb_out (a test entry; the production
 // instance has no extra stores in its loop, which keeps the load wait counts exact).
 template <int RP, int VB, bool NRM, bool COMB>
-__global__ __launch_bounds__(QS_WAVES * WAVE)
+__global__ __launch_bounds__(QS_MAXW * WAVE)
 void quad_score_kernel(const QuadParams p) {
-    constexpr int REC = rec_bytes<RP, VB>();
+    constexpr int VM = vm_bytes<RP, VB>();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kg = lane >> 4;
-    // XCD-aware placement: workgroup b runs on XCD b % 8; the n_kv heads of a unit u
-    // (request, page range) are consecutive workgroups of one XCD.
-    const int b = blockIdx.x;
-    const int local = b >> 3;
-    const int h = local % p.n_kv;
-    const int u = (local / p.n_kv) * 8 + (b & 7);
-    if (u >= p.units) return;
+    // workgroup (unit u = (request, z), head group y): wave w serves head y * hw + w
+    const int h = blockIdx.y * p.hw + wave;
+    const int u = blockIdx.x;
     const int req = u / p.zsplit, z = u % p.zsplit;
     const int nsh = p.nsh[req];
     const int ntile = (nsh + QS_TILE - 1) / QS_TILE;
-    const int wstride = p.zsplit * QS_WAVES;
-    const int t0 = z * QS_WAVES + wave;
+    const int wstride = p.zsplit;
+    const int t0 = z;
     if (t0 >= ntile) return;
     const int cnt = (ntile - t0 + wstride - 1) / wstride;
 
@@ -312,14 +309,15 @@ void quad_score_kernel(const QuadParams p) {
     };
     // the loop carries block ids, not record pointers: carried pointers made the
     // compiler double the load buffers and copy them at the loop head
-    const int64_t rhead = (int64_t)h * REC + 16 * kg;
+    const int64_t rhead = (int64_t)h * VM + 16 * kg;
+    const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
     auto lane_rec = [&](int64_t blk) { return p.rec + blk * p.rec_sb + rhead; };
 
     int tile = t0;
     const int8_t* lr = lane_rec(lane_blk(tile));
     QuadGroupA<RP, VB> ga;
     QuadGroupB<RP, VB> gb;
-    load_a<RP, VB>(lr, ga);
+    load_a<RP, VB>(lr, ga, moff);
     int64_t bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
     // issue order A, next block id, B -- the order the loop keeps, so the loop's wait
     // counts hold on entry as well
@@ -377,7 +375,7 @@ void quad_score_kernel(const QuadParams p) {
         // keep the refill of a buffer after its last use (bounds the live registers)
         __builtin_amdgcn_sched_barrier(0);
         const int8_t* ln = lane_rec(bn_next);
-        load_a<RP, VB>(ln, ga);
+        load_a<RP, VB>(ln, ga, moff);
         bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
         tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1,
                                        qcoef);
@@ -392,11 +390,14 @@ void quad_score_kernel(const QuadParams p) {
     tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
 }
 
-// Workgroups per CU the kernel can keep resident (queried once per instance).
+// Workgroups per CU the kernel can keep resident at `threads` per workgroup (queried once
+// per kernel instance and workgroup size).
 template <typename K>
 static int resident_per_cu(K kernel, int threads, int& cus) {
-    static int cached = 0, cached_cus = 0;
-    if (cached == 0) {
+    static int cached[QS_MAXW + 1] = {0};
+    static int cached_cus = 0;
+    const int w = threads / WAVE;
+    if (cached[w] == 0) {
         int dev = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cached_cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -405,20 +406,19 @@ static int resident_per_cu(K kernel, int threads, int& cus) {
                 hipSuccess ||
             per_cu < 1) {
             cus = 256;
-            return 2;
+            return 1;
         }
-        cached = per_cu;
+        cached[w] = per_cu;
     }
     cus = cached_cus;
-    return cached;
+    return cached[w];
 }
 
-// One resident round of workgroups over (request, kv-head) pairs, at most enough that
-// every wave gets a tile.
-static int quad_zsplit(int resident, int pairs, int tiles) {
-    int z = (resident + pairs - 1) / pairs;
-    const int zmax = (tiles + QS_WAVES - 1) / QS_WAVES;
-    z = z < zmax ? z : zmax;
+// One resident round of workgroups over (request, head group) units, at most one per
+// tile.
+static int quad_zsplit(int resident, int groups, int tiles) {
+    int z = (resident + groups - 1) / groups;
+    z = z < tiles ? z : tiles;
     return z < 1 ? 1 : z;
 }
 
@@ -426,11 +426,11 @@ template <int RP, int VB, bool NRM, bool COMB>
 static int launch_quad_k(QuadParams p, int tiles, hipStream_t s) {
     auto k = quad_score_kernel<RP, VB, NRM, COMB>;
     int cus = 0;
-    const int per_cu = resident_per_cu(k, QS_WAVES * WAVE, cus);
-    p.zsplit = quad_zsplit(per_cu * cus, p.n_req * p.n_kv, tiles);
+    const int per_cu = resident_per_cu(k, p.hw * WAVE, cus);
+    const int hg = p.n_kv / p.hw;
+    p.zsplit = quad_zsplit(per_cu * cus, p.n_req * hg, tiles);
     p.units = p.n_req * p.zsplit;
-    const int upad = (p.units + 7) / 8 * 8;
-    hipLaunchKernelGGL(k, dim3(upad * p.n_kv), dim3(QS_WAVES * WAVE), 0, s, p);
+    hipLaunchKernelGGL(k, dim3(p.units, hg), dim3(p.hw * WAVE), 0, s, p);
     return check_launch();
 }
 
@@ -454,6 +454,7 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     if (a->combine == 1 && !a->score_h) return AMASS_ERR_NULL;
     if (a->combine != 0 && a->combine != 1) return AMASS_ERR_GEOMETRY;
     if (a->d != 128 || a->n_req < 0 || a->max_pages < 1 || a->n_kv < 1) return AMASS_ERR_GEOMETRY;
+    if (a->n_kv > QS_MAXW && a->n_kv % QS_MAXW != 0) return AMASS_ERR_GEOMETRY;
     if (a->G < 1 || a->G > 8) return AMASS_ERR_GEOMETRY;
     if (a->v_bits != 8 && a->v_bits != 4) return AMASS_ERR_GEOMETRY;
     if (a->rank != 2 && a->rank != 4 && a->rank != 8) return AMASS_ERR_UNSUPPORTED;
@@ -473,6 +474,7 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     p.scale = a->scale;
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.G = a->G; p.page = a->page;
     p.max_pages = a->max_pages;
+    p.hw = a->n_kv < QS_MAXW ? a->n_kv : QS_MAXW;
     p.zsplit = 1; p.units = a->n_req;
     const int tiles = (a->max_pages + QS_TILE - 1) / QS_TILE;
     hipStream_t s = (hipStream_t)stream;

@@ -45,15 +45,16 @@ extern "C" {
  * q is quantised per q-head to two int8 limbs (qi = rn(q/qs), qs = max|q|/16383,
  * hi = rn(qi/128), lo = qi - 128 hi) and the d-contractions are exact int32 sums.
  *
- * Summary record.  The reference's five per-(block, kv-head) slabs (quad_mu, mu_scale,
- * quad_V, V_scale, quad_sig2) are packed into one contiguous record per (block, kv-head)
- * of AMASS_QUAD_REC_BYTES(rank, v_bits) bytes, n_kv records per block:
- *   [0, r'*CB)          quad_V column-major: column k = CB bytes; int8 CB = d = 128
- *                       (byte j = code[j]); int4 CB = 64 (byte j = code[j] | code[j+64] << 4)
- *   [r'*CB, +128)       quad_mu int8 codes (d)
- *   [r'*CB+128, +64)    fp16: V_scale[0..r') at half 0, sig2[0..r') at half 8,
- *                       mu_scale at half 16, the rest zero
- * rec points at block 0 of the layer, rec_sb is the block stride in bytes. */
+ * Summary records.  The reference's five per-(block, kv-head) slabs (quad_mu, mu_scale,
+ * quad_V, V_scale, quad_sig2) are packed per block, AMASS_QUAD_REC_BYTES(rank, v_bits)
+ * bytes per kv head (VM = r'*CB + 128 of them first, in head order, then 64 per head):
+ *   head h at h*VM:         quad_V column-major, column k = CB bytes; int8 CB = d = 128
+ *                           (byte j = code[j]); int4 CB = 64 (byte j = code[j] | code[j+64] << 4),
+ *                           then the 128 quad_mu int8 codes
+ *   head h at n_kv*VM+64h:  fp16 V_scale[0..r') at half 0, sig2[0..r') at half 8,
+ *                           mu_scale at half 16, the rest zero
+ * rec points at block 0 of the layer, rec_sb is the block stride in bytes (at least
+ * n_kv * AMASS_QUAD_REC_BYTES, a multiple of 16).  n_kv <= 8 or a multiple of 8. */
 #define AMASS_QUAD_REC_BYTES(rank, v_bits) ((rank) * ((v_bits) == 8 ? 128 : 64) + 192)
 typedef struct amass_quad_score_args {
     const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
