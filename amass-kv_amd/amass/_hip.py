@@ -18,6 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
+ABI_VERSION = 2     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):
@@ -44,10 +45,9 @@ class QuadScoreArgs(C.Structure):
 
 class R8ScoreArgs(C.Structure):
     _fields_ = _fields(
-        "q:p q_st:i64 q_hs:i64 mu:p mu_sb:i64 mu_scale:p mus_sb:i64 vk:p vk_sb:i64 "
-        "vk_scale:p vks_sb:i64 c:p c_sb:i64 c_scale:p cs_sb:i64 block_table:p bt_st:i64 "
-        "seq_lens:p n_sel_hi:p score:p sc_sr:i64 sc_sh:i64 comb_out:p scale:f32 n_req:i32 "
-        "n_kv:i32 G:i32 d:i32 page:i32 rank:i32 vk_bits:i32 c_bits:i32 max_pages:i32")
+        "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 seq_lens:p "
+        "n_sel_hi:p score:p sc_sr:i64 sc_sh:i64 comb_out:p scale:f32 n_req:i32 n_kv:i32 "
+        "G:i32 d:i32 page:i32 rank:i32 vk_bits:i32 c_bits:i32 max_pages:i32")
 
 
 class DeriveArgs(C.Structure):
@@ -157,6 +157,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     lib.amass_status_string.argtypes = [C.c_int]
     lib.amass_status_string.restype = C.c_char_p
     lib.amass_last_hip_error.restype = C.c_int
+    if lib.amass_abi_version() != ABI_VERSION:
+        raise AmassError(f"{path} has ABI version {lib.amass_abi_version()}, these bindings "
+                         f"expect {ABI_VERSION}: rebuild it")
     _LIB = lib
     return lib
 

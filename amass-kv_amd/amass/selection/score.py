@@ -16,17 +16,23 @@ def r8_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
              comb_out=None) -> None:
     if n_req > st.max_reqs:
         raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
-    mu, mu_s, Vk, Vk_s, c, c_s, _ = st.layer_state(layer)
-    require_cuda(q, block_table, seq_lens, mu)
+    rec = st.r8_rec[layer]
+    require_cuda(q, block_table, seq_lens, rec)
     if q.dtype != torch.bfloat16 or q.stride(2) != 1:
         raise ValueError("q must be bf16 (T, H, d) with unit stride on d")
     if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise ValueError("block_table / seq_lens must be int32")
+    if block_table.stride(1) != 1:
+        raise ValueError("block_table must have unit column stride")
+    if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
+        raise ValueError("r8_rec must hold each block's records contiguously")
+    if comb_out is not None and (comb_out.dtype != torch.int32 or not comb_out.is_contiguous()
+                                 or tuple(comb_out.shape[1:]) != (st.n_kv, st.max_pages, st.G,
+                                                                  st.r + 1)):
+        raise ValueError("comb_out must be a contiguous int32 (R, n_kv, MP, G, r+1) tensor")
     a = R8ScoreArgs(
         q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),
-        mu=ptr(mu), mu_sb=mu.stride(0), mu_scale=ptr(mu_s), mus_sb=mu_s.stride(0),
-        vk=ptr(Vk), vk_sb=Vk.stride(0), vk_scale=ptr(Vk_s), vks_sb=Vk_s.stride(0),
-        c=ptr(c), c_sb=c.stride(0), c_scale=ptr(c_s), cs_sb=c_s.stride(0),
+        rec=ptr(rec), rec_sb=rec.stride(0),
         block_table=ptr(block_table), bt_st=block_table.stride(0),
         seq_lens=ptr(seq_lens), n_sel_hi=ptr(st.n_sel_hi),
         score=ptr(st.score), sc_sr=st.score.stride(0), sc_sh=st.score.stride(1),

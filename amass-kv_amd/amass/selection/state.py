@@ -1,13 +1,29 @@
 """R8State -- persistent buffers of the r8 (low-rank per-key LSE) selector.
 
-Same tensors, dtypes and layout as the reference (``selection/state.py:35-112``): every
-buffer is allocated once from engine maxima so its address is stable across HIP-graph
-replays.  Physical-block keyed, L-major summary slabs:
+Every buffer is allocated once from engine maxima so its address is stable across
+HIP-graph replays.  The reference (``selection/state.py:35-112``) keeps six summary slabs
+per layer; this build packs them into one block-keyed buffer and exposes the reference's
+names as views into it.  Per (layer, block), REC = r*CB + 128 + 16*r*c_bits/8 + 64 bytes
+per kv head:
 
-  r8_mu    (L, NB, n_kv, d)       int8   + mu_scale  (L, NB, n_kv)      fp16
-  r8_Vk    (L, NB, n_kv, d, r)    int8   + Vk_scale  (L, NB, n_kv, r)   fp16   (int4: d, r/2)
-  r8_c     (L, NB, n_kv, page, r) int8   + c_scale   (L, NB, n_kv, page) fp16  (int4: page, r/2)
-  r8_tag   (L, NB, n_kv, TAGW)    bf16   NaN-init content tag
+  r8_rec   (L, NB, n_kv * REC)  int8, per block:
+    n_kv records of VM = r*CB + 128 + 16*r*c_bits/8 bytes, head h at h * VM:
+      r8_Vk    (L, NB, n_kv, r, CB)   int8  column-major: column k holds CB bytes;
+               int8 CB = d (byte j = code[j]); int4 CB = d/2, byte j = code[j] | code[j+d/2] << 4
+               (the reference keeps (.., d, r) with two columns per int4 byte)
+      r8_mu    (L, NB, n_kv, d)       int8  page-mean codes
+      r8_c     (L, NB, n_kv, page, r) int8  per-key coordinates (int4: (.., page, r/2),
+               low nibble = even column, as in the reference)
+    then n_kv scale blocks of 64 bytes (fp16 halves), head h at n_kv * VM + 64 h:
+      Vk_scale (L, NB, n_kv, r)       half 0..r-1
+      c_scale  (L, NB, n_kv, page)    half 8..23
+      mu_scale (L, NB, n_kv)          half 24; the other halves are zero
+  r8_tag   (L, NB, n_kv, TAGW)  bf16  NaN-init content tag (separate)
+
+A block's records are contiguous and the score kernel feeds each 16-byte load of a Vk
+column straight into an int8 matrix-core instruction (the quad record's reasoning,
+:mod:`amass.selection.quad_state`).  ``reference_Vk`` / ``load_reference`` convert Vk
+between this and the reference layout.
 
 Per-step outputs (request-row keyed): score (R, n_kv, MP) fp32, page_table (R, n_kv, MP)
 int32, page_cnt (R, n_kv) int32, n_pages / n_sel_hi / b_fix (R,) int32, budget64.
@@ -46,14 +62,23 @@ class R8State:
         self.device = device
         i8, f16, bf16 = torch.int8, torch.float16, torch.bfloat16
         i32, f32, f64 = torch.int32, torch.float32, torch.float64
-        rvk = r // 2 if vk_bits == 4 else r
+        if D != 128 or page != 16 or not 1 <= r <= 8 or (4 in (vk_bits, c_bits) and r % 2):
+            raise ValueError("the packed r8 record holds r <= 8 columns of d = 128 and "
+                             "16-token pages (r even for int4 codes)")
+        cb = D // 2 if vk_bits == 4 else D
         rc = r // 2 if c_bits == 4 else r
-        self.r8_mu = torch.zeros(L, NB, n_kv, D, device=device, dtype=i8)
-        self.mu_scale = torch.zeros(L, NB, n_kv, device=device, dtype=f16)
-        self.r8_Vk = torch.zeros(L, NB, n_kv, D, rvk, device=device, dtype=i8)
-        self.Vk_scale = torch.zeros(L, NB, n_kv, r, device=device, dtype=f16)
-        self.r8_c = torch.zeros(L, NB, n_kv, page, rc, device=device, dtype=i8)
-        self.c_scale = torch.zeros(L, NB, n_kv, page, device=device, dtype=f16)
+        vb, cbytes = r * cb, page * rc
+        vm = vb + D + cbytes                              # Vk + mu + c bytes per head
+        self.rec_bytes = vm + 64                          # + the head's scale block
+        self.r8_rec = torch.zeros(L, NB, n_kv * self.rec_bytes, device=device, dtype=i8)
+        recs = self.r8_rec[..., :n_kv * vm].unflatten(-1, (n_kv, vm))
+        meta = self.r8_rec[..., n_kv * vm:].unflatten(-1, (n_kv, 64)).view(f16)
+        self.r8_Vk = recs[..., :vb].unflatten(-1, (r, cb))
+        self.r8_mu = recs[..., vb:vb + D]
+        self.r8_c = recs[..., vb + D:].unflatten(-1, (page, rc))
+        self.Vk_scale = meta[..., 0:r]
+        self.c_scale = meta[..., 8:8 + page]
+        self.mu_scale = meta[..., 24]
         self.r8_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=device, dtype=bf16)
         self.score = torch.empty(R, n_kv, MP, device=device, dtype=f32)
         self.page_table = torch.empty(R, n_kv, MP, device=device, dtype=i32)
@@ -65,12 +90,28 @@ class R8State:
         self.budget64 = torch.tensor([self.budget], device=device, dtype=f64)
 
     def bytes_per_layer(self) -> int:
-        return (self.r8_mu[0].numel() + self.r8_Vk[0].numel() + self.r8_c[0].numel()
-                + 2 * (self.mu_scale[0].numel() + self.Vk_scale[0].numel()
-                       + self.c_scale[0].numel() + self.r8_tag[0].numel()))
+        return self.r8_rec[0].numel() + 2 * self.r8_tag[0].numel()
 
     def layer_state(self, layer: int):
-        """(mu, mu_scale, Vk, Vk_scale, c, c_scale, tag) views of ``layer``."""
+        """(mu, mu_scale, Vk, Vk_scale, c, c_scale, tag) views of ``layer`` (Vk
+        column-major; :meth:`reference_Vk` gives the reference layout)."""
         return (self.r8_mu[layer], self.mu_scale[layer], self.r8_Vk[layer],
                 self.Vk_scale[layer], self.r8_c[layer], self.c_scale[layer],
                 self.r8_tag[layer])
+
+    def load_reference(self, layer: int, mu, mu_scale, Vk, Vk_scale, c, c_scale) -> None:
+        """Write one layer's summaries given in the reference layout
+        (``selection/state.py:35-112``: r8_Vk (NB, n_kv, d, r[/2]))."""
+        from .quad_state import v_to_device
+        dev = self.r8_rec.device
+        self.r8_mu[layer].copy_(torch.as_tensor(mu).to(dev))
+        self.mu_scale[layer].copy_(torch.as_tensor(mu_scale).to(dev))
+        self.r8_Vk[layer].copy_(v_to_device(torch.as_tensor(Vk).to(dev), self.vk_bits))
+        self.Vk_scale[layer].copy_(torch.as_tensor(Vk_scale).to(dev))
+        self.r8_c[layer].copy_(torch.as_tensor(c).to(dev))
+        self.c_scale[layer].copy_(torch.as_tensor(c_scale).to(dev))
+
+    def reference_Vk(self, layer: int) -> torch.Tensor:
+        """r8_Vk of ``layer`` in the reference layout (NB, n_kv, d, r[/2])."""
+        from .quad_state import v_to_reference
+        return v_to_reference(self.r8_Vk[layer], self.vk_bits)

@@ -33,14 +33,12 @@
 // [0, r'/2) + mu + scales, then [r'/2, r')), double-buffered so one group streams in
 // while the other is multiplied.  Result rows 4kg..4kg+3 of lane (kg, n) are limbs
 // (hi, lo) of g = 2kg and 2kg+1, so the fp32 epilogue runs on every lane with 2kg < G.
-#include "common.h"
+#include "score_mfma.h"
 
 namespace amass {
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
 constexpr int QS_MAXW = 8;      // waves (kv heads) per workgroup
-constexpr int QS_TILE = 16;     // pages per MFMA tile
+constexpr int QS_TILE = SC_TILE;
 
 struct QuadParams {
     const uint16_t* q; int64_t q_st, q_hs;
@@ -53,21 +51,9 @@ struct QuadParams {
     float scale;
     int n_req, n_kv, G, page, max_pages;
     int hw;         // kv heads (waves) per workgroup
-    int zsplit;     // workgroups per (request, head group)
-    int units;      // n_req * zsplit
+    int target;     // workgroups the batch's tiles are balanced over
 };
 
-__device__ __forceinline__ i32x4_t ld16(const int8_t* p) {
-    return *reinterpret_cast<const i32x4_t*>(p);
-}
-
-__device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
-// bytes per V column / loads per column (int8: two K-steps; int4: one word set)
-template <int VB> constexpr int col_bytes() { return VB == 8 ? 128 : 64; }
-template <int VB> constexpr int loads_per_col() { return VB == 8 ? 2 : 1; }
 template <int RP, int VB> constexpr int vm_bytes() { return RP * col_bytes<VB>() + 128; }
 
 template <int RP, int VB>
@@ -134,34 +120,6 @@ __device__ __forceinline__ PageScales gather_scales(i32x4_t meta, int n) {
     }
     s.mus = (uint32_t)__shfl(meta[0], n + 32, WAVE);
     return s;
-}
-
-__device__ __forceinline__ float half_at(const uint32_t (&w)[4], int k) {
-    return fp16_to_f32((uint16_t)((w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu));
-}
-
-// MFMA over one column: int8 -> two K-steps; int4 -> both K-steps from one word set.
-template <int VB>
-__device__ __forceinline__ i32x4_t col_mfma(const i32x4_t (&qa)[2], const i32x4_t* x) {
-    i32x4_t acc = {0, 0, 0, 0};
-    if constexpr (VB == 8) {
-        acc = mfma_i8(qa[0], x[0], acc);
-        acc = mfma_i8(qa[1], x[1], acc);
-    } else {
-        const i32x4_t m = {(int)0xF0F0F0F0u, (int)0xF0F0F0F0u, (int)0xF0F0F0F0u,
-                           (int)0xF0F0F0F0u};
-        acc = mfma_i8(qa[0], (x[0] << 4) & m, acc);
-        acc = mfma_i8(qa[1], x[0] & m, acc);
-    }
-    return acc;
-}
-
-// Combined int32 d-contractions of g = 2kg (x) and 2kg+1 (y) from one MFMA result.
-template <int VB>
-__device__ __forceinline__ void comb2(i32x4_t acc, int& x, int& y) {
-    x = acc[0] * 128 + acc[1];
-    y = acc[2] * 128 + acc[3];
-    if constexpr (VB == 4) { x >>= 4; y >>= 4; }   // exact: both are multiples of 16
 }
 
 // Running fp32 epilogue of one tile for g = 2kg + e: the quad sum in column order and
@@ -272,32 +230,17 @@ void quad_score_kernel(const QuadParams p) {
     const int n = lane & 15, kg = lane >> 4;
     // workgroup (unit u = (request, z), head group y): wave w serves head y * hw + w
     const int h = blockIdx.y * p.hw + wave;
-    const int u = blockIdx.x;
-    const int req = u / p.zsplit, z = u % p.zsplit;
+    TileWalk tw;
+    if (!tile_walk(p.nsh, p.n_req, p.target, blockIdx.x, tw) || tw.count <= 0) return;
+    const int req = tw.req;
     const int nsh = p.nsh[req];
-    const int ntile = (nsh + QS_TILE - 1) / QS_TILE;
-    const int wstride = p.zsplit;
-    const int t0 = z;
-    if (t0 >= ntile) return;
-    const int cnt = (ntile - t0 + wstride - 1) / wstride;
+    const int cnt = tw.count;
+    const int t0 = tw.first;
+    const int wstride = tw.stride;
 
     // ---- query limbs: lane row m = n holds limb (n & 1) of g = n >> 1 -------------------
-    const int qg = n >> 1;
-    const bool qlive = qg < p.G;
     uint32_t qw[2][8];          // bf16 pairs, d = 64 t + 16 kg + 2 i (+1)
-    {
-        const int gq = qlive ? qg : p.G - 1;       // unconditional loads, zeroed below
-        const uint16_t* qrow = p.q + (int64_t)req * p.q_st + (int64_t)(h * p.G + gq) * p.q_hs;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint4 x0 = *reinterpret_cast<const uint4*>(qrow + 64 * t + 16 * kg);
-            const uint4 x1 = *reinterpret_cast<const uint4*>(qrow + 64 * t + 16 * kg + 8);
-            qw[t][0] = x0.x; qw[t][1] = x0.y; qw[t][2] = x0.z; qw[t][3] = x0.w;
-            qw[t][4] = x1.x; qw[t][5] = x1.y; qw[t][6] = x1.z; qw[t][7] = x1.w;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qw[t][i] = qlive ? qw[t][i] : 0u;
-        }
-    }
+    load_q_rows(p.q, p.q_st, p.q_hs, req, h, p.G, n, kg, false, qw);
 
     // tile addressing: lane n owns page 16 tile + n; clamped pages load valid data and
     // are never written
@@ -324,41 +267,8 @@ void quad_score_kernel(const QuadParams p) {
     __builtin_amdgcn_sched_barrier(0);
     load_b<RP, VB>(lr, gb);
 
-    // |bf16| orders like its magnitude bits: take the max as integers
-    uint32_t amax = 0;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            amax = max(amax, max(qw[t][i] & 0x7FFFu, (qw[t][i] >> 16) & 0x7FFFu));
-    float mx = __uint_as_float(amax << 16);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-    mx = fmaxf(mx, 1e-12f);
-    const float qs = mx / 16383.0f;            // correctly rounded divides
-    const float inv = 16383.0f / mx;
-    const int limb = n & 1;
     i32x4_t qa[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int wi = 0; wi < 4; ++wi) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 4 * wi + j;
-                const uint32_t wv = qw[t][e >> 1];
-                const float fv = (e & 1) ? bf16hi(wv) : bf16lo(wv);
-                int qi = (int)rintf(__fmul_rn(fv, inv));
-                qi = max(-16383, min(16383, qi));
-                int hi = (int)rintf((float)qi * 0.0078125f);
-                hi = max(-127, min(127, hi));
-                const int v = limb ? qi - 128 * hi : hi;
-                word |= ((uint32_t)(v & 0xFF)) << (8 * j);
-            }
-            qa[t][wi] = (int)word;
-        }
-    }
+    const float qs = quantize_q_rows(qw, n, qa);
     const float qs0 = __shfl(qs, 4 * kg, WAVE);        // lane 4kg: row 4kg = g 2kg
     const float qs1 = __shfl(qs, 4 * kg + 2, WAVE);
     const float qcoef = p.scale * p.scale / (2.0f * (float)p.page);
@@ -390,57 +300,27 @@ void quad_score_kernel(const QuadParams p) {
     tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
 }
 
-// Workgroups per CU the kernel can keep resident at `threads` per workgroup (queried once
-// per kernel instance and workgroup size).
-template <typename K>
-static int resident_per_cu(K kernel, int threads, int& cus) {
-    static int cached[QS_MAXW + 1] = {0};
-    static int cached_cus = 0;
-    const int w = threads / WAVE;
-    if (cached[w] == 0) {
-        int dev = 0, per_cu = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cached_cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) !=
-                hipSuccess ||
-            per_cu < 1) {
-            cus = 256;
-            return 1;
-        }
-        cached[w] = per_cu;
-    }
-    cus = cached_cus;
-    return cached[w];
-}
-
-// One resident round of workgroups over (request, head group) units, at most one per
-// tile.
-static int quad_zsplit(int resident, int groups, int tiles) {
-    int z = (resident + groups - 1) / groups;
-    z = z < tiles ? z : tiles;
-    return z < 1 ? 1 : z;
-}
-
 template <int RP, int VB, bool NRM, bool COMB>
-static int launch_quad_k(QuadParams p, int tiles, hipStream_t s) {
+static int launch_quad_k(QuadParams p, hipStream_t s) {
     auto k = quad_score_kernel<RP, VB, NRM, COMB>;
+    // all min(n_kv, 8) heads of a block in one workgroup: measured faster for this kernel
+    // than the 4-head split even where that keeps more waves resident
     int cus = 0;
-    const int per_cu = resident_per_cu(k, p.hw * WAVE, cus);
+    p.hw = p.n_kv < QS_MAXW ? p.n_kv : QS_MAXW;
+    const int per_cu = resident_per_cu((const void*)k, p.hw * WAVE, cus);
     const int hg = p.n_kv / p.hw;
-    p.zsplit = quad_zsplit(per_cu * cus, p.n_req * hg, tiles);
-    p.units = p.n_req * p.zsplit;
-    hipLaunchKernelGGL(k, dim3(p.units, hg), dim3(p.hw * WAVE), 0, s, p);
+    p.target = score_target(per_cu * cus, hg);
+    hipLaunchKernelGGL(k, dim3(p.target + p.n_req, hg), dim3(p.hw * WAVE), 0, s, p);
     return check_launch();
 }
 
 template <int RP, int VB>
-static int launch_quad_rv(const QuadParams& p, bool nrm, int tiles, hipStream_t s) {
+static int launch_quad_rv(const QuadParams& p, bool nrm, hipStream_t s) {
     if (p.comb_out != nullptr)
-        return nrm ? launch_quad_k<RP, VB, true, true>(p, tiles, s)
-                   : launch_quad_k<RP, VB, false, true>(p, tiles, s);
-    return nrm ? launch_quad_k<RP, VB, true, false>(p, tiles, s)
-               : launch_quad_k<RP, VB, false, false>(p, tiles, s);
+        return nrm ? launch_quad_k<RP, VB, true, true>(p, s)
+                   : launch_quad_k<RP, VB, false, true>(p, s);
+    return nrm ? launch_quad_k<RP, VB, true, false>(p, s)
+               : launch_quad_k<RP, VB, false, false>(p, s);
 }
 
 }  // namespace amass
@@ -475,21 +355,20 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.G = a->G; p.page = a->page;
     p.max_pages = a->max_pages;
     p.hw = a->n_kv < QS_MAXW ? a->n_kv : QS_MAXW;
-    p.zsplit = 1; p.units = a->n_req;
-    const int tiles = (a->max_pages + QS_TILE - 1) / QS_TILE;
+    p.target = 1;
     hipStream_t s = (hipStream_t)stream;
     const bool nrm = a->combine == 1;
     if (a->v_bits == 8) {
         switch (a->rank) {
-            case 2: return launch_quad_rv<2, 8>(p, nrm, tiles, s);
-            case 4: return launch_quad_rv<4, 8>(p, nrm, tiles, s);
-            case 8: return launch_quad_rv<8, 8>(p, nrm, tiles, s);
+            case 2: return launch_quad_rv<2, 8>(p, nrm, s);
+            case 4: return launch_quad_rv<4, 8>(p, nrm, s);
+            case 8: return launch_quad_rv<8, 8>(p, nrm, s);
         }
     } else {
         switch (a->rank) {
-            case 2: return launch_quad_rv<2, 4>(p, nrm, tiles, s);
-            case 4: return launch_quad_rv<4, 4>(p, nrm, tiles, s);
-            case 8: return launch_quad_rv<8, 4>(p, nrm, tiles, s);
+            case 2: return launch_quad_rv<2, 4>(p, nrm, s);
+            case 4: return launch_quad_rv<4, 4>(p, nrm, s);
+            case 8: return launch_quad_rv<8, 4>(p, nrm, s);
         }
     }
     return AMASS_ERR_UNSUPPORTED;

@@ -1,0 +1,241 @@
+// Int8 matrix-core front end shared by the quad and r8 page-score kernels (gfx950).
+//
+// Both scores start with the same small integer product per page: the 2G int8 query
+// limbs of one kv head against the r' (or r) columns of the page's column-major code
+// matrix plus its mean codes, [2G x d] x [d x (r'+1)].  It runs on
+// v_mfma_i32_16x16x64_i8 with M = the limb rows, N = 16 pages of a tile and K = 64 d per
+// instruction; lane = 16 kg + n feeds 16 consecutive d (d = 64 t + 16 kg + s) of column
+// k of page n and receives result rows 4kg..4kg+3 of column n.
+//
+// q limbs: qi = rint(q * inv) with inv = 16383 / max|q| and qs = max|q| / 16383 (both
+// correctly rounded divides), clamped to +-16383; hi = rint(qi / 128) clamped to +-127,
+// lo = qi - 128 hi, so 128 hi + lo == qi and every contraction
+// comb = 128 (hi . x) + (lo . x) is an exact int32 sum (the recipe of the reference's
+// selection/quad_score_cuda.py:902-935 and selection/score_cuda.py:182-215, with IEEE
+// divides where the reference compiles with fast math).
+#pragma once
+#include <mutex>
+
+#include "common.h"
+
+namespace amass {
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int SC_TILE = 16;     // pages per MFMA tile (the N dimension)
+
+__device__ __forceinline__ i32x4_t ld16(const int8_t* p) {
+    return *reinterpret_cast<const i32x4_t*>(p);
+}
+
+__device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// bytes per code column / 16-byte loads per column and lane (int8: two K-steps; int4:
+// one word set, byte j = code[j] | code[j + 64] << 4)
+template <int VB> constexpr int col_bytes() { return VB == 8 ? 128 : 64; }
+template <int VB> constexpr int loads_per_col() { return VB == 8 ? 2 : 1; }
+
+// MFMA over one column: int8 -> two K-steps; int4 -> both K-steps from one word set
+// (shifting the low nibble up and masking gives 16 * code as a signed byte).
+template <int VB>
+__device__ __forceinline__ i32x4_t col_mfma(const i32x4_t (&qa)[2], const i32x4_t* x) {
+    i32x4_t acc = {0, 0, 0, 0};
+    if constexpr (VB == 8) {
+        acc = mfma_i8(qa[0], x[0], acc);
+        acc = mfma_i8(qa[1], x[1], acc);
+    } else {
+        const i32x4_t m = {(int)0xF0F0F0F0u, (int)0xF0F0F0F0u, (int)0xF0F0F0F0u,
+                           (int)0xF0F0F0F0u};
+        acc = mfma_i8(qa[0], (x[0] << 4) & m, acc);
+        acc = mfma_i8(qa[1], x[0] & m, acc);
+    }
+    return acc;
+}
+
+// Combined int32 contractions of result rows (4kg, 4kg+1) -> x and (4kg+2, 4kg+3) -> y.
+template <int VB>
+__device__ __forceinline__ void comb2(i32x4_t acc, int& x, int& y) {
+    x = acc[0] * 128 + acc[1];
+    y = acc[2] * 128 + acc[3];
+    if constexpr (VB == 4) { x >>= 4; y >>= 4; }   // exact: both are multiples of 16
+}
+
+__device__ __forceinline__ float half_at(const uint32_t (&w)[4], int k) {
+    return fp16_to_f32((uint16_t)((w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu));
+}
+
+// Raw bf16 words of the A-row query of lane row n: row n holds limb (n & 1) of group
+// head g = n >> 1 (DUP: g = (n >> 1) % G, so rows 2G..15 repeat rows 0..2G-1; otherwise
+// rows of g >= G are zero).  Words cover d = 64 t + 16 kg + 2 i (+1).
+__device__ __forceinline__ void load_q_rows(const uint16_t* q, int64_t q_st, int64_t q_hs,
+                                            int req, int h, int G, int n, int kg, bool dup,
+                                            uint32_t (&qw)[2][8]) {
+    const int qg0 = n >> 1;
+    const bool live = dup || qg0 < G;
+    const int gq = dup ? qg0 % G : (live ? qg0 : G - 1);   // unconditional loads
+    const uint16_t* qrow = q + (int64_t)req * q_st + (int64_t)(h * G + gq) * q_hs;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint4 x0 = *reinterpret_cast<const uint4*>(qrow + 64 * t + 16 * kg);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(qrow + 64 * t + 16 * kg + 8);
+        qw[t][0] = x0.x; qw[t][1] = x0.y; qw[t][2] = x0.z; qw[t][3] = x0.w;
+        qw[t][4] = x1.x; qw[t][5] = x1.y; qw[t][6] = x1.z; qw[t][7] = x1.w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qw[t][i] = live ? qw[t][i] : 0u;
+    }
+}
+
+// Quantise the rows loaded by load_q_rows to int8 limbs: qa[t] is the A operand of
+// K-step t; returns this row's qs (the row's amax is reduced over its four kg lanes).
+__device__ __forceinline__ float quantize_q_rows(const uint32_t (&qw)[2][8], int n,
+                                                 i32x4_t (&qa)[2]) {
+    // |bf16| orders like its magnitude bits: take the max as integers
+    uint32_t amax = 0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            amax = max(amax, max(qw[t][i] & 0x7FFFu, (qw[t][i] >> 16) & 0x7FFFu));
+    float mx = __uint_as_float(amax << 16);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+    mx = fmaxf(mx, 1e-12f);
+    const float qs = mx / 16383.0f;            // correctly rounded divides
+    const float inv = 16383.0f / mx;
+    const int limb = n & 1;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * wi + j;
+                const uint32_t wv = qw[t][e >> 1];
+                const float fv = (e & 1) ? bf16hi(wv) : bf16lo(wv);
+                int qi = (int)rintf(__fmul_rn(fv, inv));
+                qi = max(-16383, min(16383, qi));
+                int hi = (int)rintf((float)qi * 0.0078125f);
+                hi = max(-127, min(127, hi));
+                const int v = limb ? qi - 128 * hi : hi;
+                word |= ((uint32_t)(v & 0xFF)) << (8 * j);
+            }
+            qa[t][wi] = (int)word;
+        }
+    }
+    return qs;
+}
+
+// Workgroups per CU that kernel `k` keeps resident at `threads` per workgroup (queried
+// once per kernel and workgroup size; falls back to one per CU on 256 CUs).
+static inline int resident_per_cu(const void* k, int threads, int& cus) {
+    struct Entry { const void* k; int threads, per_cu; };
+    static Entry cache[64];
+    static int n_cache = 0;
+    static int cached_cus = 0;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_cache; ++i)
+        if (cache[i].k == k && cache[i].threads == threads) {
+            cus = cached_cus;
+            return cache[i].per_cu;
+        }
+    int dev = 0, per_cu = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, 0) != hipSuccess ||
+        per_cu < 1) {
+        cus = 256;
+        return 1;
+    }
+    cached_cus = ncu;
+    if (n_cache < 64) cache[n_cache++] = Entry{k, threads, per_cu};
+    cus = ncu;
+    return per_cu;
+}
+
+// kv heads (waves) per workgroup: min(n_kv, 8), so the heads of one block are read by one
+// CU together, or 4 when that keeps more waves resident per CU (a kernel above 128 VGPRs
+// fits one 8-wave workgroup per CU but three 4-wave ones).  Returns the heads per
+// workgroup and the resident workgroups per CU for it.
+static inline int pick_heads(const void* k, int n_kv, int& per_cu, int& cus) {
+    int hw = n_kv < 8 ? n_kv : 8;
+    per_cu = resident_per_cu(k, hw * 64, cus);
+    if (hw == 8 && n_kv % 4 == 0) {
+        int cus4 = 0;
+        const int per4 = resident_per_cu(k, 4 * 64, cus4);
+        if (per4 * 4 > per_cu * 8) {
+            hw = 4;
+            per_cu = per4;
+            cus = cus4;
+        }
+    }
+    return hw;
+}
+
+// Chunks per head group: one per resident workgroup slot (a chunk runs alone on its CU
+// slot, so equal chunks finish together).
+static inline int score_target(int resident, int head_groups) {
+    const int t = resident / (head_groups > 0 ? head_groups : 1);
+    return t < 1 ? 1 : t;
+}
+
+// ---- balanced split of a (ragged) batch's page tiles over the grid ---------------------
+// Request r has tiles_r = ceil(n_sel_hi[r] / 16) tiles.  Every wave computes the batch's
+// total T and the target tiles per workgroup tpw = ceil(T / target); request r gets
+// n_r = ceil(tiles_r / tpw) workgroups, numbered consecutively over the batch, and its
+// workgroup j walks tiles j, j + n_r, j + 2 n_r, ... (a uniform batch is the plain
+// strided split).  Nothing depends on host-side knowledge of the lengths (the launch
+// stays graph-capturable); the grid is target + n_req workgroups, an upper bound of
+// sum n_r, and workgroups past the last one exit at once.
+struct TileWalk {
+    int req;       // request
+    int first;     // first tile
+    int stride;    // tile stride (workgroups of the request)
+    int count;     // tiles walked
+};
+
+__device__ __forceinline__ int tiles_of(int nsh) {
+    return nsh > 0 ? (nsh + SC_TILE - 1) / SC_TILE : 0;
+}
+
+__device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int target, int x,
+                                          TileWalk& w) {
+    const int lane = threadIdx.x & 63;
+    int total = 0;
+    for (int base = 0; base < n_req; base += WAVE) {
+        const int r = base + lane;
+        total += wave_sumi(r < n_req ? tiles_of(nsh[r]) : 0);
+    }
+    const int tpw = total > 0 ? (total + target - 1) / target : 1;
+    int before = 0;                                     // workgroups of earlier batches
+    for (int base = 0; base < n_req; base += WAVE) {
+        const int r = base + lane;
+        const int t = r < n_req ? tiles_of(nsh[r]) : 0;
+        const int nw = (t + tpw - 1) / tpw;
+        int incl = nw;                                  // inclusive scan over the lanes
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const int y = __shfl_up(incl, o, WAVE);
+            if (lane >= o) incl += y;
+        }
+        const int in_batch = __shfl(incl, WAVE - 1, WAVE);
+        if (x < before + in_batch) {
+            const unsigned long long hit = __ballot(before + incl > x);
+            const int src = __ffsll((long long)hit) - 1;
+            const int excl = __shfl(incl - nw, src, WAVE);
+            const int tr = __shfl(t, src, WAVE);
+            w.req = base + src;
+            w.stride = __shfl(nw, src, WAVE);
+            w.first = x - before - excl;
+            w.count = (tr - w.first + w.stride - 1) / w.stride;
+            return true;
+        }
+        before += in_batch;
+    }
+    return false;
+}
+
+}  // namespace amass

@@ -14,7 +14,13 @@ launch stream; `cpu_baseline` times the CPU oracle (the numpy restatement of the
 reference's score / select / attend path) on a bounded sample of the same workload.
 Inputs are synthetic (amass.bench.synth, seeded) and resident in HBM before timing.
 
+Secondary lines (under "configs"; skipped with --quick): config 1 with the key-norm boost,
+config 2 (r8, 64 ragged sequences, 5 % budget), config 3 (G = 8, 131072 tokens, coverage
+0.95, split-K path) and config 4 (mem-v, 64 steps from a cold hot buffer, both boosts),
+each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s.
+
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--quick]
+                  [--configs 1k,2,3,4]
 """
 from __future__ import annotations
 
@@ -102,8 +108,20 @@ def quad_score_bytes(st, n_req, G):
     return units * (rec + out) + int(nsh.sum()) * 4 + n_req * st.n_kv * G * st.d * 2
 
 
+def r8_score_bytes(st, n_req, G):
+    """Algorithmic HBM bytes of one r8-score launch: per scored (page, kv-head) Vk
+    d*r*vb/8 + mu d + c page*r*cb/8 + Vk_scale 2r + mu_scale 2 + c_scale 2*page (1330 B
+    at r=8 int8), plus the block table, q and one score float per record."""
+    nsh = st.n_sel_hi[:n_req].clamp_min(0).long()
+    units = int(nsh.sum()) * st.n_kv
+    rec = (st.d * st.r * st.vk_bits // 8 + st.d + st.page * st.r * st.c_bits // 8
+           + 2 * st.r + 2 + 2 * st.page)
+    return units * (rec + 4) + int(nsh.sum()) * 4 + n_req * st.n_kv * G * st.d * 2
+
+
 def select_bytes(st, n_req, G):
-    """score_h read (G floats per record) + score write + page_table + page_cnt."""
+    """score_h read (G floats per record; G = 0 when the score is read instead) + score
+    write (or read) + page_table + page_cnt."""
     nsh = st.n_sel_hi[:n_req].clamp_min(0).long()
     units = int(nsh.sum()) * st.n_kv
     return units * (G * 4 + 4) + n_req * st.n_kv * st.max_pages * 4 + n_req * st.n_kv * 4
@@ -158,6 +176,208 @@ def cpu_baseline(case, st, budget_s=15.0):
                       f"coverage select, fp64 attend; numpy, 1 thread), scaled x{B / done:.1f}"}
 
 
+def kernel_entry(us, nbytes, traffic=None):
+    return dict(us=round(us, 2), bytes=nbytes, gbs=round(nbytes / us / 1e3, 1),
+                frac=round(nbytes / (us * 1e-6) / PEAK_HBM, 4), traffic=traffic)
+
+
+def free_gpu():
+    import gc
+
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def measure_step(case, st, args, *, score="quad", traffic=None):
+    """Time one layer's sparse decode step (score + select + attend, one HIP graph) and
+    the dense paged decode of the same batch, then each kernel alone (10 launches per
+    graph); returns the per-config result dict."""
+    import torch
+
+    from amass.attention.decode import (ResidentVSource, dense_paged_decode,
+                                        sparse_paged_decode_batched)
+    from amass.selection import derive_page_params, select_pages_quad, select_pages_r8
+    from amass.selection.quad_score import quad_score_launch
+    from amass.selection.score import r8_score
+    from amass.selection.select import select_pages
+
+    traffic = traffic or {}
+    B, G, n_kv = case.q.shape[0], case.G, case.n_kv
+    q, kv, bt, sl = case.q, case.kv_cache, case.block_table, case.seq_lens
+    derive_page_params(st, sl, B)
+    out = torch.zeros(B, n_kv * G, 128, dtype=torch.bfloat16, device=q.device)
+    out_d = torch.zeros_like(out)
+    vsrc = ResidentVSource(kv)
+    nrm = score == "quad" and st.combine == "nrm"
+
+    def stage_a():
+        if score == "quad":
+            select_pages_quad(st, 0, q, bt, sl, B, case.scale, derive=False)
+        else:
+            select_pages_r8(st, 0, q, bt, sl, B, case.scale, derive=False)
+
+    def sparse_step():
+        stage_a()
+        sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc, scale=case.scale)
+
+    def dense_step():
+        dense_paged_decode(q, kv, bt, sl, st, out_d, scale=case.scale)
+
+    def score_only():
+        if score == "quad":
+            quad_score_launch(st, 0, q, bt, B, case.scale)
+        else:
+            r8_score(st, 0, q, bt, sl, B, case.scale)
+
+    sparse_step()
+    dense_step()
+    torch.cuda.synchronize()
+    g_sparse = graph_of(sparse_step)
+    g_dense = graph_of(dense_step)
+    ms_sparse = time_graph(g_sparse, args.steps, args.warmup)
+    ms_dense = time_graph(g_dense, args.steps, args.warmup)
+    reps = 10
+    k_steps = max(5, args.steps // 5)
+    g_score = graph_of(score_only, reps)
+    us_score = time_graph(g_score, k_steps, 2, reps) * 1e3
+    g_sel = graph_of(lambda: select_pages(st, B, score_h=st.score_h if nrm else None), reps)
+    us_sel = time_graph(g_sel, k_steps, 2, reps) * 1e3
+    g_att = graph_of(lambda: sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc,
+                                                          scale=case.scale), reps)
+    us_att = time_graph(g_att, k_steps, 2, reps) * 1e3
+    torch.cuda.synchronize()
+    del g_sparse, g_dense, g_score, g_sel, g_att
+    cnt = st.page_cnt[:B]
+    S_all = (st.n_sel_hi[:B] - st.sink_pages).clamp_min(0).double()
+    frac = float(st.n_sel[:B].double().sum() / (S_all.sum() * n_kv))
+    att_frac = float(cnt.double().sum() / (st.n_pages[:B].double().sum() * n_kv))
+    b_score = (quad_score_bytes if score == "quad" else r8_score_bytes)(st, B, G)
+    b_sel = select_bytes(st, B, G if nrm else 0)
+    b_att = attend_bytes(cnt, B, n_kv, G)
+    b_dense = attend_bytes(st.n_pages[:B][:, None].expand(B, n_kv), B, n_kv, G)
+    sname = "quad_score" if score == "quad" else "r8_score"
+    kernels = {sname: kernel_entry(us_score, b_score, traffic.get(sname)),
+               ("select_nrm_coverage" if nrm else "select"):
+                   kernel_entry(us_sel, b_sel, traffic.get("select_nrm_coverage")),
+               "sparse_decode": kernel_entry(us_att, b_att, traffic.get("sparse_decode"))}
+    return dict(us=round(ms_sparse * 1e3, 2),
+                gb_s=round((b_score + b_sel + b_att) / (ms_sparse * 1e-3) / 1e9, 1),
+                dense_us=round(ms_dense * 1e3, 2),
+                dense_gb_s=round(b_dense / (ms_dense * 1e-3) / 1e9, 1),
+                speedup_vs_dense=round(ms_dense / ms_sparse, 3),
+                selected_fraction=round(frac, 4), attended_fraction=round(att_frac, 4),
+                kernels=kernels)
+
+
+def run_secondary(idx, args, boost="sigma"):
+    """A BASELINE configuration other than the headline, measured like config 1."""
+    from amass.bench.synth import CONFIGS, build_quad_state, build_r8_state, config_case
+
+    cfg = CONFIGS[idx]
+    t0 = time.time()
+    case = config_case(idx, seed=args.seed, device="cuda", boost=boost)
+    if cfg["score"] == "r8":
+        st = build_r8_state(case, rank=8, vk_bits=8, c_bits=8, budget=cfg["budget"])
+    else:
+        st = build_quad_state(case, rank=8, v_bits=8, combine="nrm",
+                              coverage=cfg["coverage"], budget=cfg["budget"] or 0.1)
+    log(f"config {idx} ({boost}): inputs + summaries {time.time() - t0:.1f}s")
+    res = measure_step(case, st, args, score=cfg["score"])
+    lens = case.seq_lens.long()
+    sel = (f"top-b {cfg['budget']:.0%}" if cfg["budget"] else f"coverage {cfg['coverage']}")
+    res["workload"] = (f"config{idx}: B={case.q.shape[0]} ctx "
+                       + (f"{int(lens.min())}..{int(lens.max())} (sum {int(lens.sum())})"
+                          if isinstance(cfg["ctx"], tuple) else f"{cfg['ctx']}")
+                       + f" G={case.G} {cfg['score']} r=8 int8, {sel}, boost {boost}")
+    log(f"config {idx}: sparse {res['us']} us, dense {res['dense_us']} us")
+    return res
+
+
+def run_config4(args, boost="sigma", steps=64):
+    """mem-v: V in the pinned, device-mapped host pool, a 10 % hot buffer, 64 decode steps
+    with fresh N(0, 1) queries over a fixed boosted page set.  Each step = quad score +
+    coverage select + residency plan + fetch + tiered decode (eager, one event pair around
+    the 64 steps, from a cold hot buffer).  Host bytes = miss pages x 4 KiB (each miss is
+    read over the host link once, into its slot or, when the buffer is exhausted, directly
+    by the decode)."""
+    import torch
+
+    from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
+    from amass.bench.synth import build_quad_state, config_case
+    from amass.selection import derive_page_params, select_pages_quad
+    from amass.tier import Tier, mem_dynamic_decode
+
+    t0 = time.time()
+    case = config_case(4, seed=args.seed, device="cuda", boost=boost)
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
+    B, G, n_kv, MP = case.q.shape[0], case.G, case.n_kv, case.max_pages
+    NB = case.kv_cache.shape[0]
+    slots = (B * MP) // 10
+    tier = Tier(num_layers=1, num_blocks=NB, n_kv=n_kv, page=16, d=128, hot_slots=slots,
+                max_reqs=B, max_pages=MP, device="cuda", v_blocks=4)
+    tier.flush_layer(0, case.kv_cache[:, 1])
+    log(f"config 4 ({boost}): inputs, summaries, pinned pool {time.time() - t0:.1f}s")
+    bt, sl = case.block_table, case.seq_lens
+    derive_page_params(st, sl, B)
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 404)
+    qs = [torch.randn(B, n_kv * G, 128, generator=gen, device="cuda").to(torch.bfloat16)
+          for _ in range(steps)]
+    out = torch.zeros(B, n_kv * G, 128, dtype=torch.bfloat16, device="cuda")
+    r5 = tier.residency
+
+    def cold():
+        r5.page2slot.fill_(-1)
+        r5.slot2page.fill_(-1)
+        r5.lru_clock.zero_()
+        r5.clock.fill_(1)
+        r5.overflow.zero_()
+
+    def one(qt):
+        select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
+        mem_dynamic_decode(qt, case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale,
+                           fetch="kernel")
+
+    # pass 1 (statistics, host reads between steps), pass 2 (timed), both from cold
+    cold()
+    sel = miss = 0
+    for qt in qs:
+        one(qt)
+        sel += int(st.page_cnt[:B].sum())
+        miss += int(r5.miss_cnt[:B].sum())
+    cold()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for qt in qs:
+        one(qt)
+    b.record()
+    torch.cuda.synchronize()
+    us_step = a.elapsed_time(b) / steps * 1e3
+    # the same steps with V resident in HBM (graph per step is not needed: eager, same loop)
+    vsrc = ResidentVSource(case.kv_cache)
+    a.record()
+    for qt in qs:
+        select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
+        sparse_paged_decode_batched(qt, case.kv_cache, bt, sl, st, out, vsrc, scale=case.scale)
+    b.record()
+    torch.cuda.synchronize()
+    us_res = a.elapsed_time(b) / steps * 1e3
+    host_bytes = miss * 16 * 128 * 2 / steps
+    res = dict(workload=f"config4: mem-v B={B} ctx 32768 quad r'=8 int8 nrm coverage 0.95, "
+                        f"hot buffer {slots} slots per kv head (10 %), {steps} steps, fresh "
+                        f"N(0,1) queries, boost {boost}",
+               us_per_step=round(us_step, 1), resident_us_per_step=round(us_res, 1),
+               hit_rate=round(1.0 - miss / max(sel, 1), 4),
+               selected_pages_per_step=round(sel / steps, 1),
+               host_bytes_per_step=int(host_bytes),
+               host_link_gb_s=round(host_bytes / (us_step * 1e-6) / 1e9, 2))
+    log(f"config 4 ({boost}): {us_step:.1f} us/step (resident {us_res:.1f}), "
+        f"hit rate {res['hit_rate']}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,6 +387,8 @@ def main():
     ap.add_argument("--boost", default="sigma", choices=["sigma", "keynorm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
+    ap.add_argument("--configs", default="1k,2,3,4",
+                    help="secondary lines: 1k (config 1 with the key-norm boost), 2, 3, 4")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB read + 256 MiB write kernel (HBM counter calibration)")
     args = ap.parse_args()
@@ -178,12 +400,8 @@ def main():
 
     import torch
 
-    from amass.attention.decode import (ResidentVSource, dense_paged_decode,
-                                        sparse_paged_decode_batched)
     from amass.bench.synth import build_quad_state, config_case
-    from amass.selection import derive_page_params, select_pages_quad
-    from amass.selection.quad_score import quad_score_launch
-    from amass.selection.select import select_pages
+    from amass.selection import derive_page_params
 
     dev = "cuda"
     if args.copy_calibration:
@@ -199,74 +417,23 @@ def main():
     log(f"inputs generated ({time.time() - t0:.1f}s)")
     st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
     log(f"quad summaries built ({time.time() - t0:.1f}s)")
-    B, G, n_kv = case.q.shape[0], case.G, case.n_kv
-    q, kv, bt, sl = case.q, case.kv_cache, case.block_table, case.seq_lens
-    derive_page_params(st, sl, B)
-    out = torch.zeros(B, n_kv * G, 128, dtype=torch.bfloat16, device=dev)
-    out_d = torch.zeros_like(out)
-    vsrc = ResidentVSource(kv)
-
-    def sparse_step():
-        select_pages_quad(st, 0, q, bt, sl, B, case.scale, derive=False)
-        sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc, scale=case.scale)
-
-    def dense_step():
-        dense_paged_decode(q, kv, bt, sl, st, out_d, scale=case.scale)
-
-    sparse_step()
-    dense_step()
-    torch.cuda.synchronize()
-    g_sparse = graph_of(sparse_step)
-    g_dense = graph_of(dense_step)
-    ms_sparse = time_graph(g_sparse, args.steps, args.warmup)
-    ms_dense = time_graph(g_dense, args.steps, args.warmup)
-    log(f"sparse {ms_sparse * 1e3:.1f} us, dense {ms_dense * 1e3:.1f} us")
-
-    # ---- per-kernel durations (each kernel repeated inside one graph) ----------------
-    reps = 10
-    k_steps = max(5, args.steps // 5)
-    g_score = graph_of(lambda: quad_score_launch(st, 0, q, bt, B, case.scale), reps)
-    us_score = time_graph(g_score, k_steps, 2, reps) * 1e3
-    g_sel = graph_of(lambda: select_pages(st, B, score_h=st.score_h), reps)
-    us_sel = time_graph(g_sel, k_steps, 2, reps) * 1e3
-    g_att = graph_of(lambda: sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc,
-                                                          scale=case.scale), reps)
-    us_att = time_graph(g_att, k_steps, 2, reps) * 1e3
-    torch.cuda.synchronize()
-    cnt = st.page_cnt[:B]
-    nsel = st.n_sel[:B].double()
-    S_all = (st.n_sel_hi[:B] - st.sink_pages).clamp_min(0).double()
-    frac = float(nsel.sum() / (S_all.sum() * n_kv))
-    att_frac = float(cnt.double().sum() / (st.n_pages[:B].double().sum() * n_kv))
-    b_score = quad_score_bytes(st, B, G)
-    b_sel = select_bytes(st, B, G)
-    b_att = attend_bytes(cnt, B, n_kv, G)
-    b_dense = attend_bytes(st.n_pages[:B][:, None].expand(B, n_kv), B, n_kv, G)
-    kernels = {
-        "quad_score": dict(us=round(us_score, 2), bytes=b_score,
-                           gbs=round(b_score / us_score / 1e3, 1)),
-        "select_nrm_coverage": dict(us=round(us_sel, 2), bytes=b_sel,
-                                    gbs=round(b_sel / us_sel / 1e3, 1)),
-        "sparse_decode": dict(us=round(us_att, 2), bytes=b_att,
-                              gbs=round(b_att / us_att / 1e3, 1)),
-    }
+    B = case.q.shape[0]
     traffic = profiled_traffic()
-    for k, v in kernels.items():
-        v["traffic"] = traffic.get(k)
+    m = measure_step(case, st, args, score="quad", traffic=traffic)
+    log(f"sparse {m['us']} us, dense {m['dense_us']} us")
+    kernels = m["kernels"]
     dom = max(kernels, key=lambda k: kernels[k]["us"])
     dk = kernels[dom]
-    roof = {"bound": "hbm", "kernel": dom, "achieved": round(dk["bytes"] / dk["us"] / 1e3, 1),
-            "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(dk["bytes"] / (dk["us"] * 1e-6) / PEAK_HBM, 4),
+    roof = {"bound": "hbm", "kernel": dom, "achieved": dk["gbs"],
+            "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": dk["frac"],
             "traffic": traffic.get(dom),
             "traffic_source": "profiles/hbm_traffic_config1.txt: rocprofv3 FETCH_SIZE x2.000 "
                               "+ WRITE_SIZE x1.000 (scales from a 256 MiB neg kernel)"
             if dom in traffic else None}
-    total_bytes = b_score + b_sel + b_att
     res = {
         "metric": "sparse decode attn us/layer + HBM GB/s at B=32 ctx16k; speedup vs dense paged",
-        "value": round(ms_sparse * 1e3, 2), "unit": "us/layer", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_sparse, 5),
+        "value": m["us"], "unit": "us/layer", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(m["us"] / 1e3, 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 score / bf16 attention", "data": "synthetic",
         "config": {"workload": "config1: B=32 ctx16384 llama3.1-8B GQA (32q/8kv, d128), "
@@ -274,31 +441,57 @@ def main():
                                "coverage 0.95, one layer",
                    "boost": f"{args.boost} (beta={case.meta['beta']:.3f})",
                    "graph": "hipGraph replay of score+select+attend"},
-        "gb_s": round(total_bytes / (ms_sparse * 1e-3) / 1e9, 1),
-        "dense_us": round(ms_dense * 1e3, 2),
-        "dense_gb_s": round(b_dense / (ms_dense * 1e-3) / 1e9, 1),
-        "speedup_vs_dense": round(ms_dense / ms_sparse, 3),
-        "selected_fraction": round(frac, 4), "attended_fraction": round(att_frac, 4),
+        "gb_s": m["gb_s"], "dense_us": m["dense_us"], "dense_gb_s": m["dense_gb_s"],
+        "speedup_vs_dense": m["speedup_vs_dense"],
+        "selected_fraction": m["selected_fraction"],
+        "attended_fraction": m["attended_fraction"],
         "kernels": kernels,
         "roofline": roof,
     }
     if not args.quick:
         # secondary: fixed 5% budget at the same shape (same summaries, top-b selection)
+        from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
+        from amass.selection import select_pages_quad
         st.coverage = None
         st.budget = 0.05
-        derive_page_params(st, sl, B)
-        g_b = graph_of(sparse_step)
+        derive_page_params(st, case.seq_lens, B)
+        out = torch.zeros(B, case.n_kv * case.G, 128, dtype=torch.bfloat16, device=dev)
+        vs = ResidentVSource(case.kv_cache)
+
+        def step5():
+            select_pages_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                              derive=False)
+            sparse_paged_decode_batched(case.q, case.kv_cache, case.block_table,
+                                        case.seq_lens, st, out, vs, scale=case.scale)
+        g_b = graph_of(step5)
         ms_b = time_graph(g_b, args.steps, args.warmup)
         res["fixed_budget_5pct"] = {"us": round(ms_b * 1e3, 2),
-                                    "speedup_vs_dense": round(ms_dense / ms_b, 3)}
-        st.coverage = 0.95
-        derive_page_params(st, sl, B)
-        torch.cuda.synchronize()
+                                    "speedup_vs_dense": round(m["dense_us"] / (ms_b * 1e3), 3)}
         del g_b
+        st.coverage = 0.95
+        derive_page_params(st, case.seq_lens, B)
+        torch.cuda.synchronize()
     if not args.no_cpu_baseline:
-        sparse_step()
+        from amass.selection import select_pages_quad
+        select_pages_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                          derive=False)
         torch.cuda.synchronize()
         res["cpu_baseline"] = cpu_baseline(case, st)
+    if not args.quick:
+        del case, st
+        free_gpu()
+        sec = {}
+        for c in [x.strip() for x in args.configs.split(",") if x.strip()]:
+            if c == "1k":
+                sec["config1_keynorm"] = run_secondary(1, args, boost="keynorm")
+            elif c in ("2", "3"):
+                sec[f"config{c}"] = run_secondary(int(c), args)
+            elif c == "4":
+                sec["config4_memv"] = run_config4(args, "sigma")
+                free_gpu()
+                sec["config4_memv_keynorm"] = run_config4(args, "keynorm")
+            free_gpu()
+        res["configs"] = sec
     print(json.dumps(res), flush=True)
 
 

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 1
+#define AMASS_ABI_VERSION 2
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -73,15 +73,25 @@ int amass_quad_score(const amass_quad_score_args* a, void* stream);
 /* Replaces selection/score.py:123-148 (Triton golden) and selection/score_cuda.py:888-913.
  *   q~[g,k] = (Vk_code[:,k] Vk_scale[k]) . q_g ; tok[g,t] = s * c_scale[t] * (c_code[t,:] . q~[g])
  *   S_g = s * mu.q_g + logsumexp_{t : 16p+t < seq_len} tok[g,t] ; score = max_g S_g
- * comb_out (optional) receives the exact int32 sums sum_d qi*code for the r columns and mu. */
+ * comb_out (optional) receives the exact int32 sums sum_d qi*code for the r columns and mu.
+ *
+ * Summary records.  The reference's six per-(block, kv-head) slabs (r8_mu, mu_scale, r8_Vk,
+ * Vk_scale, r8_c, c_scale; selection/state.py:35-112) are packed per block,
+ * AMASS_R8_REC_BYTES(rank, vk_bits, c_bits) bytes per kv head (VM of them first, in head
+ * order, then 64 per head):
+ *   head h at h*VM:         r8_Vk column-major, column k = CB bytes; int8 CB = 128 (byte j =
+ *                           code[j]); int4 CB = 64 (byte j = code[j] | code[j+64] << 4),
+ *                           then r8_mu (128 int8), then r8_c: 16 token rows of r*c_bits/8
+ *                           bytes (int4: two columns per byte, low nibble = even column)
+ *   at n_kv*VM + 64*h:      fp16 halves: Vk_scale[0..r), c_scale[0..16) at half 8,
+ *                           mu_scale at half 24
+ * VM = r*CB + 128 + 16*r*c_bits/8.  rec_sb (bytes between blocks) >= n_kv * REC_BYTES, a
+ * multiple of 16.  rank 4 or 8; G 1, 2, 4 or 8; n_kv <= 8 or a multiple of 8. */
+#define AMASS_R8_REC_BYTES(rank, vk_bits, c_bits) \
+    ((rank) * ((vk_bits) == 8 ? 128 : 64) + 128 + 2 * (rank) * (c_bits) + 64)
 typedef struct amass_r8_score_args {
     const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
-    const int8_t*  mu;       int64_t mu_sb;          /* (NB,n_kv,d) int8                */
-    const void*    mu_scale; int64_t mus_sb;         /* (NB,n_kv) fp16                  */
-    const int8_t*  vk;       int64_t vk_sb;          /* (NB,n_kv,d,r) int8 | (..,r/2) int4 */
-    const void*    vk_scale; int64_t vks_sb;         /* (NB,n_kv,r) fp16                */
-    const int8_t*  c;        int64_t c_sb;           /* (NB,n_kv,page,r) int8 | (..,r/2) */
-    const void*    c_scale;  int64_t cs_sb;          /* (NB,n_kv,page) fp16             */
+    const int8_t*  rec;      int64_t rec_sb;         /* (NB,n_kv,REC) summary records   */
     const int32_t* block_table; int64_t bt_st;
     const int32_t* seq_lens;                         /* (R,) int32                      */
     const int32_t* n_sel_hi;                         /* (R,) int32                      */

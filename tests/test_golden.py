@@ -106,9 +106,8 @@ def test_gpu_r8_fixture():
     MP = inp["block_table"].shape[1]
     st = R8State(DEV, num_layers=1, num_blocks=NB, n_kv=n_kv, G=H // n_kv, head_dim=d,
                  page=16, max_reqs=R, max_pages=MP, rank=8)
-    for name, key in (("r8_mu", "mu"), ("mu_scale", "mu_scale"), ("r8_Vk", "Vk"),
-                      ("Vk_scale", "Vk_scale"), ("r8_c", "c"), ("c_scale", "c_scale")):
-        getattr(st, name)[0].copy_(_t(inp[key]))
+    st.load_reference(0, *(_t(inp[k]) for k in ("mu", "mu_scale", "Vk", "Vk_scale", "c",
+                                                 "c_scale")))
     st.n_sel_hi.copy_(_t(inp["n_sel_hi"]))
     r8_score(st, 0, _t(inp["q"], torch.bfloat16), _t(inp["block_table"]), _t(inp["seq_lens"]),
              R, 1 / np.sqrt(128))

@@ -68,7 +68,8 @@ def test_config2_r8_ragged():
     r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
     select_pages(st, B)
     torch.cuda.synchronize()
-    mu, mus, Vk, Vks, c, cs, _ = st.layer_state(0)
+    mu, mus, _, Vks, c, cs, _ = st.layer_state(0)
+    Vk = st.reference_Vk(0)
     nsh = npi(st.n_sel_hi)
     rows = [0, 1, 4]
     sub = lambda t: npi(t)  # noqa: E731

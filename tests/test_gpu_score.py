@@ -108,20 +108,26 @@ def test_quad_padded_rows_untouched():
     assert bool((st.score[2] == 123.0).all())
 
 
-@pytest.mark.parametrize("vk_bits,c_bits", [(8, 8), (4, 4), (8, 4)])
-@pytest.mark.parametrize("G", [4, 8])
-def test_r8_comb_exact_and_scores(vk_bits, c_bits, G):
-    announce(f"r8 vk={vk_bits} c={c_bits} G={G}")
-    case = make_case(B=3, ctx=(300, 1400), n_kv=8, G=G, seed=11)
-    st = build_r8_state(case, vk_bits=vk_bits, c_bits=c_bits)
+R8_CASES = ([(8, vb, cb, G) for vb in (8, 4) for cb in (8, 4) for G in (1, 2, 4, 8)]
+            + [(4, vb, cb, G) for vb in (8, 4) for cb in (8, 4) for G in (2, 4)])
+
+
+@pytest.mark.parametrize("rank,vk_bits,c_bits,G", R8_CASES)
+def test_r8_comb_exact_and_scores(rank, vk_bits, c_bits, G):
+    """Every (rank, Vk bits, c bits) record layout and every token split of the kernel
+    (G = 8: 16 tokens per lane, G = 4: 8, G <= 2: 4, with 8-byte c rows at r = 4 int4)."""
+    announce(f"r8 rank={rank} vk={vk_bits} c={c_bits} G={G}")
+    case = make_case(B=3, ctx=(300, 1400), n_kv=8, G=G, seed=11 + G + rank)
+    st = build_r8_state(case, rank=rank, vk_bits=vk_bits, c_bits=c_bits)
     to_device(st, DEV)
     case_to(case, DEV)
     B, MP = 3, st.max_pages
     derive_page_params(st, case.seq_lens, B)
-    comb = torch.zeros(B, 8, MP, G, 9, dtype=torch.int32, device=DEV)
+    comb = torch.zeros(B, 8, MP, G, rank + 1, dtype=torch.int32, device=DEV)
     r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
     torch.cuda.synchronize()
-    mu, mus, Vk, Vks, c, cs, _ = st.layer_state(0)
+    mu, mus, _, Vks, c, cs, _ = st.layer_state(0)
+    Vk = st.reference_Vk(0)
     nsh = npi(st.n_sel_hi)
     ref_comb = osc.r8_comb(npf(case.q), npi(mu), npi(Vk), npi(case.block_table), nsh, G=G,
                            vk_bits=vk_bits, max_pages=MP)
@@ -132,7 +138,14 @@ def test_r8_comb_exact_and_scores(vk_bits, c_bits, G):
     ref = osc.r8_score(npf(case.q), npi(mu), npf(mus), npi(Vk), npf(Vks), npi(c), npf(cs),
                        npi(case.block_table), npi(case.seq_lens), nsh, scale=case.scale,
                        page=16, G=G, vk_bits=vk_bits, c_bits=c_bits, max_pages=MP)
+    # the production instance (no comb_out) writes the same scores
+    sc_comb = npf(st.score).copy()
+    r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale)
+    torch.cuda.synchronize()
     sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert rel_close(sc[r, :, :n], sc_comb[r, :, :n], 1) <= 1e-6
     for r in range(B):
         n = int(nsh[r])
         assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3

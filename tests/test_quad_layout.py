@@ -46,3 +46,50 @@ def test_state_load_reference_round_trip():
                       np.ones((5, 2, 4), np.float16))
     assert np.array_equal(st.reference_V(1).numpy(), V)
     assert not st.quad_V[0].any()
+
+
+@pytest.mark.parametrize("vk_bits,c_bits,r", [(8, 8, 8), (4, 4, 8), (8, 4, 4), (4, 8, 4)])
+def test_r8_record_positions(vk_bits, c_bits, r):
+    """The packed r8 record (include/amass_hip.h, AMASS_R8_REC_BYTES): per block the n_kv
+    heads' [Vk column-major | mu | c rows], then 64-byte fp16 scale blocks with Vk_scale
+    at half 0, c_scale at halves 8..23, mu_scale at half 24.  Bytes are checked at their
+    documented offsets in the raw buffer, so a view that drifts from the kernel's
+    addressing fails here."""
+    from amass.selection import R8State
+    n_kv, NB = 2, 3
+    st = R8State("cpu", num_layers=1, num_blocks=NB, n_kv=n_kv, G=4, head_dim=128, page=16,
+                 max_reqs=1, max_pages=4, rank=r, vk_bits=vk_bits, c_bits=c_bits)
+    cb = 128 if vk_bits == 8 else 64
+    crow = r * c_bits // 8
+    vm = r * cb + 128 + 16 * crow
+    rec_bytes = r * cb + 128 + 2 * r * c_bits + 64          # AMASS_R8_REC_BYTES
+    assert st.rec_bytes == rec_bytes == vm + 64 and st.r8_rec.shape[-1] == n_kv * rec_bytes
+    rng = np.random.default_rng(r + vk_bits)
+    lv = 127 if vk_bits == 8 else 7
+    vcode = rng.integers(-lv, lv + 1, (NB, n_kv, 128, r)).astype(np.int8)
+    Vk = vcode if vk_bits == 8 else oq.pack_i4(vcode)
+    lc = 127 if c_bits == 8 else 7
+    ccode = rng.integers(-lc, lc + 1, (NB, n_kv, 16, r)).astype(np.int8)
+    c = ccode if c_bits == 8 else oq.pack_i4(ccode)
+    mu = rng.integers(-127, 128, (NB, n_kv, 128)).astype(np.int8)
+    mus = rng.random((NB, n_kv)).astype(np.float16)
+    vks = rng.random((NB, n_kv, r)).astype(np.float16)
+    cs = rng.random((NB, n_kv, 16)).astype(np.float16)
+    st.load_reference(0, mu, mus, Vk, vks, c, cs)
+    assert np.array_equal(st.reference_Vk(0).numpy(), Vk)
+    raw = st.r8_rec[0].numpy().view(np.uint8)               # (NB, n_kv * REC)
+    b, h, k, j, t = 2, 1, r - 1, 77, 13
+    base = h * vm
+    if vk_bits == 8:
+        assert raw[b, base + k * cb + j].view(np.int8) == vcode[b, h, j, k]
+    else:
+        byte = int(raw[b, base + k * cb + 13])
+        lo, hi = byte & 0xF, byte >> 4
+        assert (lo - 16 if lo >= 8 else lo) == vcode[b, h, 13, k]
+        assert (hi - 16 if hi >= 8 else hi) == vcode[b, h, 13 + 64, k]
+    assert raw[b, base + r * cb + j].view(np.int8) == mu[b, h, j]
+    crow_bytes = raw[b, base + r * cb + 128 + t * crow: base + r * cb + 128 + (t + 1) * crow]
+    assert np.array_equal(crow_bytes.view(np.int8), c[b, h, t])
+    meta = raw[b, n_kv * vm + 64 * h: n_kv * vm + 64 * (h + 1)].view(np.float16)
+    assert np.array_equal(meta[:r], vks[b, h]) and np.array_equal(meta[8:24], cs[b, h])
+    assert meta[24] == mus[b, h] and not meta[25:].any()
