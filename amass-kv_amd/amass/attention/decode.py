@@ -4,8 +4,10 @@ Same contract as the reference ``sparse_paged_decode_batched`` (attention/decode
 247-304): consumes st.page_table / st.page_cnt and writes rows [0, n_req) of ``out``
 (T, H, d) in place, reading K from the resident paged cache and V through an injected
 V source (the fast / mem-v seam, attention/decode.py:44-95).  No allocation, no host
-sync.  ``path``: "split" (split-K partials + LSE merge), "fused" (one launch, page stripes
-merged through LDS), "auto" (fused when n_req * n_kv fills the GPU).
+sync.  Each (request, kv-head) unit gets S workgroups whose waves merge through LDS;
+with S > 1 they write split-K partials and a second launch does the LSE merge.  ``path``: "split" (S up to
+the partial capacity, at least 8 * pps_min pages per workgroup), "fused" (S = 1),
+"auto" (S sized so the units fill the GPU).
 ``dense_paged_decode`` attends every page of every request (the dense baseline).
 """
 from __future__ import annotations
@@ -71,7 +73,8 @@ def ensure_stage_b_buffers(st, device, split: int = SPLIT) -> None:
 
 
 def _pps_min(n_req: int) -> int:
-    """Minimum pages per split: fewer, fatter splits once the batch fills the GPU."""
+    """Minimum pages per wave of a split workgroup (8 waves): fewer, fatter splits once
+    the batch fills the GPU."""
     return 4 if n_req == 1 else 8
 
 

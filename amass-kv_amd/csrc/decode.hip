@@ -20,14 +20,22 @@
 // vector load per wave (broadcast with readlane); the next page's loads are issued before
 // the current page is computed; the accumulator rescale is skipped when no row max moved
 // (alpha == 1 exactly).
+//
+// Workgroups.  A unit (request, kv-head) gets S workgroups of 8 waves (S = 1 when the
+// units alone fill the GPU, e.g. 32 requests x 8 heads; more for few, long units); wave
+// w of workgroup s attends pages s*8 + w, s*8 + w + 8S, ...  The 8 waves merge their
+// online-softmax states through LDS.  With S = 1 that is the output (the fused single
+// pass).  With S > 1 each workgroup writes one LSE partial (the split-K partial of
+// attention/decode.py:146-241) and a second launch, one workgroup per unit, merges the
+// S partials (attention/merge.py:21-50); a cross-workgroup ticket in one launch was
+// measured slower, its device-scope fences write back and invalidate the XCD's L2.
 #include "common.h"
 
 namespace amass {
 
 constexpr int DEC_D = 128;
 constexpr int DEC_PAGE = 16;
-constexpr int SPLIT_WAVES = 4;
-constexpr int FUSED_WAVES = 8;
+constexpr int DEC_WAVES = 8;      // waves per workgroup
 
 struct PageData {
     uint4 kq[4];          // K[t = l%16][d = 32 i2 + 8 (l/16) .. +8]
@@ -214,88 +222,36 @@ __device__ __forceinline__ int unit_count(const amass_decode_args& a, int r, int
     return a.page_cnt[(int64_t)r * a.pc_sr + kh];
 }
 
-// ------------------------------------------------------------------ split-K
-template <int VSRC, bool DENSE>
-__global__ __launch_bounds__(SPLIT_WAVES * WAVE) void decode_split_kernel(const amass_decode_args a) {
-    const int lane = threadIdx.x & 63;
-    const int sp = blockIdx.x * SPLIT_WAVES + (threadIdx.x >> 6);
-    const int kh = blockIdx.y, r = blockIdx.z;
-    if (sp >= a.split) return;
-    const int sl = a.seq_lens[r];
-    const int cnt = unit_count<DENSE>(a, r, kh, sl);
-    const int pps = max((cnt + a.split - 1) / a.split, a.pps_min);
-    const int j0 = sp * pps;
-    if (j0 >= cnt) return;
-    const int j1 = min(j0 + pps, cnt);
-    bf16x4_t qb[8];
-    load_q(a, r, kh, lane, qb);
-    WaveState st;
-    init_state(st);
-    attend_run<VSRC, DENSE>(a, r, kh, sl, j0, j1, 1, lane, qb, st);
-    float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
-    lt += __shfl_xor(lt, 32, WAVE);
-    const int64_t base = (((int64_t)r * a.n_kv + kh) * a.split + sp) * a.G;
-    if (lane < a.G) {
-        a.m_part[base + lane] = st.m;
-        a.l_part[base + lane] = lt;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int g = 4 * (lane >> 4) + j;
-        if (g < a.G) {
-            float* dst = a.acc_part + (base + g) * DEC_D + 8 * (lane & 15);
-            *reinterpret_cast<float4*>(dst) =
-                make_float4(st.acc[0][j], st.acc[1][j], st.acc[2][j], st.acc[3][j]);
-            *reinterpret_cast<float4*>(dst + 4) =
-                make_float4(st.acc[4][j], st.acc[5][j], st.acc[6][j], st.acc[7][j]);
-        }
-    }
+// ------------------------------------------------------------------ decode
+// Workgroups of a unit that carry pages: at least 8 * pps_min pages each, at most S.
+__device__ __forceinline__ int unit_workgroups(int cnt, int S, int pps_min) {
+    const int per = DEC_WAVES * pps_min;
+    const int want = (cnt + per - 1) / per;
+    return max(1, min(S, want));
 }
 
-template <bool DENSE>
-__global__ __launch_bounds__(WAVE) void merge_kernel(const amass_decode_args a) {
-    const int lane = threadIdx.x;
-    const int h = blockIdx.x, r = blockIdx.y;
-    const int kh = h / a.G, g = h % a.G;
-    const int sl = a.seq_lens[r];
-    const int cnt = unit_count<DENSE>(a, r, kh, sl);
-    const int pps = max((cnt + a.split - 1) / a.split, a.pps_min);
-    const int nact = cnt > 0 ? (cnt + pps - 1) / pps : 0;
-    const int64_t base = ((int64_t)r * a.n_kv + kh) * a.split * a.G + g;
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < nact; ++s2) M = fmaxf(M, a.m_part[base + (int64_t)s2 * a.G]);
-    float lt = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int s2 = 0; s2 < nact; ++s2) {
-        const int64_t idx = base + (int64_t)s2 * a.G;
-        const float ls = a.l_part[idx];
-        const float w = ls > 0.f ? __expf(a.m_part[idx] - M) : 0.f;
-        lt += ls * w;
-        const float2 v = *reinterpret_cast<const float2*>(a.acc_part + idx * DEC_D + 2 * lane);
-        o0 += v.x * w;
-        o1 += v.y * w;
-    }
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
-                                                (int64_t)h * a.o_hs + 2 * lane);
-    *out = pack_bf16x2(o0 * inv, o1 * inv);
-}
-
-// ------------------------------------------------------------------ fused
+// One workgroup = DEC_WAVES waves over the page stripe j = s*8 + w (mod 8 * S_eff) of
+// unit (r = blockIdx.z, kh = blockIdx.y); the waves' online-softmax states merge through
+// LDS.  S_eff = 1: normalise and write out.  S_eff > 1: write the workgroup's LSE
+// partial for merge_kernel.
 template <int VSRC, bool DENSE>
-__global__ __launch_bounds__(FUSED_WAVES * WAVE) void decode_fused_kernel(const amass_decode_args a) {
-    __shared__ float sm_m[FUSED_WAVES][8];
-    __shared__ float sm_l[FUSED_WAVES][8];
-    __shared__ float sm_acc[FUSED_WAVES][8][DEC_D];
+__global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_decode_args a) {
+    __shared__ float sm_m[DEC_WAVES][8];
+    __shared__ float sm_l[DEC_WAVES][8];
+    __shared__ float sm_acc[DEC_WAVES][8][DEC_D];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int kh = blockIdx.x, r = blockIdx.y;
+    const int s = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int sl = a.seq_lens[r];
     const int cnt = unit_count<DENSE>(a, r, kh, sl);
+    const int S = unit_workgroups(cnt, a.split, a.pps_min);
+    if (s >= S) return;
     WaveState st;
     init_state(st);
-    if (w < cnt) {
+    const int j0 = s * DEC_WAVES + w;
+    if (j0 < cnt) {
         bf16x4_t qb[8];
         load_q(a, r, kh, lane, qb);
-        attend_run<VSRC, DENSE>(a, r, kh, sl, w, cnt, FUSED_WAVES, lane, qb, st);
+        attend_run<VSRC, DENSE>(a, r, kh, sl, j0, cnt, DEC_WAVES * S, lane, qb, st);
     }
     float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
     lt += __shfl_xor(lt, 32, WAVE);
@@ -312,25 +268,120 @@ __global__ __launch_bounds__(FUSED_WAVES * WAVE) void decode_fused_kernel(const 
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < a.G * (DEC_D / 2); idx += blockDim.x) {
+    // merge the waves: (M, L, sum_w wt acc_w) per (g, d pair)
+    const int64_t ubase = ((int64_t)r * a.n_kv + kh) * a.split;   // partial slots of the unit
+    const int items = a.G * (DEC_D / 2);
+    for (int idx = threadIdx.x; idx < items; idx += blockDim.x) {
         const int g = idx / (DEC_D / 2), d = 2 * (idx % (DEC_D / 2));
         float M = -INFINITY;
 #pragma unroll
-        for (int x = 0; x < FUSED_WAVES; ++x) M = fmaxf(M, sm_m[x][g]);
+        for (int x = 0; x < DEC_WAVES; ++x) M = fmaxf(M, sm_m[x][g]);
         float lsum = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-        for (int x = 0; x < FUSED_WAVES; ++x) {
+        for (int x = 0; x < DEC_WAVES; ++x) {
             const float ls = sm_l[x][g];
             const float wt = ls > 0.f ? __expf(sm_m[x][g] - M) : 0.f;
             lsum += ls * wt;
             o0 += sm_acc[x][g][d] * wt;
             o1 += sm_acc[x][g][d + 1] * wt;
         }
+        if (S == 1) {
+            const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+            uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
+                                                        (int64_t)(kh * a.G + g) * a.o_hs + d);
+            *out = pack_bf16x2(o0 * inv, o1 * inv);
+        } else {
+            const int64_t pg = (ubase + s) * a.G + g;
+            *reinterpret_cast<float2*>(a.acc_part + pg * DEC_D + d) = make_float2(o0, o1);
+            if (d == 0) {
+                a.m_part[pg] = M;
+                a.l_part[pg] = lsum;
+            }
+        }
+    }
+}
+
+// LSE merge of the split-K partials of unit (kh = blockIdx.x, r = blockIdx.y): m* = max
+// m_s over the non-empty partials, w_s = exp(m_s - m*), out = sum w_s acc_s / sum w_s l_s
+// (attention/merge.py:21-50).  Units the decode served with one workgroup (S_eff = 1)
+// were written directly and are skipped.
+__global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a) {
+    const int kh = blockIdx.x, r = blockIdx.y;
+    const int sl = a.seq_lens[r];
+    const int cnt = a.dense ? (sl > 0 ? (sl + DEC_PAGE - 1) / DEC_PAGE : 0)
+                            : a.page_cnt[(int64_t)r * a.pc_sr + kh];
+    const int S = unit_workgroups(cnt, a.split, a.pps_min);
+    if (S <= 1) return;
+    const int64_t ubase = ((int64_t)r * a.n_kv + kh) * a.split;
+    for (int idx = threadIdx.x; idx < a.G * (DEC_D / 2); idx += blockDim.x) {
+        const int g = idx / (DEC_D / 2), d = 2 * (idx % (DEC_D / 2));
+        float M = -INFINITY;
+#pragma unroll 4
+        for (int x = 0; x < S; ++x) {
+            const int64_t pg = (ubase + x) * a.G + g;
+            if (a.l_part[pg] > 0.f) M = fmaxf(M, a.m_part[pg]);
+        }
+        float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll 4
+        for (int x = 0; x < S; ++x) {
+            const int64_t pg = (ubase + x) * a.G + g;
+            const float ls = a.l_part[pg];
+            const float wt = ls > 0.f ? __expf(a.m_part[pg] - M) : 0.f;
+            const float2 v = *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + d);
+            lsum += ls * wt;
+            o0 += v.x * wt;
+            o1 += v.y * wt;
+        }
         const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
         uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
                                                     (int64_t)(kh * a.G + g) * a.o_hs + d);
         *out = pack_bf16x2(o0 * inv, o1 * inv);
     }
+}
+
+// Workgroups of the decode kernel resident per CU (queried once per instance).
+template <int VSRC, bool DENSE>
+static int decode_resident(int& cus) {
+    static int per_cu = 0, ncu = 0;
+    if (per_cu == 0) {
+        int dev = 0, p = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&p, decode_kernel<VSRC, DENSE>,
+                                                         DEC_WAVES * WAVE, 0) != hipSuccess ||
+            p < 1) {
+            cus = 256;
+            return 1;
+        }
+        ncu = n;
+        per_cu = p;
+    }
+    cus = ncu;
+    return per_cu;
+}
+
+template <int VSRC, bool DENSE>
+static int launch_decode(amass_decode_args a, int path, hipStream_t s) {
+    int S = 1;
+    if (path == 1) {
+        S = a.split;
+    } else if (path == 0) {
+        // one resident round of workgroups over the units
+        int cus = 0;
+        const int resident = decode_resident<VSRC, DENSE>(cus) * cus;
+        const int units = a.n_req * a.n_kv;
+        S = (resident + units - 1) / units;
+        S = S < a.split ? S : a.split;
+        S = S < 1 ? 1 : S;
+    }
+    if (S > 1 && (!a.m_part || !a.l_part || !a.acc_part)) return AMASS_ERR_NULL;
+    a.split = S;
+    hipLaunchKernelGGL((decode_kernel<VSRC, DENSE>), dim3(S, a.n_kv, a.n_req),
+                       dim3(DEC_WAVES * WAVE), 0, s, a);
+    int rc = check_launch();
+    if (rc || S == 1) return rc;
+    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req), dim3(256), 0, s, a);
+    return check_launch();
 }
 
 static int decode_common(const amass_decode_args* ain, int force_dense, int v_src_force,
@@ -346,41 +397,14 @@ static int decode_common(const amass_decode_args* ain, int force_dense, int v_sr
     if (a.v_src != 0 && a.v_src != 1) return AMASS_ERR_GEOMETRY;
     if (a.dense && a.v_src == 1) return AMASS_ERR_UNSUPPORTED;
     if (a.d != DEC_D || a.page != DEC_PAGE) return AMASS_ERR_GEOMETRY;
-    if (a.G < 1 || a.G > 16 || a.n_kv < 1 || a.n_req < 0) return AMASS_ERR_GEOMETRY;
-    if (a.G > 8 && a.path == 2) return AMASS_ERR_GEOMETRY;
+    if (a.G < 1 || a.G > 8 || a.n_kv < 1 || a.n_req < 0) return AMASS_ERR_GEOMETRY;
+    if (a.path < 0 || a.path > 2) return AMASS_ERR_GEOMETRY;
+    if (a.path != 2 && (a.split < 1 || a.pps_min < 1)) return AMASS_ERR_GEOMETRY;
+    if (a.path == 2) a.pps_min = a.pps_min < 1 ? 1 : a.pps_min;
     if (a.n_req == 0) return AMASS_OK;
-    int path = a.path;
-    if (path == 0) path = (a.n_req * a.n_kv >= 128 && a.G <= 8) ? 2 : 1;
-    if (path == 1) {
-        if (!a.m_part || !a.l_part || !a.acc_part) return AMASS_ERR_NULL;
-        if (a.split < 1 || a.pps_min < 1) return AMASS_ERR_GEOMETRY;
-        dim3 grid((a.split + SPLIT_WAVES - 1) / SPLIT_WAVES, a.n_kv, a.n_req);
-        const dim3 blk(SPLIT_WAVES * WAVE);
-        if (a.dense)
-            hipLaunchKernelGGL((decode_split_kernel<0, true>), grid, blk, 0, s, a);
-        else if (a.v_src == 1)
-            hipLaunchKernelGGL((decode_split_kernel<1, false>), grid, blk, 0, s, a);
-        else
-            hipLaunchKernelGGL((decode_split_kernel<0, false>), grid, blk, 0, s, a);
-        int rc = check_launch();
-        if (rc) return rc;
-        if (a.dense)
-            hipLaunchKernelGGL((merge_kernel<true>), dim3(a.n_kv * a.G, a.n_req), dim3(WAVE), 0, s, a);
-        else
-            hipLaunchKernelGGL((merge_kernel<false>), dim3(a.n_kv * a.G, a.n_req), dim3(WAVE), 0, s, a);
-        return check_launch();
-    }
-    if (path == 2) {
-        const dim3 grid(a.n_kv, a.n_req), blk(FUSED_WAVES * WAVE);
-        if (a.dense)
-            hipLaunchKernelGGL((decode_fused_kernel<0, true>), grid, blk, 0, s, a);
-        else if (a.v_src == 1)
-            hipLaunchKernelGGL((decode_fused_kernel<1, false>), grid, blk, 0, s, a);
-        else
-            hipLaunchKernelGGL((decode_fused_kernel<0, false>), grid, blk, 0, s, a);
-        return check_launch();
-    }
-    return AMASS_ERR_GEOMETRY;
+    if (a.dense) return launch_decode<0, true>(a, a.path, s);
+    if (a.v_src == 1) return launch_decode<1, false>(a, a.path, s);
+    return launch_decode<0, false>(a, a.path, s);
 }
 
 }  // namespace amass

@@ -130,3 +130,50 @@ def test_split_equals_fused_and_padded_rows():
     torch.cuda.synchronize()
     assert np.all(outs[0][3] == 0) and np.all(outs[1][3] == 0)
     assert np.allclose(outs[0], outs[1], atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dense", [False, True])
+def test_split_merge_repeatable_across_launches_and_graph_replays(dense):
+    """Split-K partials + merge launch: eager launches and HIP-graph replays (with eager
+    work between them) give bit-identical outputs that match the fp64 oracle."""
+    announce(f"split-K repeatability, dense={dense}")
+    case = _case(3, 8, seed=91)
+    tab, cnt = _selection(case, 0.9, seed=3)
+    q, K, V, bt, sl = _np_inputs(case)
+    ref = odec.attend(q, K, V, bt, sl, None if dense else tab, None if dense else cnt,
+                      scale=case.scale, G=8, dense=dense)
+    kv = case.kv_cache.to(DEV)
+    st = _st(case, tab, cnt)
+    qd, btd, sld = case.q.to(DEV), case.block_table.to(DEV), case.seq_lens.to(DEV)
+    out = torch.zeros((3, 64, 128), dtype=torch.bfloat16, device=DEV)
+
+    def step():
+        if dense:
+            dense_paged_decode(qd, kv, btd, sld, st, out, scale=case.scale, path="split")
+        else:
+            sparse_paged_decode_batched(qd, kv, btd, sld, st, out, ResidentVSource(kv),
+                                        scale=case.scale, path="split")
+    step()
+    torch.cuda.synchronize()
+    first = out.clone()
+    got = npf(first)
+    assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), first.view(torch.int16))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), first.view(torch.int16))
+        step()                                   # eager launch between replays
+        torch.cuda.synchronize()
