@@ -18,7 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
-ABI_VERSION = 2     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
+ABI_VERSION = 3     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):
@@ -93,6 +93,13 @@ class TierFetchArgs(C.Structure):
         "pool_valid:p t_layer:i32 nb:i32 n_kv:i32 slots:i32 page:i32 d:i32 fcap:i32 grid:i32")
 
 
+class BuildArgs(C.Structure):
+    _fields_ = _fields(
+        "k:p k_sb:i64 k_st:i64 k_sh:i64 k_layers:p blocks:p rec:p rec_sb:i64 rec_lsb:i64 "
+        "tag:p tag_sb:i64 tag_sh:i64 tag_lsb:i64 n:i32 n_layers:i32 n_kv:i32 d:i32 page:i32 "
+        "kind:i32 rank:i32 v_bits:i32 c_bits:i32 v_grain:i32 c_grain:i32 tagw:i32")
+
+
 class CopyRun(C.Structure):
     _fields_ = _fields("dst:p src:p dpitch:i64 spitch:i64 width:i64 height:i64")
 
@@ -107,6 +114,7 @@ STRUCTS = {
     "amass_tier_plan_args": (6, TierPlanArgs),
     "amass_tier_fetch_args": (7, TierFetchArgs),
     "amass_copy_run": (8, CopyRun),
+    "amass_build_args": (9, BuildArgs),
 }
 
 # entry point -> argument struct (None = custom signature)
@@ -122,6 +130,7 @@ ENTRY_POINTS = {
     "amass_tier_decode": DecodeArgs,
     "amass_tier_gather_plan": TierPlanArgs,
     "amass_tier_fetch": TierFetchArgs,
+    "amass_summary_build": BuildArgs,
 }
 
 _LIB: Optional[C.CDLL] = None

@@ -1,9 +1,13 @@
-"""Page-summary builder (off the hot path): eigh of the centred page gram + int8/int4
-fake-quant, scattered into the R8State / QuadState slabs.
+"""Page-summary builder: eigh of the centred page gram + int8/int4 fake-quant, written
+into the R8State / QuadState records.
 
-Restates the reference builder (selection/build.py:297-348 quant helpers, :396-412
-``_page_eigh``, :415-632 r8 lifecycle) in torch; it runs on the device of the K cache
-(the 16x16 eigh goes through ``torch.linalg.eigh``).  Per (block, kv-head) of a finalised
+Device-resident K (the serving case) goes through the HIP kernel ``amass_summary_build``
+(one launch per layer over a block list: mean, centred Gram on the matrix cores,
+parallel-Jacobi eigh, top-r factors, quantisation and the content tag, straight into the
+packed records).  A K cache in host memory (CPU-only tests of the lifecycle) takes the
+torch restatement below of the reference builder (selection/build.py:297-348 quant
+helpers, :396-412 ``_page_eigh``, :415-632 r8 lifecycle), whose 16x16 eigh goes through
+``torch.linalg.eigh``.  Per (block, kv-head) of a finalised
 page:  mu = mean_t K ; dc = K - mu ; Gm = dc dc^T (page x page) ; S2, U = eigh(Gm)
 ascending ; top-r: S2r = clamp(S2[-r:], 1e-10), U8 = U[:, -r:], S8 = sqrt(S2r) ;
 Vk = dc^T U8 / S8 (d x r) ; c = U8 * S8 (page x r).
@@ -129,6 +133,73 @@ def r8_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> Non
     st.r8_tag[layer, blocks] = Kp_flat[:, st.page - 1, :, :st.tagw].to(st.r8_tag.dtype)
 
 
+def summary_build_hip(st, layer, K, blocks: torch.Tensor) -> None:
+    """Build the summaries of physical ``blocks`` (int64 device tensor) from device K
+    views (NB, page, n_kv, d) with one ``amass_summary_build`` launch: ``layer`` an int
+    with ``K`` one view, or ``layer`` a range of consecutive layers with ``K`` their
+    list of views (same strides; the launch reads their base addresses from a device
+    array cached on the state, so a graph replay sees the same array)."""
+    from .._hip import BuildArgs, call, current_stream, ptr, require_cuda
+    r8 = hasattr(st, "r8_rec")
+    rec_all = st.r8_rec if r8 else st.quad_rec
+    tag_all = st.r8_tag if r8 else st.quad_tag
+    if isinstance(layer, range):
+        Ks, l0, nl = list(K), layer.start, len(layer)
+        if layer.step != 1 or len(Ks) != nl or nl < 1:
+            raise ValueError("layers must be a unit-step range matching the K views")
+    else:
+        Ks, l0, nl = [K], int(layer), 1
+    K0 = Ks[0]
+    require_cuda(*Ks, blocks, rec_all)
+    for Kl in Ks:
+        if Kl.dtype != torch.bfloat16 or Kl.stride() != K0.stride() or Kl.stride(3) != 1:
+            raise ValueError("K views must be bf16 (NB, page, n_kv, d) with equal strides and "
+                             "unit stride on d")
+    blocks = blocks.to(torch.int64).contiguous()
+    kl = None
+    if nl > 1:
+        key = tuple(Kl.data_ptr() for Kl in Ks)
+        cache = st.__dict__.setdefault("_k_layer_ptrs", {})
+        kl = cache.get(key)
+        if kl is None:
+            kl = torch.tensor(key, dtype=torch.int64, device=K0.device)
+            cache[key] = kl
+    rec, tag = rec_all[l0], tag_all[l0]
+    v_bits = st.vk_bits if r8 else st.v_bits
+    v_grain = (st.vk_grain if r8 else st.v_grain) == "tensor"
+    a = BuildArgs(
+        k=ptr(K0), k_sb=K0.stride(0), k_st=K0.stride(1), k_sh=K0.stride(2), k_layers=ptr(kl),
+        blocks=ptr(blocks), rec=ptr(rec), rec_sb=rec.stride(0), rec_lsb=rec_all.stride(0),
+        tag=ptr(tag), tag_sb=tag.stride(0), tag_sh=tag.stride(1), tag_lsb=tag_all.stride(0),
+        n=int(blocks.numel()), n_layers=nl, n_kv=st.n_kv, d=st.d, page=st.page,
+        kind=1 if r8 else 0, rank=st.r, v_bits=v_bits, c_bits=st.c_bits if r8 else 8,
+        v_grain=int(v_grain), c_grain=int(r8 and st.c_grain == "tensor"), tagw=st.tagw)
+    call("amass_summary_build", a, current_stream(K0.device))
+
+
+def _write_blocks(st, layer: int, K: torch.Tensor, blocks: torch.Tensor, writer) -> None:
+    """Summaries of ``blocks`` into ``layer``: the HIP builder for a device K, the torch
+    restatement (in chunks) for a host K."""
+    if K.is_cuda:
+        summary_build_hip(st, layer, K, blocks)
+        return
+    for i in range(0, blocks.numel(), CHUNK):
+        b = blocks[i:i + CHUNK]
+        writer(st, K[b], layer, b)
+
+
+def _write_layers(st, K_layers, blocks: torch.Tensor, writer) -> None:
+    """Summaries of ``blocks`` in every layer: one HIP launch when all layers' K views
+    are on the device with equal strides, else per layer."""
+    K_layers = list(K_layers)
+    if (K_layers and all(K.is_cuda for K in K_layers)
+            and all(K.stride() == K_layers[0].stride() for K in K_layers)):
+        summary_build_hip(st, range(len(K_layers)), K_layers, blocks)
+        return
+    for l, K in enumerate(K_layers):
+        _write_blocks(st, l, K, blocks, writer)
+
+
 def _stale(tag_slab, K, blocks, page, tagw):
     cur = K[blocks, page - 1, :, :tagw].float()
     return (cur != tag_slab[blocks].float()).any(dim=(1, 2))   # NaN tag -> stale
@@ -141,9 +212,7 @@ def _refresh(st, layer, K, block_table, seq_lens, n_req, force, tag_slab, writer
     if not force:
         blocks = blocks[_stale(tag_slab[layer], K, blocks, st.page, st.tagw)]
     blocks = torch.unique(blocks)
-    for i in range(0, blocks.numel(), CHUNK):
-        b = blocks[i:i + CHUNK]
-        writer(st, K[b], layer, b)
+    _write_blocks(st, layer, K, blocks, writer)
     return int(blocks.numel())
 
 
@@ -166,8 +235,7 @@ def r8_build_tail(st, K_layers, block_table, seq_lens, n_req: int, rows=None) ->
     if n_req == 0:
         return 0
     blocks = _tail_blocks(block_table, seq_lens, n_req, st.page, rows)
-    for l, K in enumerate(K_layers):
-        r8_write(st, K[blocks], l, blocks)
+    _write_layers(st, K_layers, blocks, r8_write)
     return len(K_layers) * int(blocks.numel())
 
 

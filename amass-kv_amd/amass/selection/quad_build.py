@@ -5,14 +5,16 @@ r8 builder (:mod:`amass.selection.build`), storing the top-r' eigenvalues ``sig2
 of the per-key coordinates.  Per (block, kv-head): quad_mu/mu_scale = int8 page mean,
 quad_V/V_scale = Vk = dc^T U8 / S8 quantised per column (int8 or packed int4, stored
 in the column-major kernel layout),
-quad_sig2 = fp16(S2r), quad_tag = leading TAGW channels of the page's last key.
+quad_sig2 = fp16(S2r), quad_tag = leading TAGW channels of the page's last key.  A device
+K is summarised by the HIP builder (``amass_summary_build``), a host K by the torch
+restatement below.
 """
 from __future__ import annotations
 
 import torch
 
 from .build import (CHUNK, _page_eigh, _quant_mu, _quant_vk, _refresh, _tail_blocks,
-                    finalized_blocks)
+                    _write_blocks, _write_layers, finalized_blocks)
 from .quad_state import v_to_device
 
 
@@ -39,8 +41,7 @@ def quad_build_tail(st, K_layers, block_table, seq_lens, n_req: int, rows=None) 
     if n_req == 0:
         return 0
     blocks = _tail_blocks(block_table, seq_lens, n_req, st.page, rows)
-    for l, K in enumerate(K_layers):
-        quad_write(st, K[blocks], l, blocks)
+    _write_layers(st, K_layers, blocks, quad_write)
     return len(K_layers) * int(blocks.numel())
 
 

@@ -42,6 +42,7 @@ extern "C" size_t amass_abi_struct_size(int which) {
         case 6: return sizeof(amass_tier_plan_args);
         case 7: return sizeof(amass_tier_fetch_args);
         case 8: return sizeof(amass_copy_run);
+        case 9: return sizeof(amass_build_args);
         default: return 0;
     }
 }

@@ -17,7 +17,8 @@ Inputs are synthetic (amass.bench.synth, seeded) and resident in HBM before timi
 Secondary lines (under "configs"; skipped with --quick): config 1 with the key-norm boost,
 config 2 (r8, 64 ragged sequences, 5 % budget), config 3 (G = 8, 131072 tokens, coverage
 0.95, split-K path) and config 4 (mem-v, 64 steps from a cold hot buffer, both boosts),
-each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s.
+each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s; and the HIP
+page-summary builder (bulk build and steady-state tail rebuild at config 1).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--quick]
                   [--configs 1k,2,3,4]
@@ -295,6 +296,45 @@ def run_secondary(idx, args, boost="sigma"):
     return res
 
 
+def run_summary_build(args):
+    """The HIP page-summary builder (amass_summary_build) at config 1: the bulk build of
+    every finalised page (32 x 1024 blocks x 8 kv heads, quad r'=8 int8), and the
+    steady-state tail rebuild of each request's last finalised page in one layer and in
+    all 32 layers of the 8B model (one launch)."""
+    import torch
+
+    from amass.bench.synth import build_quad_state, config_case
+    from amass.selection import QuadState
+    from amass.selection.build import finalized_blocks, summary_build_hip
+    from amass.selection.quad_build import quad_build_tail
+
+    case = config_case(1, seed=args.seed, device="cuda")
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
+    B = case.q.shape[0]
+    blocks = torch.unique(finalized_blocks(case.block_table, case.seq_lens, B, 16))
+    g = graph_of(lambda: summary_build_hip(st, 0, case.K, blocks))
+    ms_bulk = time_graph(g, 3, 1, batches=3)
+    del g
+    g = graph_of(lambda: quad_build_tail(st, [case.K], case.block_table, case.seq_lens, B), 10)
+    us_tail = time_graph(g, 5, 2, reps=10) * 1e3
+    del g, st
+    L = 32
+    st32 = QuadState("cuda", num_layers=L, num_blocks=case.kv_cache.shape[0], n_kv=case.n_kv,
+                     G=case.G, head_dim=128, page=16, max_reqs=B, max_pages=case.max_pages,
+                     rank=8, combine="nrm")
+    Ks = [case.K] * L
+    g = graph_of(lambda: quad_build_tail(st32, Ks, case.block_table, case.seq_lens, B), 5)
+    us_tail32 = time_graph(g, 5, 2, reps=5) * 1e3
+    del g, st32
+    n = int(blocks.numel()) * case.n_kv
+    log(f"summary build: bulk {ms_bulk:.2f} ms for {n} (block, head) pages, tail {us_tail:.1f} "
+        f"us (1 layer), {us_tail32:.1f} us ({L} layers)")
+    return dict(workload=f"config1 K pages, quad r'=8 int8: bulk = {int(blocks.numel())} blocks "
+                         f"x {case.n_kv} heads; tail = {B} blocks x {case.n_kv} heads per layer",
+                bulk_ms=round(ms_bulk, 3), bulk_ns_per_page_head=round(ms_bulk * 1e6 / n, 1),
+                tail_us_1layer=round(us_tail, 2), tail_us_32layers=round(us_tail32, 2))
+
+
 def run_config4(args, boost="sigma", steps=64):
     """mem-v: V in the pinned, device-mapped host pool, a 10 % hot buffer, 64 decode steps
     with fresh N(0, 1) queries over a fixed boosted page set.  Each step = quad score +
@@ -387,8 +427,9 @@ def main():
     ap.add_argument("--boost", default="sigma", choices=["sigma", "keynorm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
-    ap.add_argument("--configs", default="1k,2,3,4",
-                    help="secondary lines: 1k (config 1 with the key-norm boost), 2, 3, 4")
+    ap.add_argument("--configs", default="1k,2,3,4,build",
+                    help="secondary lines: 1k (config 1 with the key-norm boost), 2, 3, 4, "
+                         "build (the HIP summary builder)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB read + 256 MiB write kernel (HBM counter calibration)")
     args = ap.parse_args()
@@ -486,6 +527,8 @@ def main():
                 sec["config1_keynorm"] = run_secondary(1, args, boost="keynorm")
             elif c in ("2", "3"):
                 sec[f"config{c}"] = run_secondary(int(c), args)
+            elif c == "build":
+                sec["summary_build"] = run_summary_build(args)
             elif c == "4":
                 sec["config4_memv"] = run_config4(args, "sigma")
                 free_gpu()

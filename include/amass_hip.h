@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 2
+#define AMASS_ABI_VERSION 3
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -101,6 +101,32 @@ typedef struct amass_r8_score_args {
     int32_t n_req, n_kv, G, d, page, rank, vk_bits, c_bits, max_pages;
 } amass_r8_score_args;
 int amass_r8_score(const amass_r8_score_args* a, void* stream);
+
+/* ---- page-summary builder ---------------------------------------------------------- */
+/* Replaces the summary math of selection/quad_build.py:124-198 (quad_build_refresh) and
+ * selection/build.py:396-632 (_page_eigh, _r8_write, the *_build_{refresh,tail,bulk,delta}
+ * op chains) and the jacobi_eigh16 kernels of selection/build.py:84-242.  For each
+ * physical block blocks[i] and kv head h of the K view (16-token pages, d = 128):
+ * mu = mean_t K, dc = K - mu, Gm = dc dc^T, eigh(Gm) (parallel Jacobi, fp32), the top-r
+ * eigenpairs (S2r = max(eig, 1e-10), ascending), Vk = dc^T U8 / sqrt(S2r) and, for r8,
+ * c = U8 sqrt(S2r); symmetric quantisation s = max(amax / lvl, 1e-8), code =
+ * clamp(rint(x / s), +-lvl), scale stored as fp16(s) (mu per head; Vk per column for
+ * v_grain 0 or per head for 1; c per token for c_grain 0 or per head for 1).  Writes the
+ * block's packed record (kind 0: quad, AMASS_QUAD_REC_BYTES layout with sig2 = fp16(S2r);
+ * kind 1: r8, AMASS_R8_REC_BYTES layout) and, if tag != NULL, the content tag
+ * K[page-1][h][0:tagw].  rank 1..8 (even for int4 codes).  n_layers layers in one launch:
+ * layer l reads K at k_layers[l] (a device array of base addresses; k itself when
+ * n_layers == 1 and k_layers == NULL), with the same strides, and writes rec + l*rec_lsb,
+ * tag + l*tag_lsb (the L-major state slabs). */
+typedef struct amass_build_args {
+    const void*    k;  int64_t k_sb, k_st, k_sh;   /* K view (NB,page,n_kv,d) bf16      */
+    const uint64_t* k_layers;                       /* optional (n_layers,) K base addrs */
+    const int64_t* blocks;                          /* (n,) physical blocks to summarise */
+    int8_t*        rec;  int64_t rec_sb, rec_lsb;   /* records (L,NB,n_kv*REC), bytes    */
+    void*          tag;  int64_t tag_sb, tag_sh, tag_lsb; /* optional (L,NB,n_kv,tagw) bf16 */
+    int32_t n, n_layers, n_kv, d, page, kind, rank, v_bits, c_bits, v_grain, c_grain, tagw;
+} amass_build_args;
+int amass_summary_build(const amass_build_args* a, void* stream);
 
 /* ---- per-step derived page parameters --------------------------------------------- */
 /* Replaces selection/select.py:30-54 (_derive_params_kernel / derive_page_params):

@@ -23,6 +23,11 @@ Modules and what pins each function (beyond "it restates the reference"):
                                                         f2u order-preserving
   decode.py  attend (decode.py:128-241 math)            pinned: dense softmax attention
              split_merge (decode.py:146-153, merge.py:21-50)  pinned: split invariance
+  build.py   page_factors (build.py:396-412, quad_build.py:124-198)
+                                                        pinned: exact reconstruction at
+                                                        rank <= r, sig2 == svd(dc)^2,
+                                                        Vk orthonormal, rank-1 page by hand
+             quad_summary / r8_summary (quant rules)    pinned: via quant + the factors
   tier.py    plan (residency.py:45-139)                 pinned: hand-worked LRU example,
                                                         page2slot/slot2page inverse,
                                                         victims are the oldest untouched

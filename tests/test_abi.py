@@ -52,10 +52,10 @@ _KIND = {"p": ctypes.c_void_p, "int64_t": ctypes.c_int64, "int32_t": ctypes.c_in
 def test_library_loads_and_exports_every_symbol():
     lib = _hip.load_library()
     names = _declared_functions()
-    assert len(names) == 18
+    assert len(names) == 19
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
-    assert lib.amass_abi_version() == 2
+    assert lib.amass_abi_version() == 3
 
 
 def test_struct_mirrors_header():
@@ -79,6 +79,8 @@ def test_status_strings_and_null_rejection():
     d = _hip.DecodeArgs()
     assert lib.amass_sparse_decode(ctypes.byref(d), None) == -1
     assert lib.amass_topb_select(None, None) == -1
+    b = _hip.BuildArgs()
+    assert lib.amass_summary_build(ctypes.byref(b), None) == -1
     assert lib.amass_host_pool_alloc(16, None, None) == -1
 
 
