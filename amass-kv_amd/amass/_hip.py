@@ -18,7 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
-ABI_VERSION = 3     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
+ABI_VERSION = 4     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):
@@ -48,6 +48,14 @@ class R8ScoreArgs(C.Structure):
         "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 seq_lens:p "
         "n_sel_hi:p score:p sc_sr:i64 sc_sh:i64 comb_out:p scale:f32 n_req:i32 n_kv:i32 "
         "G:i32 d:i32 page:i32 rank:i32 vk_bits:i32 c_bits:i32 max_pages:i32")
+
+
+class ClseScoreArgs(C.Structure):
+    _fields_ = _fields(
+        "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 seq_lens:p "
+        "n_sel_hi:p score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 "
+        "comb_out:p scale:f32 n_req:i32 n_kv:i32 G:i32 d:i32 page:i32 rank:i32 v_bits:i32 "
+        "c_bits:i32 max_pages:i32 combine:i32")
 
 
 class DeriveArgs(C.Structure):
@@ -115,6 +123,7 @@ STRUCTS = {
     "amass_tier_fetch_args": (7, TierFetchArgs),
     "amass_copy_run": (8, CopyRun),
     "amass_build_args": (9, BuildArgs),
+    "amass_clse_score_args": (10, ClseScoreArgs),
 }
 
 # entry point -> argument struct (None = custom signature)
@@ -131,6 +140,7 @@ ENTRY_POINTS = {
     "amass_tier_gather_plan": TierPlanArgs,
     "amass_tier_fetch": TierFetchArgs,
     "amass_summary_build": BuildArgs,
+    "amass_clse_score": ClseScoreArgs,
 }
 
 _LIB: Optional[C.CDLL] = None

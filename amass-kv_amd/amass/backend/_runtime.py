@@ -38,8 +38,6 @@ def unsupported_reason(cfg: Optional[AmassConfig], *, head_size: int, block_size
     if cfg.variant != "fast":
         return (f"variant {cfg.variant!r}: the tier's write path (staging / flush) is not "
                 "part of this build, so mem variants keep the stock attention")
-    if cfg.score == "clse":
-        return "score='clse' is not built on this backend (use score='quad' or 'r8')"
     if head_size != HEAD_DIM or block_size != PAGE:
         return f"head_size {head_size} / block_size {block_size} (built for 128 / 16)"
     if not 1 <= G <= 8:
@@ -56,9 +54,11 @@ def make_state(cfg: AmassConfig, device, *, num_layers: int, num_blocks: int, n_
     common = dict(num_layers=num_layers, num_blocks=num_blocks, n_kv=n_kv, G=G,
                   head_dim=HEAD_DIM, page=PAGE, max_reqs=max_reqs, max_pages=max_pages,
                   budget=budget, sink_pages=cfg.sink_pages, window_pages=cfg.window_pages)
-    if cfg.score == "quad":
+    if cfg.score in ("quad", "clse"):
+        clse = cfg.score == "clse"
         st = QuadState(device, rank=cfg.quad_rank, v_bits=cfg.quad_v_bits,
-                       combine=cfg.quad_combine, **common)
+                       combine=cfg.quad_combine, coords="lse" if clse else "none",
+                       c_bits=cfg.quad_c_bits, c_grain=cfg.quad_c_grain, **common)
     else:
         st = R8State(device, rank=cfg.r8_rank, **common)
     # budget None -> the per-(request, kv-head) coverage nucleus; else fixed top-b
@@ -84,9 +84,11 @@ def select(q, kv_cache, block_table, seq_lens, st, n_req: int, scale: float,
            cfg: AmassConfig) -> None:
     """Stage A for one layer: score + (nrm) + top-b / coverage -> st.page_table,
     st.page_cnt.  ``derive=False``: the builder derived this step's page params."""
-    from ..selection import QuadState, select_pages_quad, select_pages_r8
+    from ..selection import QuadState, select_pages_clse, select_pages_quad, select_pages_r8
     lidx = layer_index(st, kv_cache)
-    if isinstance(st, QuadState):
+    if isinstance(st, QuadState) and st.coords == "lse":
+        select_pages_clse(st, lidx, q, block_table, seq_lens, n_req, scale, derive=False)
+    elif isinstance(st, QuadState):
         select_pages_quad(st, lidx, q, block_table, seq_lens, n_req, scale, derive=False)
     else:
         select_pages_r8(st, lidx, q, block_table, seq_lens, n_req, scale, derive=False)

@@ -175,7 +175,7 @@ class AmassMetadataBuilderMixin:
     # ---- summary refresh gate -------------------------------------------------------- #
     def _amass_fns(self):
         from .. import selection as sel
-        if self._amass_cfg.score == "quad":
+        if self._amass_cfg.score in ("quad", "clse"):
             return sel.quad_build_tail, sel.quad_build_bulk, sel.quad_build_delta
         return sel.r8_build_tail, sel.r8_build_bulk, sel.r8_build_delta
 

@@ -130,8 +130,10 @@ def config_case(idx: int, *, seed: int = 0, device="cpu", boost: str = "sigma", 
 
 def build_quad_state(case: Case, *, rank: int = 8, v_bits: int = 8, combine: str = "nrm",
                      budget: float = 0.1, coverage: Optional[float] = None, sink: int = 1,
-                     window: int = 1, max_reqs: Optional[int] = None):
-    """QuadState with layer 0 summarised from the case's K (the torch builder)."""
+                     window: int = 1, max_reqs: Optional[int] = None, coords: str = "none",
+                     c_bits: int = 4, c_grain: str = "token"):
+    """QuadState with layer 0 summarised from the case's K (the HIP builder for a device
+    case, the torch builder for a host one); coords="lse" makes the CLSE state."""
     from ..selection import QuadState, quad_build_refresh
     from ..attention import ensure_stage_b_buffers
     dev = case.kv_cache.device
@@ -139,7 +141,8 @@ def build_quad_state(case: Case, *, rank: int = 8, v_bits: int = 8, combine: str
                    G=case.G, head_dim=case.d, page=case.page,
                    max_reqs=max_reqs or case.q.shape[0], max_pages=case.max_pages,
                    rank=rank, budget=budget, sink_pages=sink, window_pages=window,
-                   v_bits=v_bits, combine=combine)
+                   v_bits=v_bits, combine=combine, coords=coords, c_bits=c_bits,
+                   c_grain=c_grain)
     st.coverage = coverage
     st.scale = case.scale
     quad_build_refresh(st, 0, case.K, case.block_table, case.seq_lens, case.q.shape[0],

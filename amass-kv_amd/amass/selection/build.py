@@ -165,15 +165,19 @@ def summary_build_hip(st, layer, K, blocks: torch.Tensor) -> None:
             kl = torch.tensor(key, dtype=torch.int64, device=K0.device)
             cache[key] = kl
     rec, tag = rec_all[l0], tag_all[l0]
+    clse = not r8 and getattr(st, "coords", "none") == "lse"
     v_bits = st.vk_bits if r8 else st.v_bits
     v_grain = (st.vk_grain if r8 else st.v_grain) == "tensor"
+    # one c scale per (block, head): r8 c_grain "tensor", CLSE c_grain "page"
+    c_head = (r8 and st.c_grain == "tensor") or (clse and st.c_grain == "page")
     a = BuildArgs(
         k=ptr(K0), k_sb=K0.stride(0), k_st=K0.stride(1), k_sh=K0.stride(2), k_layers=ptr(kl),
         blocks=ptr(blocks), rec=ptr(rec), rec_sb=rec.stride(0), rec_lsb=rec_all.stride(0),
         tag=ptr(tag), tag_sb=tag.stride(0), tag_sh=tag.stride(1), tag_lsb=tag_all.stride(0),
         n=int(blocks.numel()), n_layers=nl, n_kv=st.n_kv, d=st.d, page=st.page,
-        kind=1 if r8 else 0, rank=st.r, v_bits=v_bits, c_bits=st.c_bits if r8 else 8,
-        v_grain=int(v_grain), c_grain=int(r8 and st.c_grain == "tensor"), tagw=st.tagw)
+        kind=1 if r8 else (2 if clse else 0), rank=st.r, v_bits=v_bits,
+        c_bits=st.c_bits if (r8 or clse) else 8, v_grain=int(v_grain), c_grain=int(c_head),
+        tagw=st.tagw)
     call("amass_summary_build", a, current_stream(K0.device))
 
 

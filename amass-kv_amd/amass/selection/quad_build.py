@@ -13,20 +13,32 @@ from __future__ import annotations
 
 import torch
 
-from .build import (CHUNK, _page_eigh, _quant_mu, _quant_vk, _refresh, _tail_blocks,
+from .build import (CHUNK, _page_eigh, _quant_c, _quant_mu, _quant_vk, _refresh, _tail_blocks,
                     _write_blocks, _write_layers, finalized_blocks)
 from .quad_state import v_to_device
 
 
 def quad_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> None:
-    mu, _U8, _S8, S2r, Vk = _page_eigh(Kp_flat, st.r)
+    mu, U8, S8, S2r, Vk = _page_eigh(Kp_flat, st.r)
     mu_code, mu_s = _quant_mu(mu)
     v_code, v_s = _quant_vk(Vk, st.v_grain, st.v_bits)
     st.quad_mu[layer, blocks] = mu_code
     st.mu_scale[layer, blocks] = mu_s
     st.quad_V[layer, blocks] = v_to_device(v_code, st.v_bits)
     st.V_scale[layer, blocks] = v_s
-    st.quad_sig2[layer, blocks] = S2r.to(st.quad_sig2.dtype)
+    if getattr(st, "coords", "none") == "lse":
+        # CLSE extras (reference selection/quad_build.py:38-54): c = U8 * S8 quantised per
+        # token ("token") or per (block, head) ("page"); resid = trace - sum(top-r' eig)
+        c = U8 * S8[..., None, :]
+        c_code, c_s = _quant_c(c, "page" if st.c_grain == "token" else "tensor", st.c_bits)
+        Kp = Kp_flat.permute(0, 2, 1, 3).float()
+        trace = Kp.pow(2).sum(dim=(2, 3)) - st.page * mu.pow(2).sum(-1)
+        st.quad_c[layer, blocks] = c_code
+        st._c_scale16[layer, blocks] = c_s.to(st._c_scale16.dtype)
+        st.quad_resid[layer, blocks] = (trace - S2r.sum(-1)).clamp_min(0).to(
+            st.quad_resid.dtype)
+    else:
+        st.quad_sig2[layer, blocks] = S2r.to(st.quad_sig2.dtype)
     st.quad_tag[layer, blocks] = Kp_flat[:, st.page - 1, :, :st.tagw].to(st.quad_tag.dtype)
 
 

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from .._hip import NrmArgs, QuadScoreArgs, call, current_stream, ptr, require_cuda
+from .._hip import ClseScoreArgs, NrmArgs, QuadScoreArgs, call, current_stream, ptr, require_cuda
 from .select import derive_page_params, select_pages
 
 
@@ -26,6 +26,8 @@ def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadSc
         raise ValueError("block_table narrower than the scored page range")
     if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
         raise ValueError("quad_rec must hold each block's records contiguously")
+    if getattr(st, "coords", "none") != "none":
+        raise ValueError("a CLSE state (coords='lse') is scored by clse_score")
     nrm = st.combine == "nrm"
     sh = st.score_h
     return QuadScoreArgs(
@@ -78,10 +80,46 @@ def select_pages_quad(st, layer: int, q, block_table, seq_lens, n_req: int, scal
     select_pages(st, n_req, score_h=st.score_h if st.combine == "nrm" else None)
 
 
-def clse_score(*_a, **_k):
-    raise NotImplementedError("score='clse' is outside this build's hot path "
-                              "(quad and r8 are implemented)")
+def clse_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
+               comb_out=None) -> None:
+    """Stage-A.1 (CLSE mode, reference selection/quad_score.py:373-393): combine="max"
+    writes st.score (R, n_kv, MP); combine="nrm" writes the per-head st.score_h, which the
+    selection launch then combines (select_pages_clse)."""
+    if n_req > st.max_reqs:
+        raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
+    if getattr(st, "coords", "none") != "lse":
+        raise ValueError("clse_score needs a QuadState built with coords='lse'")
+    rec = st.quad_rec[layer]
+    require_cuda(q, block_table, seq_lens, rec)
+    if q.dtype != torch.bfloat16 or q.stride(2) != 1:
+        raise ValueError("q must be bf16 (T, H, d) with unit stride on d")
+    if block_table.dtype != torch.int32 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be int32 with unit column stride")
+    if seq_lens.dtype != torch.int32:
+        raise ValueError("seq_lens must be int32")
+    if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
+        raise ValueError("quad_rec must hold each block's records contiguously")
+    nrm = st.combine == "nrm"
+    sh = st.score_h
+    a = ClseScoreArgs(
+        q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1), rec=ptr(rec), rec_sb=rec.stride(0),
+        block_table=ptr(block_table), bt_st=block_table.stride(0), seq_lens=ptr(seq_lens),
+        n_sel_hi=ptr(st.n_sel_hi),
+        score=ptr(st.score), sc_sr=st.score.stride(0), sc_sh=st.score.stride(1),
+        score_h=ptr(sh) if nrm else None,
+        sh_sr=sh.stride(0) if nrm else 0, sh_sh=sh.stride(1) if nrm else 0,
+        sh_sg=sh.stride(2) if nrm else 0,
+        comb_out=ptr(comb_out), scale=float(scale), n_req=n_req, n_kv=st.n_kv, G=st.G,
+        d=st.d, page=st.page, rank=st.r, v_bits=st.v_bits, c_bits=st.c_bits,
+        max_pages=st.max_pages, combine=1 if nrm else 0)
+    call("amass_clse_score", a, current_stream(q.device))
 
 
-def select_pages_clse(*_a, **_k):
-    raise NotImplementedError("score='clse' is outside this build's hot path")
+def select_pages_clse(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
+                      *, derive: bool = True) -> None:
+    """One-call Stage A (CLSE mode, reference selection/quad_score.py:396-404): (derive)
+    + clse_score + selection (the nrm combine fused into it for combine="nrm")."""
+    if derive:
+        derive_page_params(st, seq_lens, n_req)
+    clse_score(st, layer, q, block_table, seq_lens, n_req, scale)
+    select_pages(st, n_req, score_h=st.score_h if st.combine == "nrm" else None)

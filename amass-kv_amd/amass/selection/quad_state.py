@@ -23,6 +23,14 @@ instruction, and reads a page's scales with one more 16-byte load per lane.
 ``v_to_device`` / ``v_to_reference`` convert V between this and the reference layout;
 ``load_reference`` and ``reference_V`` use them.
 
+CLSE (``coords="lse"``, the reference's ``score="clse"``) keeps the per-key coordinates
+and the residual scatter energy instead of sig2, in the r8 record layout
+(AMASS_R8_REC_BYTES, see :mod:`amass.selection.state`): per head
+``[quad_V column-major | quad_mu | quad_c (page, r'[/2])]`` and a 64-byte scale block
+with V_scale at half 0, c_scale at halves 8..23 (``c_grain="page"``: one scale per
+(block, head), kept in all 16 halves and exposed as half 8), mu_scale at half 24 and
+quad_resid at half 25; ``quad_sig2`` is None there.
+
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
 (R, n_kv, G, MP) and hmax (R, n_kv, G).
 """
@@ -81,9 +89,12 @@ class QuadState:
             raise ValueError("quad V codes are int4 or int8; mu stays int8")
         if rank < 1 or (v_bits == 4 and rank % 2):
             raise ValueError(f"rank {rank} invalid for v_bits={v_bits}")
-        if coords != "none":
-            raise NotImplementedError(
-                "score='clse' (per-key coords) is not part of this build's hot path")
+        if coords not in ("none", "lse"):
+            raise ValueError(f"coords must be 'none' or 'lse', got {coords!r}")
+        if coords == "lse" and (c_bits not in (4, 8) or c_grain not in ("token", "page")
+                                or (c_bits == 4 and rank % 2)):
+            raise ValueError(f"CLSE coords: c_bits 4|8, c_grain token|page (got {c_bits}, "
+                             f"{c_grain!r}; int4 needs an even rank)")
         if combine not in ("max", "nrm"):
             raise ValueError(f"combine must be 'max' or 'nrm', got {combine!r}")
         L, NB, D, r, MP, R = num_layers, num_blocks, head_dim, rank, max_pages, max_reqs
@@ -100,22 +111,32 @@ class QuadState:
         self.device = device
         i8, f16, bf16 = torch.int8, torch.float16, torch.bfloat16
         i32, f32, f64 = torch.int32, torch.float32, torch.float64
-        if r > 8 or D != 128:
-            raise ValueError("the packed quad record holds r' <= 8 columns of d = 128")
+        if r > 8 or D != 128 or (coords == "lse" and page != 16):
+            raise ValueError("the packed quad record holds r' <= 8 columns of d = 128 "
+                             "(and 16-token pages with CLSE coordinates)")
         cb = D // 2 if v_bits == 4 else D
         vb = r * cb
-        vm = vb + D                                       # V + mu bytes per head
+        rc = (r // 2 if c_bits == 4 else r) if coords == "lse" else 0
+        vm = vb + D + page * rc                           # V + mu (+ c) bytes per head
         self.rec_bytes = vm + 64                          # + the head's scale block
         self.quad_rec = torch.zeros(L, NB, n_kv * self.rec_bytes, device=device, dtype=i8)
         recs = self.quad_rec[..., :n_kv * vm].unflatten(-1, (n_kv, vm))
         meta = self.quad_rec[..., n_kv * vm:].unflatten(-1, (n_kv, 64)).view(f16)
         self.quad_V = recs[..., :vb].unflatten(-1, (r, cb))
-        self.quad_mu = recs[..., vb:]
+        self.quad_mu = recs[..., vb:vb + D]
         self.V_scale = meta[..., 0:r]
-        self.quad_sig2 = meta[..., 8:8 + r]
-        self.mu_scale = meta[..., 16]
         self.quad_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=device, dtype=bf16)
-        self.quad_c = self.c_scale = self.quad_resid = None
+        if coords == "lse":
+            self.quad_c = recs[..., vb + D:].unflatten(-1, (page, rc))
+            self._c_scale16 = meta[..., 8:8 + page]
+            self.c_scale = self._c_scale16 if c_grain == "token" else meta[..., 8]
+            self.mu_scale = meta[..., 24]
+            self.quad_resid = meta[..., 25]
+            self.quad_sig2 = None
+        else:
+            self.quad_sig2 = meta[..., 8:8 + r]
+            self.mu_scale = meta[..., 16]
+            self.quad_c = self.c_scale = self.quad_resid = self._c_scale16 = None
         self.score = torch.empty(R, n_kv, MP, device=device, dtype=f32)
         self.page_table = torch.empty(R, n_kv, MP, device=device, dtype=i32)
         self.page_cnt = torch.zeros(R, n_kv, device=device, dtype=i32)
@@ -135,18 +156,30 @@ class QuadState:
 
     def layer_state(self, layer: int):
         """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer`` (V column-major)."""
+        sig2 = self.quad_sig2[layer] if self.quad_sig2 is not None else None   # None: CLSE
         return (self.quad_mu[layer], self.mu_scale[layer], self.quad_V[layer],
-                self.V_scale[layer], self.quad_sig2[layer], self.quad_tag[layer])
+                self.V_scale[layer], sig2, self.quad_tag[layer])
 
-    def load_reference(self, layer: int, mu, mu_scale, V, V_scale, sig2) -> None:
+    def load_reference(self, layer: int, mu, mu_scale, V, V_scale, sig2=None, c=None,
+                       c_scale=None, resid=None) -> None:
         """Write one layer's summaries given in the reference layout
-        (``selection/quad_state.py:36-151``: quad_V (NB, n_kv, d, r'[/2]))."""
+        (``selection/quad_state.py:36-151``: quad_V (NB, n_kv, d, r'[/2]); CLSE adds
+        quad_c (NB, n_kv, page, r'[/2]), c_scale (token: (NB, n_kv, page), page:
+        (NB, n_kv)) and quad_resid (NB, n_kv))."""
         dev = self.quad_mu.device
-        self.quad_mu[layer].copy_(torch.as_tensor(mu).to(dev))
-        self.mu_scale[layer].copy_(torch.as_tensor(mu_scale).to(dev))
-        self.quad_V[layer].copy_(v_to_device(torch.as_tensor(V).to(dev), self.v_bits))
-        self.V_scale[layer].copy_(torch.as_tensor(V_scale).to(dev))
-        self.quad_sig2[layer].copy_(torch.as_tensor(sig2).to(dev))
+        t = lambda x: torch.as_tensor(x).to(dev)  # noqa: E731
+        self.quad_mu[layer].copy_(t(mu))
+        self.mu_scale[layer].copy_(t(mu_scale))
+        self.quad_V[layer].copy_(v_to_device(t(V), self.v_bits))
+        self.V_scale[layer].copy_(t(V_scale))
+        if self.coords == "lse":
+            self.quad_c[layer].copy_(t(c))
+            cs = t(c_scale)
+            self._c_scale16[layer].copy_(cs if self.c_grain == "token"
+                                         else cs[..., None].expand_as(self._c_scale16[layer]))
+            self.quad_resid[layer].copy_(t(resid))
+        else:
+            self.quad_sig2[layer].copy_(t(sig2))
 
     def reference_V(self, layer: int) -> torch.Tensor:
         """quad_V of ``layer`` in the reference layout (NB, n_kv, d, r'[/2])."""

@@ -43,6 +43,7 @@ extern "C" size_t amass_abi_struct_size(int which) {
         case 7: return sizeof(amass_tier_fetch_args);
         case 8: return sizeof(amass_copy_run);
         case 9: return sizeof(amass_build_args);
+        case 10: return sizeof(amass_clse_score_args);
         default: return 0;
     }
 }

@@ -72,8 +72,11 @@ __device__ __forceinline__ uint16_t f2h_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-template <bool R8>
+// KIND 0: quad record; 1: r8 record; 2: CLSE (the r8 record + the residual energy)
+template <int KIND>
 __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_build_args a) {
+    constexpr bool R8 = KIND >= 1;
+    constexpr bool CLSE = KIND == 2;
     __shared__ BuildLds L;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
@@ -134,6 +137,9 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         }
     }
     __syncthreads();
+    // trace of the centred scatter (the sum of all eigenvalues), for CLSE's residual
+    float trace = 0.f;
+    if constexpr (CLSE) trace = wave_sumf(lane < BP ? L.a[w][lane][lane] : 0.f);
 
     // ---- parallel Jacobi ----------------------------------------------------------------
     for (int sweep = 0; sweep < BSWEEPS; ++sweep) {
@@ -322,6 +328,12 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         if constexpr (R8) {
             if (lane >= 8 && lane < 24) { v = cs_in; set = true; }
             else if (lane == 24) { v = msc; set = true; }
+            else if (CLSE && lane == 25) {
+                float top = 0.f;
+                for (int k = 0; k < r; ++k) top += L.s2[w][k];
+                v = fmaxf(trace - top, 0.f);
+                set = true;
+            }
         } else {
             if (lane >= 8 && lane < 8 + r) { v = L.s2[w][lane - 8]; set = true; }
             else if (lane == 16) { v = msc; set = true; }
@@ -338,25 +350,27 @@ extern "C" int amass_summary_build(const amass_build_args* a, void* stream) {
     if (!a) return AMASS_ERR_NULL;
     if ((!a->k && !a->k_layers) || !a->blocks || !a->rec) return AMASS_ERR_NULL;
     if (a->d != BD || a->page != BP || a->n < 0 || a->n_kv < 1) return AMASS_ERR_GEOMETRY;
-    if (a->kind != 0 && a->kind != 1) return AMASS_ERR_GEOMETRY;
+    if (a->kind < 0 || a->kind > 2) return AMASS_ERR_GEOMETRY;
     if (a->rank < 1 || a->rank > 8) return AMASS_ERR_UNSUPPORTED;
     if (a->v_bits != 8 && a->v_bits != 4) return AMASS_ERR_GEOMETRY;
-    if (a->kind == 1 && a->c_bits != 8 && a->c_bits != 4) return AMASS_ERR_GEOMETRY;
-    if ((a->v_bits == 4 || (a->kind == 1 && a->c_bits == 4)) && (a->rank & 1))
+    if (a->kind >= 1 && a->c_bits != 8 && a->c_bits != 4) return AMASS_ERR_GEOMETRY;
+    if ((a->v_bits == 4 || (a->kind >= 1 && a->c_bits == 4)) && (a->rank & 1))
         return AMASS_ERR_GEOMETRY;
     if (a->tag && (a->tagw < 0 || a->tagw > 64)) return AMASS_ERR_GEOMETRY;
     const int nw = a->n_kv < BW ? a->n_kv : BW;
     if (a->n_kv % nw != 0) return AMASS_ERR_GEOMETRY;
-    const int crow = a->kind == 1 ? a->rank * a->c_bits / 8 : 0;
+    const int crow = a->kind >= 1 ? a->rank * a->c_bits / 8 : 0;
     const int vm = a->rank * (a->v_bits == 8 ? BD : BD / 2) + BD + 16 * crow;
     if (a->rec_sb < (int64_t)a->n_kv * (vm + 64)) return AMASS_ERR_GEOMETRY;
     if (a->n_layers < 1 || (a->n_layers > 1 && !a->k_layers)) return AMASS_ERR_GEOMETRY;
     if (a->n == 0) return AMASS_OK;
     const dim3 grid(a->n, a->n_kv / nw, a->n_layers), blk(nw * WAVE);
     hipStream_t s = (hipStream_t)stream;
-    if (a->kind == 1)
-        hipLaunchKernelGGL(summary_build_kernel<true>, grid, blk, 0, s, *a);
+    if (a->kind == 2)
+        hipLaunchKernelGGL(summary_build_kernel<2>, grid, blk, 0, s, *a);
+    else if (a->kind == 1)
+        hipLaunchKernelGGL(summary_build_kernel<1>, grid, blk, 0, s, *a);
     else
-        hipLaunchKernelGGL(summary_build_kernel<false>, grid, blk, 0, s, *a);
+        hipLaunchKernelGGL(summary_build_kernel<0>, grid, blk, 0, s, *a);
     return check_launch();
 }

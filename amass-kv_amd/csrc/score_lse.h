@@ -1,0 +1,467 @@
+// Low-rank per-key logsumexp page scores for gfx950: r8 and CLSE (the kernel shared by
+// r8_score.hip and clse_score.hip).
+//
+// Math per (request r, kv-head h, page p < n_sel_hi[r]) and GQA head g (reference:
+// selection/score.py:3-16,30-120; int path selection/score_cuda.py:160-448):
+//   q~[g,k]  = (Vk_code[:,k] * Vk_scale[k]) . q_g                       k < r
+//   tok[g,t] = s * c_scale[t] * (c_code[t,:] . q~[g,:])                t < page, 16p+t < seq_len
+//   S_g      = s * (mu_code * mu_scale) . q_g + logsumexp_t tok[g,t]
+//   score    = max_g S_g   (kv-union group max)
+//
+// Front end: the quad kernel's int8 matrix-core product (score_mfma.h) over the page's
+// column-major Vk and its mean codes -- exact int32 sums comb = sum_d qi * code.  For
+// G < 8 the unused M rows repeat the group's limb rows, so lane (kg, n) receives the sums
+// of heads g0 = 2 (kg % GP), g1 = g0 + 1 (GP = max(G/2, 1) head pairs) and the 4 / GP
+// lane groups holding the same pair split the page's 16 tokens between them (TPL tokens
+// each): the token tail needs no exchange of q~, only a max and a sum across those
+// groups for the logsumexp, and a max across pairs for the group max.
+//
+// Layout (AMASS_R8_REC_BYTES per kv head).  Per block, the n_kv heads' records
+// [Vk column-major: r columns of CB bytes | 128 mu codes | c: 16 token rows of
+// r * c_bits / 8 bytes], then the n_kv heads' 64-byte fp16 scale blocks (Vk_scale at
+// half 0, c_scale at halves 8..23, mu_scale at half 24).  Vk int8 column k is CB = 128
+// bytes (byte j = code[j]); int4 CB = 64 with byte j = code[j] | code[j + 64] << 4.  c
+// rows keep the reference order (int4: two columns per byte, low nibble = even column).
+// Each tile is two load groups -- columns [0, r/2) + mu + scales, then [r/2, r) + the
+// lane's c rows -- double-buffered as in the quad kernel.
+//
+// CLSE (reference selection/quad_score.py:156-276, score="clse") is the same computation
+// over the same record (its quad_V / quad_mu / quad_c / c_scale; the residual scatter
+// energy at half 25 of the scale block) plus an isotropic term for the key variance
+// outside the stored subspace:
+//   iso_g = max(|q_g|^2 - |q~_g|^2, 0) * resid * s^2 / (2 P (d - r))
+//   S_g   = s mu.q_g + logsumexp_t tok[g,t] + iso_g ; combine "max" or per head ("nrm").
+// |q_g|^2 comes from the bf16 query in fp32, |q~_g|^2 from the lane's own q~.
+#pragma once
+#include "score_mfma.h"
+
+namespace amass {
+
+constexpr int R8_MAXW = 8;      // waves (kv heads) per workgroup
+
+struct R8Params {
+    const uint16_t* q; int64_t q_st, q_hs;
+    const int8_t* rec; int64_t rec_sb;
+    const int32_t* bt; int64_t bt_st;
+    const int32_t* sl;
+    const int32_t* nsh;
+    float* score; int64_t sc_sr, sc_sh;
+    float* score_h; int64_t sh_sr, sh_sh, sh_sg;   // CLSE per-head output (combine 1)
+    int32_t* comb_out;
+    float scale;
+    float iso_coef;                               // CLSE: s^2 / (2 P (d - r))
+    int combine;                                  // CLSE: 0 group max, 1 per head
+    int n_req, n_kv, page, max_pages;
+    int hw;         // kv heads (waves) per workgroup
+    int target;     // workgroups the batch's tiles are balanced over
+};
+
+template <int RP, int VB, int CBITS>
+struct R8Geom {
+    static constexpr int CB = col_bytes<VB>();
+    static constexpr int CROW = RP * CBITS / 8;          // bytes per token row of c
+    static constexpr int VM = RP * CB + 128 + 16 * CROW; // record bytes before the scales
+};
+
+template <int G>
+struct R8Split {
+    static constexpr int GP = G >= 2 ? G / 2 : 1;       // head pairs over the 4 lane groups
+    static constexpr int TPL = 4 * GP;                  // tokens per lane (16 / (4 / GP))
+};
+
+template <int RP, int VB>
+struct R8GroupA {                         // columns [0, RP/2), mu, the page's scales
+    static constexpr int NC = RP / 2;
+    i32x4_t v[NC * loads_per_col<VB>()];
+    i32x4_t mu[2];
+    i32x4_t meta;                         // 16 bytes kg of the 64-byte scale block
+};
+template <int RP, int VB>
+struct R8GroupB {                         // columns [RP/2, RP)
+    static constexpr int NC = RP - RP / 2;
+    i32x4_t v[NC * loads_per_col<VB>()];
+};
+template <int CL>
+struct R8GroupC {                         // the lane's c rows
+    uint32_t c[CL / 4];
+};
+
+template <int RP, int VB>
+__device__ __forceinline__ void r8_load_a(const int8_t* lr, R8GroupA<RP, VB>& a, int moff) {
+    constexpr int CB = col_bytes<VB>();
+#pragma unroll
+    for (int c = 0; c < R8GroupA<RP, VB>::NC; ++c) {
+        if constexpr (VB == 8) {
+            a.v[2 * c] = ld16(lr + c * CB);
+            a.v[2 * c + 1] = ld16(lr + c * CB + 64);
+        } else {
+            a.v[c] = ld16(lr + c * CB);
+        }
+    }
+    a.mu[0] = ld16(lr + RP * CB);
+    a.mu[1] = ld16(lr + RP * CB + 64);
+    a.meta = ld16(lr + moff);
+}
+
+template <int RP, int VB>
+__device__ __forceinline__ void r8_load_b(const int8_t* lr, R8GroupB<RP, VB>& b) {
+    constexpr int CB = col_bytes<VB>();
+    constexpr int C0 = RP / 2;
+#pragma unroll
+    for (int c = 0; c < R8GroupB<RP, VB>::NC; ++c) {
+        if constexpr (VB == 8) {
+            b.v[2 * c] = ld16(lr + (C0 + c) * CB);
+            b.v[2 * c + 1] = ld16(lr + (C0 + c) * CB + 64);
+        } else {
+            b.v[c] = ld16(lr + (C0 + c) * CB);
+        }
+    }
+}
+
+template <int CL>
+__device__ __forceinline__ void r8_load_c(const int8_t* cp, R8GroupC<CL>& g) {
+    if constexpr (CL >= 16) {
+#pragma unroll
+        for (int i = 0; i < CL / 16; ++i) {
+            const i32x4_t x = ld16(cp + 16 * i);
+            g.c[4 * i] = (uint32_t)x[0]; g.c[4 * i + 1] = (uint32_t)x[1];
+            g.c[4 * i + 2] = (uint32_t)x[2]; g.c[4 * i + 3] = (uint32_t)x[3];
+        }
+    } else if constexpr (CL == 8) {
+        const uint2 x = *reinterpret_cast<const uint2*>(cp);
+        g.c[0] = x.x; g.c[1] = x.y;
+    } else {                              // CL == 4 (r = 2, int4 c, G <= 2)
+        g.c[0] = *reinterpret_cast<const uint32_t*>(cp);
+    }
+}
+
+// fp16 scales of one page for this lane: Vk_scale (from lane group 0), mu_scale (group 3)
+// and the c_scale of the lane's TPL tokens (groups 1 and 2 hold tokens 0..7 / 8..15).
+template <int RP, int TPL>
+struct R8Scales {
+    uint32_t vs[4];
+    float mus;
+    float resid;                          // CLSE residual energy (half 25)
+    float cs[TPL];
+};
+
+template <int RP, int TPL>
+__device__ __forceinline__ R8Scales<RP, TPL> r8_gather_scales(i32x4_t meta, int n, int part) {
+    R8Scales<RP, TPL> s;
+    constexpr int NW = RP / 2;            // dwords holding r halves
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.vs[i] = i < NW ? (uint32_t)__shfl(meta[i], n, WAVE) : 0u;
+    const uint32_t w24 = (uint32_t)__shfl(meta[0], n + 48, WAVE);   // halves 24, 25
+    s.mus = fp16_to_f32((uint16_t)(w24 & 0xFFFFu));
+    s.resid = fp16_to_f32((uint16_t)(w24 >> 16));
+    if constexpr (TPL == 16) {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[i] = (uint32_t)__shfl(meta[i], n + 16, WAVE);
+            w[4 + i] = (uint32_t)__shfl(meta[i], n + 32, WAVE);
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            s.cs[t] = fp16_to_f32((uint16_t)((w[t >> 1] >> (16 * (t & 1))) & 0xFFFFu));
+    } else {
+        const int t0 = part * TPL;        // first token of the lane
+        const int src = n + 16 * (1 + (t0 >> 3));
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (uint32_t)__shfl(meta[i], src, WAVE);
+        if constexpr (TPL == 8) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                s.cs[t] = fp16_to_f32((uint16_t)((w[t >> 1] >> (16 * (t & 1))) & 0xFFFFu));
+        } else {                          // TPL == 4: tokens t0 % 8 .. + 4 of the source
+            const bool up = (t0 & 7) != 0;
+            const uint32_t x0 = up ? w[2] : w[0], x1 = up ? w[3] : w[1];
+            s.cs[0] = fp16_to_f32((uint16_t)(x0 & 0xFFFFu));
+            s.cs[1] = fp16_to_f32((uint16_t)(x0 >> 16));
+            s.cs[2] = fp16_to_f32((uint16_t)(x1 & 0xFFFFu));
+            s.cs[3] = fp16_to_f32((uint16_t)(x1 >> 16));
+        }
+    }
+    return s;
+}
+
+// q~ of the lane's two heads (e = 0: g0, e = 1: g1) and their mu terms.
+template <int RP>
+struct R8Acc {
+    float qt[2][RP];
+    float qmu[2];
+};
+
+template <int RP>
+__device__ __forceinline__ int32_t* r8_comb_row(const R8Params& p, int G, int req, int h,
+                                                int page, int g) {
+    return p.comb_out + (((int64_t)req * p.n_kv + h) * p.max_pages + page) * (G * (RP + 1)) +
+           (int64_t)g * (RP + 1);
+}
+
+template <int NC, int VB, int RP>
+__device__ __forceinline__ void r8_cols(const i32x4_t (&qa)[2], const i32x4_t* v,
+                                        const uint32_t (&vs)[4], int col0, float qs0, float qs1,
+                                        R8Acc<RP>& acc, int32_t* co0, int32_t* co1) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int x[2];
+        comb2<VB>(col_mfma<VB>(qa, &v[c * loads_per_col<VB>()]), x[0], x[1]);
+        const float vsc = half_at(vs, col0 + c);
+        acc.qt[0][col0 + c] = (float)x[0] * qs0 * vsc;
+        acc.qt[1][col0 + c] = (float)x[1] * qs1 * vsc;
+        if (co0) co0[col0 + c] = x[0];
+        if (co1) co1[col0 + c] = x[1];
+    }
+}
+
+template <int RP, int VB, int G, bool COMB>
+__device__ __forceinline__ void r8_tile_start(const R8Params& p, const i32x4_t (&qa)[2],
+                                              const R8GroupA<RP, VB>& a,
+                                              const R8Scales<RP, R8Split<G>::TPL>& sc, float qs0,
+                                              float qs1, R8Acc<RP>& acc, int req, int h,
+                                              int page, bool valid, int pair, int part) {
+    const bool co_on = COMB && valid && part == 0;
+    int32_t* co0 = co_on ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair) : nullptr;
+    int32_t* co1 = (co_on && G >= 2) ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair + 1)
+                                     : nullptr;
+    r8_cols<RP / 2, VB, RP>(qa, a.v, sc.vs, 0, qs0, qs1, acc, co0, co1);
+    i32x4_t m = {0, 0, 0, 0};
+    m = mfma_i8(qa[0], a.mu[0], m);
+    m = mfma_i8(qa[1], a.mu[1], m);
+    const int cmu[2] = {m[0] * 128 + m[1], m[2] * 128 + m[3]};
+    acc.qmu[0] = (float)cmu[0] * qs0 * sc.mus * p.scale;
+    acc.qmu[1] = (float)cmu[1] * qs1 * sc.mus * p.scale;
+    if (co0) co0[RP] = cmu[0];
+    if (co1) co1[RP] = cmu[1];
+}
+
+// signed code k of token row t of the lane's c words
+template <int RP, int CBITS>
+__device__ __forceinline__ float c_code(const uint32_t* cw, int t, int k) {
+    constexpr int CROW = RP * CBITS / 8;
+    if constexpr (CBITS == 8) {
+        const int byte = t * CROW + k;
+        return (float)(((int)(cw[byte >> 2] << (24 - 8 * (byte & 3)))) >> 24);
+    } else {
+        const int nib = t * 2 * CROW + k;       // low nibble = even column
+        return (float)(((int)(cw[nib >> 3] << (28 - 4 * (nib & 7)))) >> 28);
+    }
+}
+
+template <int RP, int VB, int G, bool COMB>
+__device__ __forceinline__ void r8_tile_mid(const R8Params& p, const i32x4_t (&qa)[2],
+                                            const R8GroupB<RP, VB>& b,
+                                            const R8Scales<RP, R8Split<G>::TPL>& sc, float qs0,
+                                            float qs1, R8Acc<RP>& acc, int req, int h, int page,
+                                            bool valid, int pair, int part) {
+    const bool co_on = COMB && valid && part == 0;
+    int32_t* co0 = co_on ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair) : nullptr;
+    int32_t* co1 = (co_on && G >= 2) ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair + 1)
+                                     : nullptr;
+    r8_cols<RP - RP / 2, VB, RP>(qa, b.v, sc.vs, RP / 2, qs0, qs1, acc, co0, co1);
+}
+
+template <int RP, int CBITS, int G, bool CLSE>
+__device__ __forceinline__ void r8_tile_tail(const R8Params& p,
+                                             const R8GroupC<R8Split<G>::TPL * RP * CBITS / 8>& b,
+                                             const R8Scales<RP, R8Split<G>::TPL>& sc,
+                                             const R8Acc<RP>& acc, int req, int h, int page,
+                                             bool valid, int pair, int part, int kg, int sl,
+                                             float qsq0, float qsq1) {
+    constexpr int TPL = R8Split<G>::TPL;
+    constexpr int GP = R8Split<G>::GP;
+    // token logits of the lane's TPL tokens for both heads
+    const int tok0 = page * p.page + part * TPL;
+    float lg[2][TPL];
+#pragma unroll
+    for (int t = 0; t < TPL; ++t) {
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < RP; ++k) {
+            const float cf = c_code<RP, CBITS>(b.c, t, k);
+            a0 += cf * acc.qt[0][k];
+            a1 += cf * acc.qt[1][k];
+        }
+        const float f = p.scale * sc.cs[t];
+        const bool live = tok0 + t < sl;
+        lg[0][t] = live ? a0 * f : -INFINITY;
+        lg[1][t] = live ? a1 * f : -INFINITY;
+    }
+    float S[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        float m = lg[e][0];
+#pragma unroll
+        for (int t = 1; t < TPL; ++t) m = fmaxf(m, lg[e][t]);
+        if constexpr (GP == 2) m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+        if constexpr (GP == 1) {
+            m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+            m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+        }
+        const float mm = m == -INFINITY ? 0.f : m;
+        float se = 0.f;
+#pragma unroll
+        for (int t = 0; t < TPL; ++t) se += __expf(lg[e][t] - mm);
+        if constexpr (GP == 2) se += __shfl_xor(se, 32, WAVE);
+        if constexpr (GP == 1) {
+            se += __shfl_xor(se, 16, WAVE);
+            se += __shfl_xor(se, 32, WAVE);
+        }
+        S[e] = acc.qmu[e] + (m + __logf(se));
+        if constexpr (CLSE) {
+            float qh = 0.f;
+#pragma unroll
+            for (int k = 0; k < RP; ++k) qh += acc.qt[e][k] * acc.qt[e][k];
+            S[e] += fmaxf((e ? qsq1 : qsq0) - qh, 0.f) * sc.resid * p.iso_coef;
+        }
+    }
+    if (CLSE && p.combine == 1) {             // per-head scores (the nrm combine's input)
+        if (valid && part == 0) {
+            const int64_t row = (int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh + page;
+            p.score_h[row + (int64_t)(2 * pair) * p.sh_sg] = S[0];
+            if (G >= 2) p.score_h[row + (int64_t)(2 * pair + 1) * p.sh_sg] = S[1];
+        }
+        return;
+    }
+    float smax = G >= 2 ? fmaxf(S[0], S[1]) : S[0];
+    if constexpr (GP == 4) {
+        smax = fmaxf(smax, __shfl_xor(smax, 16, WAVE));
+        smax = fmaxf(smax, __shfl_xor(smax, 32, WAVE));
+    }
+    if constexpr (GP == 2) smax = fmaxf(smax, __shfl_xor(smax, 16, WAVE));
+    if (valid && kg == 0) p.score[(int64_t)req * p.sc_sr + (int64_t)h * p.sc_sh + page] = smax;
+}
+
+// COMB: also write the int32 contractions to comb_out (a test entry).  CLSE: the CLSE
+// score (iso term, optional per-head output) instead of r8.
+template <int RP, int VB, int CBITS, int G, bool COMB, bool CLSE>
+__global__ __launch_bounds__(R8_MAXW * WAVE)
+void r8_score_kernel(const R8Params p) {
+    using Geo = R8Geom<RP, VB, CBITS>;
+    constexpr int VM = Geo::VM;
+    constexpr int TPL = R8Split<G>::TPL;
+    constexpr int GP = R8Split<G>::GP;
+    constexpr int CL = TPL * Geo::CROW;              // c bytes per lane
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, kg = lane >> 4;
+    const int pair = kg % GP, part = kg / GP;
+    const int h = blockIdx.y * p.hw + wave;
+    TileWalk tw;
+    if (!tile_walk(p.nsh, p.n_req, p.target, blockIdx.x, tw) || tw.count <= 0) return;
+    const int req = tw.req;
+    const int nsh = p.nsh[req];
+    const int sl = p.sl[req];
+    const int cnt = tw.count;
+    const int t0 = tw.first;
+    const int wstride = tw.stride;
+
+    uint32_t qw[2][8];
+    load_q_rows(p.q, p.q_st, p.q_hs, req, h, G, n, kg, true, qw);
+
+    auto page_of = [&](int tile) { return tile * SC_TILE + n; };
+    auto lane_blk = [&](int tile) -> int64_t {
+        const int page = page_of(tile);
+        const int pc = page < nsh ? page : nsh - 1;
+        return (int64_t)p.bt[(int64_t)req * p.bt_st + pc];
+    };
+    const int64_t rhead = (int64_t)h * VM + 16 * kg;
+    const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
+    const int coff = RP * Geo::CB + 128 + part * CL - 16 * kg;
+    auto lane_rec = [&](int64_t blk) { return p.rec + blk * p.rec_sb + rhead; };
+
+    // Three load groups per tile, each refilled right after its last use: A (columns
+    // [0, r/2), mu, scales) and B (columns [r/2, r)) are consumed by the matrix-core
+    // product, C (the lane's c rows) by the token tail, so both column groups of the next
+    // tile are in flight during this tile's tail.
+    int tile = t0;
+    const int8_t* lr = lane_rec(lane_blk(tile));
+    R8GroupA<RP, VB> ga;
+    R8GroupB<RP, VB> gb;
+    R8GroupC<CL> gc;
+    r8_load_a<RP, VB>(lr, ga, moff);
+    int64_t bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
+    __builtin_amdgcn_sched_barrier(0);
+    r8_load_b<RP, VB>(lr, gb);
+    __builtin_amdgcn_sched_barrier(0);
+    r8_load_c<CL>(lr + coff, gc);
+
+    i32x4_t qa[2];
+    const float qs = quantize_q_rows(qw, n, qa);
+    const float qs0 = __shfl(qs, 4 * kg, WAVE);        // row 4kg: limb hi of g0
+    const float qs1 = __shfl(qs, 4 * kg + 2, WAVE);
+    float qsq0 = 0.f, qsq1 = 0.f;                      // CLSE: |q_g0|^2, |q_g1|^2 (fp32)
+    if constexpr (CLSE) {
+        float ss = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float lo = bf16lo(qw[t][i]), hi = bf16hi(qw[t][i]);
+                ss += lo * lo + hi * hi;
+            }
+        ss += __shfl_xor(ss, 16, WAVE);                // the row's four 32-d quarters
+        ss += __shfl_xor(ss, 32, WAVE);
+        qsq0 = __shfl(ss, 4 * kg, WAVE);               // rows 4kg, 4kg+2: g0, g1
+        qsq1 = __shfl(ss, 4 * kg + 2, WAVE);
+    }
+
+    R8Acc<RP> acc;
+    for (int i = 0; i + 1 < cnt; ++i) {
+        const int page = page_of(tile);
+        const bool valid = page < nsh;
+        const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part);
+        r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, pair,
+                                       part);
+        __builtin_amdgcn_sched_barrier(0);
+        const int8_t* ln = lane_rec(bn_next);
+        r8_load_a<RP, VB>(ln, ga, moff);
+        bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
+        r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, req, h, page, valid, pair,
+                                     part);
+        __builtin_amdgcn_sched_barrier(0);
+        r8_load_b<RP, VB>(ln, gb);
+        r8_tile_tail<RP, CBITS, G, CLSE>(p, gc, sc, acc, req, h, page, valid, pair, part, kg, sl,
+                                         qsq0, qsq1);
+        __builtin_amdgcn_sched_barrier(0);
+        r8_load_c<CL>(ln + coff, gc);
+        tile += wstride;
+    }
+    const int page = page_of(tile);
+    const bool valid = page < nsh;
+    const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part);
+    r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, pair, part);
+    r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, req, h, page, valid, pair, part);
+    r8_tile_tail<RP, CBITS, G, CLSE>(p, gc, sc, acc, req, h, page, valid, pair, part, kg, sl,
+                                     qsq0, qsq1);
+}
+
+template <int RP, int VB, int CBITS, int G, bool COMB, bool CLSE>
+static int launch_r8_k(R8Params p, hipStream_t s) {
+    auto k = r8_score_kernel<RP, VB, CBITS, G, COMB, CLSE>;
+    int cus = 0, per_cu = 1;
+    p.hw = pick_heads((const void*)k, p.n_kv, per_cu, cus);
+    const int hg = p.n_kv / p.hw;
+    p.target = score_target(per_cu * cus, hg);
+    hipLaunchKernelGGL(k, dim3(p.target + p.n_req, hg), dim3(p.hw * WAVE), 0, s, p);
+    return check_launch();
+}
+
+template <int RP, int VB, int CBITS, bool CLSE>
+static int launch_r8_g(const R8Params& p, int G, bool comb, hipStream_t s) {
+    switch (G) {
+        case 1: return comb ? launch_r8_k<RP, VB, CBITS, 1, true, CLSE>(p, s)
+                            : launch_r8_k<RP, VB, CBITS, 1, false, CLSE>(p, s);
+        case 2: return comb ? launch_r8_k<RP, VB, CBITS, 2, true, CLSE>(p, s)
+                            : launch_r8_k<RP, VB, CBITS, 2, false, CLSE>(p, s);
+        case 4: return comb ? launch_r8_k<RP, VB, CBITS, 4, true, CLSE>(p, s)
+                            : launch_r8_k<RP, VB, CBITS, 4, false, CLSE>(p, s);
+        case 8: return comb ? launch_r8_k<RP, VB, CBITS, 8, true, CLSE>(p, s)
+                            : launch_r8_k<RP, VB, CBITS, 8, false, CLSE>(p, s);
+    }
+    return AMASS_ERR_GEOMETRY;
+}
+
+}  // namespace amass

@@ -17,11 +17,12 @@ Inputs are synthetic (amass.bench.synth, seeded) and resident in HBM before timi
 Secondary lines (under "configs"; skipped with --quick): config 1 with the key-norm boost,
 config 2 (r8, 64 ragged sequences, 5 % budget), config 3 (G = 8, 131072 tokens, coverage
 0.95, split-K path) and config 4 (mem-v, 64 steps from a cold hot buffer, both boosts),
-each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s; and the HIP
-page-summary builder (bulk build and steady-state tail rebuild at config 1).
+each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s; the CLSE
+score (the reference's default score) at the config-1 shape; and the HIP page-summary
+builder (bulk build and steady-state tail rebuild at config 1).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--quick]
-                  [--configs 1k,2,3,4]
+                  [--configs 1k,clse,2,3,4,build]
 """
 from __future__ import annotations
 
@@ -120,6 +121,19 @@ def r8_score_bytes(st, n_req, G):
     return units * (rec + 4) + int(nsh.sum()) * 4 + n_req * st.n_kv * G * st.d * 2
 
 
+def clse_score_bytes(st, n_req, G):
+    """Algorithmic HBM bytes of one CLSE-score launch: per scored (page, kv-head) V
+    d*r'*vb/8 + mu d + c page*r'*cb/8 + V_scale 2r' + c_scale (2 per token or 2) +
+    mu_scale 2 + resid 2, plus the block table, q and the score writes (nrm: G floats)."""
+    nsh = st.n_sel_hi[:n_req].clamp_min(0).long()
+    units = int(nsh.sum()) * st.n_kv
+    cs = 2 * st.page if st.c_grain == "token" else 2
+    rec = (st.d * st.r * st.v_bits // 8 + st.d + st.page * st.r * st.c_bits // 8
+           + 2 * st.r + cs + 2 + 2)
+    out = 4 * (G if st.combine == "nrm" else 1)
+    return units * (rec + out) + int(nsh.sum()) * 4 + n_req * st.n_kv * G * st.d * 2
+
+
 def select_bytes(st, n_req, G):
     """score_h read (G floats per record; G = 0 when the score is read instead) + score
     write (or read) + page_table + page_cnt."""
@@ -199,8 +213,9 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
 
     from amass.attention.decode import (ResidentVSource, dense_paged_decode,
                                         sparse_paged_decode_batched)
-    from amass.selection import derive_page_params, select_pages_quad, select_pages_r8
-    from amass.selection.quad_score import quad_score_launch
+    from amass.selection import (derive_page_params, select_pages_clse, select_pages_quad,
+                                 select_pages_r8)
+    from amass.selection.quad_score import clse_score, quad_score_launch
     from amass.selection.score import r8_score
     from amass.selection.select import select_pages
 
@@ -211,11 +226,13 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     out = torch.zeros(B, n_kv * G, 128, dtype=torch.bfloat16, device=q.device)
     out_d = torch.zeros_like(out)
     vsrc = ResidentVSource(kv)
-    nrm = score == "quad" and st.combine == "nrm"
+    nrm = score in ("quad", "clse") and st.combine == "nrm"
 
     def stage_a():
         if score == "quad":
             select_pages_quad(st, 0, q, bt, sl, B, case.scale, derive=False)
+        elif score == "clse":
+            select_pages_clse(st, 0, q, bt, sl, B, case.scale, derive=False)
         else:
             select_pages_r8(st, 0, q, bt, sl, B, case.scale, derive=False)
 
@@ -229,6 +246,8 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     def score_only():
         if score == "quad":
             quad_score_launch(st, 0, q, bt, B, case.scale)
+        elif score == "clse":
+            clse_score(st, 0, q, bt, sl, B, case.scale)
         else:
             r8_score(st, 0, q, bt, sl, B, case.scale)
 
@@ -254,11 +273,12 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     S_all = (st.n_sel_hi[:B] - st.sink_pages).clamp_min(0).double()
     frac = float(st.n_sel[:B].double().sum() / (S_all.sum() * n_kv))
     att_frac = float(cnt.double().sum() / (st.n_pages[:B].double().sum() * n_kv))
-    b_score = (quad_score_bytes if score == "quad" else r8_score_bytes)(st, B, G)
+    b_score = {"quad": quad_score_bytes, "r8": r8_score_bytes,
+               "clse": clse_score_bytes}[score](st, B, G)
     b_sel = select_bytes(st, B, G if nrm else 0)
     b_att = attend_bytes(cnt, B, n_kv, G)
     b_dense = attend_bytes(st.n_pages[:B][:, None].expand(B, n_kv), B, n_kv, G)
-    sname = "quad_score" if score == "quad" else "r8_score"
+    sname = f"{score}_score"
     kernels = {sname: kernel_entry(us_score, b_score, traffic.get(sname)),
                ("select_nrm_coverage" if nrm else "select"):
                    kernel_entry(us_sel, b_sel, traffic.get("select_nrm_coverage")),
@@ -293,6 +313,21 @@ def run_secondary(idx, args, boost="sigma"):
                           if isinstance(cfg["ctx"], tuple) else f"{cfg['ctx']}")
                        + f" G={case.G} {cfg['score']} r=8 int8, {sel}, boost {boost}")
     log(f"config {idx}: sparse {res['us']} us, dense {res['dense_us']} us")
+    return res
+
+
+def run_clse(args, boost="sigma"):
+    """The reference's default score (score="clse": quad storage r'=2 int4 + per-token int4
+    coordinates + residual energy, nrm combine) at the config-1 shape, coverage 0.95."""
+    from amass.bench.synth import build_quad_state, config_case
+
+    case = config_case(1, seed=args.seed, device="cuda", boost=boost)
+    st = build_quad_state(case, rank=2, v_bits=4, combine="nrm", coverage=0.95,
+                          coords="lse", c_bits=4, c_grain="token")
+    res = measure_step(case, st, args, score="clse")
+    res["workload"] = (f"config1 shape: B=32 ctx 16384 G=4, CLSE r'=2 int4 V + int4 per-token "
+                       f"coords, nrm, coverage 0.95, boost {boost}")
+    log(f"clse ({boost}): sparse {res['us']} us, dense {res['dense_us']} us")
     return res
 
 
@@ -427,9 +462,10 @@ def main():
     ap.add_argument("--boost", default="sigma", choices=["sigma", "keynorm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
-    ap.add_argument("--configs", default="1k,2,3,4,build",
-                    help="secondary lines: 1k (config 1 with the key-norm boost), 2, 3, 4, "
-                         "build (the HIP summary builder)")
+    ap.add_argument("--configs", default="1k,clse,2,3,4,build",
+                    help="secondary lines: 1k (config 1 with the key-norm boost), clse (the "
+                         "CLSE score at the config-1 shape), 2, 3, 4, build (the HIP "
+                         "summary builder)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB read + 256 MiB write kernel (HBM counter calibration)")
     args = ap.parse_args()
@@ -529,6 +565,10 @@ def main():
                 sec[f"config{c}"] = run_secondary(int(c), args)
             elif c == "build":
                 sec["summary_build"] = run_summary_build(args)
+            elif c == "clse":
+                sec["config1_clse"] = run_clse(args)
+                free_gpu()
+                sec["config1_clse_keynorm"] = run_clse(args, "keynorm")
             elif c == "4":
                 sec["config4_memv"] = run_config4(args, "sigma")
                 free_gpu()

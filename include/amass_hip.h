@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 3
+#define AMASS_ABI_VERSION 4
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -105,7 +105,8 @@ int amass_r8_score(const amass_r8_score_args* a, void* stream);
 /* ---- page-summary builder ---------------------------------------------------------- */
 /* Replaces the summary math of selection/quad_build.py:124-198 (quad_build_refresh) and
  * selection/build.py:396-632 (_page_eigh, _r8_write, the *_build_{refresh,tail,bulk,delta}
- * op chains) and the jacobi_eigh16 kernels of selection/build.py:84-242.  For each
+ * op chains), the CLSE extras of selection/quad_build.py:38-54 (_clse_extras) and the
+ * jacobi_eigh16 kernels of selection/build.py:84-242.  For each
  * physical block blocks[i] and kv head h of the K view (16-token pages, d = 128):
  * mu = mean_t K, dc = K - mu, Gm = dc dc^T, eigh(Gm) (parallel Jacobi, fp32), the top-r
  * eigenpairs (S2r = max(eig, 1e-10), ascending), Vk = dc^T U8 / sqrt(S2r) and, for r8,
@@ -113,7 +114,10 @@ int amass_r8_score(const amass_r8_score_args* a, void* stream);
  * clamp(rint(x / s), +-lvl), scale stored as fp16(s) (mu per head; Vk per column for
  * v_grain 0 or per head for 1; c per token for c_grain 0 or per head for 1).  Writes the
  * block's packed record (kind 0: quad, AMASS_QUAD_REC_BYTES layout with sig2 = fp16(S2r);
- * kind 1: r8, AMASS_R8_REC_BYTES layout) and, if tag != NULL, the content tag
+ * kind 1: r8, AMASS_R8_REC_BYTES layout; kind 2: CLSE, the r8 layout plus the residual
+ * scatter energy resid = max(trace(Gm) - sum S2r, 0) as fp16 at half 25, c_grain 0 per
+ * token / 1 one scale per head written to all 16 c_scale halves) and, if tag != NULL,
+ * the content tag
  * K[page-1][h][0:tagw].  rank 1..8 (even for int4 codes).  n_layers layers in one launch:
  * layer l reads K at k_layers[l] (a device array of base addresses; k itself when
  * n_layers == 1 and k_layers == NULL), with the same strides, and writes rec + l*rec_lsb,
@@ -127,6 +131,33 @@ typedef struct amass_build_args {
     int32_t n, n_layers, n_kv, d, page, kind, rank, v_bits, c_bits, v_grain, c_grain, tagw;
 } amass_build_args;
 int amass_summary_build(const amass_build_args* a, void* stream);
+
+/* ---- CLSE page score (quad storage + per-key coordinates) -------------------------- */
+/* Replaces clse_score (selection/quad_score.py:156-393, the reference's default score) and
+ * its hand-CUDA clse_score_cuda (backend/_runtime.py:214-229).  Per (request, kv-head,
+ * page p < n_sel_hi) and group head g, over the record of AMASS_R8_REC_BYTES layout
+ * (quad_V column-major | quad_mu | quad_c rows; scale block: V_scale half 0, c_scale halves
+ * 8..23 (a per-page "page" grain scale repeated 16 times), mu_scale half 24, quad_resid
+ * half 25):
+ *   q~[g,k] = (V_code[:,k] V_scale[k]) . q_g ; tok[g,t] = s c_scale[t] (c_code[t,:] . q~[g])
+ *   iso[g]  = max(|q_g|^2 - |q~[g]|^2, 0) * resid * s^2 / (2 page max(d - r', 1))
+ *   S_g = s mu.q_g + logsumexp_{t : 16p+t < seq_len} tok[g,t] + iso[g]
+ * combine 0: score[r,kh,p] = max_g S_g; combine 1: score_h[r,kh,g,p] = S_g (the input of
+ * the nrm combine fused into amass_coverage_select / amass_topb_select).  rank 2, 4 or 8;
+ * comb_out as for amass_r8_score. */
+typedef struct amass_clse_score_args {
+    const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
+    const int8_t*  rec;      int64_t rec_sb;         /* (NB,n_kv,REC) summary records   */
+    const int32_t* block_table; int64_t bt_st;
+    const int32_t* seq_lens;                         /* (R,) int32                      */
+    const int32_t* n_sel_hi;                         /* (R,) int32                      */
+    float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32, combine 0     */
+    float*         score_h;  int64_t sh_sr, sh_sh, sh_sg; /* (R,n_kv,G,MP), combine 1  */
+    int32_t*       comb_out; /* optional (R,n_kv,MP,G,r+1) exact int32 sums; NULL = off */
+    float          scale;
+    int32_t n_req, n_kv, G, d, page, rank, v_bits, c_bits, max_pages, combine;
+} amass_clse_score_args;
+int amass_clse_score(const amass_clse_score_args* a, void* stream);
 
 /* ---- per-step derived page parameters --------------------------------------------- */
 /* Replaces selection/select.py:30-54 (_derive_params_kernel / derive_page_params):

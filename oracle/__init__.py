@@ -16,6 +16,8 @@ Modules and what pins each function (beyond "it restates the reference"):
              nrm_combine (quad_score.py:276-315)        pinned: hand-computed small case
              r8_score (score.py:30-120)                 pinned: = logsumexp of the true page
                                                         logits when the page rank <= r
+             clse_score (quad_score.py:156-276)         pinned: == r8_score at resid 0; iso
+                                                        term on a hand-built page; nrm/max
   select.py  derive (select.py:30-45)                   pinned: config-0 known answer b=13
              topb (select.py:60-101 + tie rule)         pinned: sorted() brute force
              nucleus (build spec; bridge :117-133)      pinned: minimality brute force
@@ -28,6 +30,8 @@ Modules and what pins each function (beyond "it restates the reference"):
                                                         rank <= r, sig2 == svd(dc)^2,
                                                         Vk orthonormal, rank-1 page by hand
              quad_summary / r8_summary (quant rules)    pinned: via quant + the factors
+             clse_summary (quad_build.py:38-54)         pinned: resid == energy beyond the
+                                                        top r' singular values
   tier.py    plan (residency.py:45-139)                 pinned: hand-worked LRU example,
                                                         page2slot/slot2page inverse,
                                                         victims are the oldest untouched

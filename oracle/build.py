@@ -64,3 +64,23 @@ def r8_summary(K, rank: int, vk_bits: int = 8, c_bits: int = 8, vk_grain: str = 
     cs = np.broadcast_to(cs, c.shape[:-1] + (1,))[..., 0]
     return dict(mu=mu_code, mu_scale=mu_s[..., 0], Vk=V, Vk_scale=Vs,
                 c=pack_i4(c_code) if c_bits == 4 else c_code, c_scale=cs)
+
+
+def clse_summary(K, rank: int, v_bits: int = 8, c_bits: int = 4, c_grain: str = "token",
+                 v_grain: str = "col"):
+    """CLSE summary (reference selection/quad_build.py:38-54 _clse_extras + the quad
+    summary): quad's mu / V / V_scale, c = U8 S8 quantised per token ("token") or per
+    (block, head) ("page"), resid = max(trace - sum S2r, 0) (the scatter energy outside
+    the top-r' subspace; trace = the sum of all eigenvalues).  c_scale is (N, n_kv, page)
+    for "token" and (N, n_kv) for "page"."""
+    mu, dc, S2r, U8, Vk = page_factors(K, rank)
+    out = quad_summary(K, rank, v_bits, v_grain)
+    del out["sig2"]
+    c = (U8 * np.sqrt(S2r)[..., None, :]).astype(np.float32)
+    axis = -1 if c_grain == "token" else (-2, -1)
+    c_code, cs = quant(c, axis=axis, bits=c_bits)
+    out["c"] = pack_i4(c_code) if c_bits == 4 else c_code
+    out["c_scale"] = cs[..., 0] if c_grain == "token" else cs[..., 0, 0]
+    trace = (dc * dc).sum(axis=(-2, -1))
+    out["resid"] = np.maximum(trace - S2r.sum(-1), 0.0)
+    return out

@@ -122,3 +122,49 @@ def r8_score(q, mu, mu_scale, Vk, Vk_scale, c, c_scale, block_table, seq_lens, n
         S = scale * np.einsum("kgd,nkd->nkg", qr, mud) + lse
         out[r, :, :n] = S.max(axis=-1).T
     return out
+
+
+def clse_score(q, mu, mu_scale, V, V_scale, c, c_scale, resid, block_table, seq_lens,
+               n_sel_hi, *, scale, page, G, v_bits, c_bits, max_pages, combine="max",
+               q_mode="float"):
+    """CLSE score (reference selection/quad_score.py:156-276, _clse_score_kernel) in
+    float64: q~ = V^T q_g (dequantised V), tok = s (c q~) with c dequantised per token
+    (c_scale (NB, n_kv, page)) or per page (c_scale (NB, n_kv)), masked logsumexp over the
+    tokens, iso = max(|q_g|^2 - |q~|^2, 0) resid s^2 / (2 page max(d - r', 1)),
+    S_g = s mu.q_g + lse + iso.  -> (R, n_kv, MP) group max ("max") or (R, n_kv, G, MP)
+    per head ("nrm"); NaN beyond n_sel_hi."""
+    R = len(n_sel_hi)
+    n_kv, d = mu.shape[1], mu.shape[-1]
+    r = np.asarray(V_scale).shape[-1]
+    iso_coef = scale * scale / (2.0 * page * max(d - r, 1))
+    shape = (R, n_kv, max_pages) if combine == "max" else (R, n_kv, G, max_pages)
+    out = np.full(shape, np.nan)
+    token_grain = np.asarray(c_scale).ndim == 3
+    for rq in range(R):
+        n = int(n_sel_hi[rq])
+        if n <= 0:
+            continue
+        blk = np.asarray(block_table[rq, :n], np.int64)
+        Vd = codes(V[blk], v_bits).astype(np.float64) * \
+            np.asarray(V_scale[blk], np.float64)[:, :, None, :]
+        cs = np.asarray(c_scale[blk], np.float64)
+        cd = codes(c[blk], c_bits).astype(np.float64) * \
+            (cs[..., None] if token_grain else cs[..., None, None])          # (n,kv,P,r)
+        mud = mu[blk].astype(np.float64) * np.asarray(mu_scale[blk], np.float64)[..., None]
+        qr = _q(q[rq], q_mode).reshape(n_kv, G, -1)
+        qt = np.einsum("kgd,nkdr->nkgr", qr, Vd)
+        tok = scale * np.einsum("nktr,nkgr->nkgt", cd, qt)
+        pos = np.arange(n)[:, None] * page + np.arange(page)[None, :]
+        tok = np.where((pos < int(seq_lens[rq]))[:, None, None, :], tok, -np.inf)
+        m = tok.max(axis=-1, keepdims=True)
+        lse = (m + np.log(np.exp(tok - m).sum(axis=-1, keepdims=True)))[..., 0]
+        qsq = (qr * qr).sum(-1)                                             # (kv, G)
+        qhsq = (qt * qt).sum(-1)                                            # (n, kv, G)
+        iso = np.maximum(qsq[None] - qhsq, 0.0) * \
+            np.asarray(resid[blk], np.float64)[..., None] * iso_coef
+        S = scale * np.einsum("kgd,nkd->nkg", qr, mud) + lse + iso           # (n, kv, G)
+        if combine == "max":
+            out[rq, :, :n] = S.max(axis=-1).T
+        else:
+            out[rq, :, :, :n] = S.transpose(1, 2, 0)
+    return out

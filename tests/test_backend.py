@@ -65,7 +65,7 @@ def test_disable_env_makes_register_inert(vllm, monkeypatch):
     ({}, "UNIFORM_SINGLE_TOKEN_DECODE"),
     ({"force_eager": True}, "NEVER"),
     ({"variant": "mem-v"}, "NEVER"),
-    ({"score": "clse"}, "NEVER"),
+    ({"score": "clse"}, "UNIFORM_SINGLE_TOKEN_DECODE"),
     ({"score": "r8"}, "UNIFORM_SINGLE_TOKEN_DECODE"),
 ])
 def test_cudagraph_support(vllm, cfg, want):

@@ -109,3 +109,15 @@ def test_torch_host_builder_matches_oracle(kind):
     got, _ = _align(Vref, V[blocks].astype(np.float64))
     diff = np.abs(got - Vref)
     assert diff.max() <= 2 and (diff == 0).mean() > 0.95
+
+
+def test_clse_resid_is_energy_beyond_top_r():
+    rng = np.random.default_rng(11)
+    K = rng.standard_normal((3, 16, 2, 128))
+    out = ob.clse_summary(K, 2, c_bits=8, c_grain="page")
+    dc = ob.page_factors(K, 2)[1]
+    sv = np.linalg.svd(dc, compute_uv=False)
+    assert np.allclose(out["resid"], (sv[..., 2:] ** 2).sum(-1), rtol=1e-10)
+    assert out["c_scale"].shape == (3, 2)
+    tok = ob.clse_summary(K, 2, c_bits=4, c_grain="token")
+    assert tok["c_scale"].shape == (3, 2, 16) and tok["c"].shape == (3, 2, 16, 1)

@@ -485,3 +485,63 @@ def test_tier_plan_maps_stay_inverse():
             # every victim slot was untouched before this step's installs
             vict = {v for r in range(3) for v in st["victims"][r][kv] if v >= 0}
             assert all(lru0[kv, v] <= clk0 for v in vict)
+
+
+def _clse_page(rng, r=2, d=128, NB=2, n_kv=1):
+    mu = rng.integers(-100, 100, (NB, n_kv, d)).astype(np.int8)
+    mus = np.full((NB, n_kv), 0.01, np.float32)
+    V = rng.integers(-127, 128, (NB, n_kv, d, r)).astype(np.int8)
+    vs = rng.uniform(0.005, 0.02, (NB, n_kv, r)).astype(np.float32)
+    c = rng.integers(-127, 128, (NB, n_kv, 16, r)).astype(np.int8)
+    cs = rng.uniform(0.01, 0.05, (NB, n_kv, 16)).astype(np.float32)
+    return mu, mus, V, vs, c, cs
+
+
+def test_clse_equals_r8_at_zero_residual():
+    """resid = 0 removes the iso term: CLSE is then the r8 score on the same factors
+    (the r8 oracle is pinned to the exact logsumexp above)."""
+    rng = np.random.default_rng(5)
+    mu, mus, V, vs, c, cs = _clse_page(rng)
+    q = rng.standard_normal((1, 4, 128)).astype(np.float32)
+    bt, sl, nsh = np.array([[0, 1]], np.int32), np.array([29]), np.array([2])
+    kw = dict(scale=128 ** -0.5, page=16, G=4, max_pages=2)
+    a = osc.clse_score(q, mu, mus, V, vs, c, cs, np.zeros((2, 1)), bt, sl, nsh,
+                       v_bits=8, c_bits=8, **kw)
+    b = osc.r8_score(q, mu, mus, V, vs, c, cs, bt, sl, nsh, vk_bits=8, c_bits=8, **kw)
+    assert np.allclose(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_clse_iso_term_by_hand():
+    """Constant coordinates (c = 0: every token logit 0, lse = log 16) and a V of two
+    exact unit axes: S = s mu.q + log 16 + (|q|^2 - q_0^2 - q_1^2) resid s^2 / (2P(d-2))."""
+    d, s = 128, 128 ** -0.5
+    mu = np.zeros((1, 1, d), np.int8)
+    mu[0, 0, :4] = [10, -20, 30, 0]
+    mus = np.array([[0.5]], np.float32)
+    V = np.zeros((1, 1, d, 2), np.int8)
+    V[0, 0, 0, 0] = V[0, 0, 1, 1] = 100
+    vs = np.full((1, 1, 2), 0.01, np.float32)              # unit axes e_0, e_1
+    c = np.zeros((1, 1, 16, 2), np.int8)
+    cs = np.ones((1, 1), np.float32)                       # page grain
+    q = np.zeros((1, 1, d), np.float32)
+    q[0, 0, :3] = [1.5, -2.0, 0.25]
+    q[0, 0, 100] = 3.0
+    resid = np.array([[7.0]])
+    got = osc.clse_score(q, mu, mus, V, vs, c, cs, resid, np.array([[0]], np.int32),
+                         np.array([16]), np.array([1]), scale=s, page=16, G=1, v_bits=8,
+                         c_bits=8, max_pages=1)
+    qmu = s * 0.5 * (10 * 1.5 + (-20) * (-2.0) + 30 * 0.25)
+    iso = (0.25 ** 2 + 3.0 ** 2) * 7.0 * s * s / (2 * 16 * (d - 2))
+    assert np.isclose(got[0, 0, 0], qmu + np.log(16) + iso, rtol=1e-12)
+
+
+def test_clse_nrm_is_per_head_max_layout():
+    rng = np.random.default_rng(6)
+    mu, mus, V, vs, c, cs = _clse_page(rng, r=4, NB=3, n_kv=2)
+    q = rng.standard_normal((1, 8, 128)).astype(np.float32)
+    bt, sl, nsh = np.array([[2, 0, 1]], np.int32), np.array([48]), np.array([3])
+    resid = rng.uniform(0, 50, (3, 2))
+    kw = dict(scale=128 ** -0.5, page=16, G=4, v_bits=8, c_bits=8, max_pages=3)
+    mx = osc.clse_score(q, mu, mus, V, vs, c, cs, resid, bt, sl, nsh, combine="max", **kw)
+    ph = osc.clse_score(q, mu, mus, V, vs, c, cs, resid, bt, sl, nsh, combine="nrm", **kw)
+    assert ph.shape == (1, 2, 4, 3) and np.allclose(ph.max(axis=2), mx)
