@@ -46,11 +46,12 @@ def _scores(R, n_kv, MP, gen, ties: bool, kind: int):
     return sc
 
 
-def _run(st, R, mode, tie, kind, cov, gen, ties, MP):
+def _run(st, R, mode, tie, kind, cov, gen, ties, MP, sc=None):
     sl = _seq_lens(R, MP, gen)
     sl_d = sl.to(DEV)
     derive_page_params(st, sl_d, R)
-    sc = _scores(R, st.n_kv, MP, gen, ties, kind)
+    if sc is None:
+        sc = _scores(R, st.n_kv, MP, gen, ties, kind)
     st.score.copy_(sc.to(DEV))
     st.page_table.fill_(-7)
     st.combine = "nrm" if kind == 1 else "max"
@@ -122,6 +123,25 @@ def test_max_pages_16384():
     st = _state(R, MP, G=4, budget=0.02)
     _run(st, R, 0, 0, 0, 1.0, gen, False, MP)
     _run(st, R, 1, 0, 1, 0.95, gen, True, MP)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("tie", [0, 1])
+def test_clustered_scores(mode, tie):
+    """Most scores a few ulps apart plus far outliers: the first radix digits put thousands
+    of pages in one bin, so the search takes several passes before the chosen bin is small
+    enough to be ranked all-pairs; a second cluster of exact ties sits at the cut."""
+    announce(f"clustered scores mode={mode} tie={tie}")
+    gen = torch.Generator().manual_seed(31 + mode + 2 * tie)
+    R, MP = 4, 4096
+    st = _state(R, MP, budget=0.3)
+    base = torch.full((R, st.n_kv, MP), 0.5)
+    ulps = torch.randint(0, 3000, (R, st.n_kv, MP), generator=gen).to(torch.int32)
+    sc = (base.view(torch.int32) + ulps).view(torch.float32)
+    sc[..., 7::97] = 3.5                              # far outliers above
+    sc[..., 11::89] = 1e-30                           # and below
+    sc[..., 5::3] = 0.5                               # one large exact tie class
+    _run(st, R, mode, tie, 1, 0.9, gen, False, MP, sc=sc)
 
 
 def test_nrm_fused_into_select():
