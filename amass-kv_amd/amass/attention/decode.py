@@ -4,10 +4,11 @@ Same contract as the reference ``sparse_paged_decode_batched`` (attention/decode
 247-304): consumes st.page_table / st.page_cnt and writes rows [0, n_req) of ``out``
 (T, H, d) in place, reading K from the resident paged cache and V through an injected
 V source (the fast / mem-v seam, attention/decode.py:44-95).  No allocation, no host
-sync.  Each (request, kv-head) unit gets S workgroups whose waves merge through LDS;
-with S > 1 they write split-K partials and a second launch does the LSE merge.  ``path``: "split" (S up to
-the partial capacity, at least 8 * pps_min pages per workgroup), "fused" (S = 1),
-"auto" (S sized so the units fill the GPU).
+sync.  A workgroup is (request, split s) with one wave per kv head; wave h attends pages
+s, s + S, ... of head h.  A head served by more than one split writes split-K partials
+and a second launch does the LSE merge.  ``path``: "split" (S up to the partial capacity,
+at least pps_min pages per split), "fused" (S = 1: one wave per head attends all of its
+pages and writes the output), "auto" (S sized so the workgroups fill the GPU).
 ``dense_paged_decode`` attends every page of every request (the dense baseline).
 """
 from __future__ import annotations
@@ -73,8 +74,8 @@ def ensure_stage_b_buffers(st, device, split: int = SPLIT) -> None:
 
 
 def _pps_min(n_req: int) -> int:
-    """Minimum pages per wave of a split workgroup (8 waves): fewer, fatter splits once
-    the batch fills the GPU."""
+    """Minimum pages per split (one wave per head): fewer, fatter splits once the batch
+    fills the GPU."""
     return 4 if n_req == 1 else 8
 
 

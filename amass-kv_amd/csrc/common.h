@@ -72,6 +72,47 @@ __device__ __forceinline__ float unit8_maxf(float v) {
     return v;
 }
 
+// Wave-uniform int sum / max and inclusive scan with DPP inside rows of 16 lanes and
+// readlane across the 4 rows: no LDS round trips (the shuffle forms below each take one
+// per step).  All 64 lanes must be active.
+constexpr int DPP_ROW_SHR1 = 0x111;
+constexpr int DPP_ROW_SHR2 = 0x112;
+constexpr int DPP_ROW_SHR4 = 0x114;
+constexpr int DPP_ROW_SHR8 = 0x118;
+
+__device__ __forceinline__ int row16_sum(int v) {   // every lane: sum of its row
+    v += dpp_i<DPP_HALF_MIRROR>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    v += dpp_i<DPP_XOR1>(v);
+    v += dpp_i<DPP_ROW_MIRROR>(v);
+    return v;
+}
+__device__ __forceinline__ int wave_sum_uniform(int v) {
+    v = row16_sum(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+           __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+__device__ __forceinline__ int wave_max_uniform(int v) {
+    v = max(v, dpp_i<DPP_HALF_MIRROR>(v));
+    v = max(v, dpp_i<DPP_XOR2>(v));
+    v = max(v, dpp_i<DPP_XOR1>(v));
+    v = max(v, dpp_i<DPP_ROW_MIRROR>(v));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+// inclusive prefix sum over the lanes (row_shr steps leave 0 where the source is outside
+// the row)
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += dpp_i<DPP_ROW_SHR1>(v);
+    v += dpp_i<DPP_ROW_SHR2>(v);
+    v += dpp_i<DPP_ROW_SHR4>(v);
+    v += dpp_i<DPP_ROW_SHR8>(v);
+    const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+              r2 = __builtin_amdgcn_readlane(v, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
 // full-wave reductions (result in every lane)
 __device__ __forceinline__ float wave_maxf(float v) {
 #pragma unroll
@@ -86,6 +127,11 @@ __device__ __forceinline__ float wave_sumf(float v) {
 __device__ __forceinline__ int wave_sumi(int v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ __forceinline__ int wave_maxi(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, WAVE));
     return v;
 }
 __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {

@@ -21,14 +21,17 @@
 // the current page is computed; the accumulator rescale is skipped when no row max moved
 // (alpha == 1 exactly).
 //
-// Workgroups.  A unit (request, kv-head) gets S workgroups of 8 waves (S = 1 when the
-// units alone fill the GPU, e.g. 32 requests x 8 heads; more for few, long units); wave
-// w of workgroup s attends pages s*8 + w, s*8 + w + 8S, ...  The 8 waves merge their
-// online-softmax states through LDS.  With S = 1 that is the output (the fused single
-// pass).  With S > 1 each workgroup writes one LSE partial (the split-K partial of
-// attention/decode.py:146-241) and a second launch, one workgroup per unit, merges the
-// S partials (attention/merge.py:21-50); a cross-workgroup ticket in one launch was
-// measured slower, its device-scope fences write back and invalidate the XCD's L2.
+// Workgroups.  A workgroup is (request, split s) and holds one wave per kv head (up to
+// 8): wave h attends pages s, s + S, s + 2S, ... of head h's selection.  The waves of a
+// workgroup therefore read the slices of different heads (often of the same blocks)
+// together, which is the access mix that lets the non-temporal K/V loads stream at
+// ~7 TB/s; eight waves of ONE head at the same offset of eight blocks measured 6.0 TB/s
+// with or without the hint.  A head served by one split (S_eff = 1) normalises and
+// writes its output (the fused single pass); otherwise every split writes an LSE
+// partial (the split-K partial of attention/decode.py:146-241) and a second launch, one
+// workgroup per unit, merges them (attention/merge.py:21-50); a cross-workgroup ticket
+// in one launch was measured slower, its device-scope fences write back and invalidate
+// the XCD's L2.
 #include "common.h"
 
 namespace amass {
@@ -70,18 +73,29 @@ __device__ __forceinline__ const uint16_t* v_base(const amass_decode_args& a, in
     return (const uint16_t*)a.v + blk * a.v_sb + (int64_t)kh * a.v_sh;
 }
 
+// 16-byte load with the non-temporal (streaming) hint: K and V are read once per step.
+__device__ __forceinline__ uint4 ld_stream(const uint16_t* p) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u x = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 template <int VSRC>
 __device__ __forceinline__ void load_page(const amass_decode_args& a, int kh, int64_t blk, int pt,
                                           int sl, int lane, PageData& pd) {
     const uint16_t* kb = (const uint16_t*)a.k + blk * a.k_sb + (int64_t)kh * a.k_sh +
                          (int64_t)(lane & 15) * a.k_st + 8 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pd.kq[i] = *reinterpret_cast<const uint4*>(kb + 32 * i);
+    for (int i = 0; i < 4; ++i) pd.kq[i] = ld_stream(kb + 32 * i);
     int64_t vst;
     const uint16_t* vb = v_base<VSRC>(a, kh, blk, pt, sl, vst);
     vb += (int64_t)(4 * (lane >> 4)) * vst + 8 * (lane & 15);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pd.vq[u] = *reinterpret_cast<const uint4*>(vb + (int64_t)u * vst);
+    for (int u = 0; u < 4; ++u) {
+        // the mem-v tier's V may sit in host memory: plain loads there
+        pd.vq[u] = VSRC == 0 ? ld_stream(vb + (int64_t)u * vst)
+                             : *reinterpret_cast<const uint4*>(vb + (int64_t)u * vst);
+    }
 }
 
 __device__ __forceinline__ uint32_t u4at(const uint4& v, int k) {
@@ -222,80 +236,168 @@ __device__ __forceinline__ int unit_count(const amass_decode_args& a, int r, int
     return a.page_cnt[(int64_t)r * a.pc_sr + kh];
 }
 
-// ------------------------------------------------------------------ decode
-// Workgroups of a unit that carry pages: at least 8 * pps_min pages each, at most S.
-__device__ __forceinline__ int unit_workgroups(int cnt, int S, int pps_min) {
-    const int per = DEC_WAVES * pps_min;
-    const int want = (cnt + per - 1) / per;
-    return max(1, min(S, want));
+// ------------------------------------------------------------------ split plan
+// A workgroup serves one (request, split) of one head group (hw = min(n_kv, 8) kv heads,
+// one wave each).  Request r's work is W_r = the most pages any head of the group attends;
+// it gets S_r = min(smax, max(1, ceil(W_r / tpw))) splits.  Balanced plan (path 0): tpw is
+// the smallest value >= max(pps_min, ceil(sum W / target)) with sum_r S_r <= target (a
+// binary search), so a ragged batch gives long requests more splits and the grid stays
+// one resident round; fixed plan (paths 1, 2): tpw = pps_min, smax = S.  Workgroup x walks
+// the requests' split counts in order.  All of it is computed on the device by every wave
+// (no host knowledge of the lengths, so the launch stays capturable).
+struct SplitPlan {
+    int req, s, S;
+};
+
+__device__ __forceinline__ int req_work(const amass_decode_args& a, int r, int kh0, int hw) {
+    if (a.dense) {
+        const int sl = a.seq_lens[r];
+        return sl > 0 ? (sl + DEC_PAGE - 1) / DEC_PAGE : 0;
+    }
+    const int32_t* pc = a.page_cnt + (int64_t)r * a.pc_sr + kh0;
+    const int n = min(hw, a.n_kv - kh0);
+    int c[DEC_WAVES];
+#pragma unroll
+    for (int h = 0; h < DEC_WAVES; ++h) c[h] = h < n ? pc[h] : 0;   // all loads issued first
+    int m = 0;
+#pragma unroll
+    for (int h = 0; h < DEC_WAVES; ++h) m = max(m, c[h]);
+    return m;
 }
 
-// One workgroup = DEC_WAVES waves over the page stripe j = s*8 + w (mod 8 * S_eff) of
-// unit (r = blockIdx.z, kh = blockIdx.y); the waves' online-softmax states merge through
-// LDS.  S_eff = 1: normalise and write out.  S_eff > 1: write the workgroup's LSE
-// partial for merge_kernel.
+__device__ __forceinline__ int req_splits(int W, int tpw, int smax) {
+    return W <= 0 ? 1 : min(smax, (W + tpw - 1) / tpw);
+}
+
+// W of requests base + lane (0 past the batch)
+__device__ __forceinline__ int lane_work(const amass_decode_args& a, int base, int kh0, int hw) {
+    const int r = base + (threadIdx.x & 63);
+    return r < a.n_req ? req_work(a, r, kh0, hw) : 0;
+}
+
+// Splits the whole batch takes at `tpw` (every lane gets the sum).  w0 = lane_work(0).
+__device__ __forceinline__ int plan_total(const amass_decode_args& a, int w0, int kh0, int hw,
+                                          int tpw, int smax) {
+    const int lane = threadIdx.x & 63;
+    int tot = wave_sum_uniform(lane < a.n_req ? req_splits(w0, tpw, smax) : 0);
+    for (int base = WAVE; base < a.n_req; base += WAVE)
+        tot += wave_sum_uniform(base + lane < a.n_req
+                                    ? req_splits(lane_work(a, base, kh0, hw), tpw, smax) : 0);
+    return tot;
+}
+
+__device__ __forceinline__ int plan_tpw(const amass_decode_args& a, int w0, int kh0, int hw,
+                                        bool balanced, int target, int smax) {
+    if (!balanced) return a.pps_min;
+    int total = wave_sum_uniform(w0), wmax = wave_max_uniform(w0);
+    for (int base = WAVE; base < a.n_req; base += WAVE) {
+        const int w = lane_work(a, base, kh0, hw);
+        total += wave_sum_uniform(w);
+        wmax = max(wmax, wave_max_uniform(w));
+    }
+    int lo = max(a.pps_min, (total + target - 1) / target);
+    if (plan_total(a, w0, kh0, hw, lo, smax) <= target) return lo;   // uniform batches
+    int hi = max(lo, wmax);                  // at hi every request takes one split
+    ++lo;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (plan_total(a, w0, kh0, hw, mid, smax) <= target) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ bool split_walk(const amass_decode_args& a, int w0, int kh0, int hw,
+                                           int tpw, int smax, int x, SplitPlan& p) {
+    const int lane = threadIdx.x & 63;
+    int before = 0;                                     // splits of earlier batches
+    for (int base = 0; base < a.n_req; base += WAVE) {
+        const int r = base + lane;
+        const int w = base == 0 ? w0 : lane_work(a, base, kh0, hw);
+        const int n = r < a.n_req ? req_splits(w, tpw, smax) : 0;
+        const int incl = wave_incl_scan(n);
+        const int in_batch = __builtin_amdgcn_readlane(incl, WAVE - 1);
+        if (x < before + in_batch) {
+            const unsigned long long hit = __ballot(before + incl > x);
+            const int src = __ffsll((long long)hit) - 1;
+            p.req = base + src;
+            p.S = __builtin_amdgcn_readlane(n, src);
+            p.s = x - before - __builtin_amdgcn_readlane(incl - n, src);
+            return true;
+        }
+        before += in_batch;
+    }
+    return false;
+}
+
+// Workgroup x = blockIdx.x of head group blockIdx.y: split p.s of request p.req; wave w
+// attends pages s, s + S_r, ... of kv head blockIdx.y * hw + w.  S_r = 1: normalise and
+// write out.  S_r > 1: write the split's LSE partial (slot s of the unit's a.split slots)
+// for merge_kernel.  `sarg` is the plan's target (balanced) or its fixed S.
 template <int VSRC, bool DENSE>
-__global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_decode_args a) {
-    __shared__ float sm_m[DEC_WAVES][8];
-    __shared__ float sm_l[DEC_WAVES][8];
-    __shared__ float sm_acc[DEC_WAVES][8][DEC_D];
+__global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_decode_args a,
+                                                                  int balanced, int sarg) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int s = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int hw = blockDim.x >> 6;
+    const int kh0 = blockIdx.y * hw;
+    const int smax = balanced ? a.split : min(sarg, a.split);
+    const int w0 = lane_work(a, 0, kh0, hw);
+    const int tpw = plan_tpw(a, w0, kh0, hw, balanced, sarg, smax);
+    SplitPlan pl;
+    if (!split_walk(a, w0, kh0, hw, tpw, smax, blockIdx.x, pl)) return;
+    const int kh = kh0 + w;
+    if (kh >= a.n_kv) return;
+    const int r = pl.req, s = pl.s, S = pl.S;
     const int sl = a.seq_lens[r];
     const int cnt = unit_count<DENSE>(a, r, kh, sl);
-    const int S = unit_workgroups(cnt, a.split, a.pps_min);
-    if (s >= S) return;
     WaveState st;
     init_state(st);
-    const int j0 = s * DEC_WAVES + w;
-    if (j0 < cnt) {
+    if (s < cnt) {
         bf16x4_t qb[8];
         load_q(a, r, kh, lane, qb);
-        attend_run<VSRC, DENSE>(a, r, kh, sl, j0, cnt, DEC_WAVES * S, lane, qb, st);
+        attend_run<VSRC, DENSE>(a, r, kh, sl, s, cnt, S, lane, qb, st);
     }
     float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
     lt += __shfl_xor(lt, 32, WAVE);
-    if (lane < a.G) {
-        sm_m[w][lane] = st.m;
-        sm_l[w][lane] = lt;
-    }
+    // this lane holds rows g = 4 (l/16) + j, columns d = 8 (l%16) .. +8 of the O tiles
+    const int d0 = 8 * (lane & 15);
+    if (S == 1) {
+        // rows of 8 bf16 are 16-byte aligned for the usual contiguous (T, H, d) output
+        const bool out16 = ((((uintptr_t)a.out) | (uintptr_t)(a.o_st * 2) |
+                             (uintptr_t)(a.o_hs * 2)) & 15) == 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int g = 4 * (lane >> 4) + j;
-        if (g < a.G) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sm_acc[w][g][8 * (lane & 15) + e] = st.acc[e][j];
+        for (int j = 0; j < 4; ++j) {
+            const int g = 4 * (lane >> 4) + j;
+            const float lg = __shfl(lt, g, WAVE);
+            if (g < a.G) {
+                const float inv = lg > 0.f ? 1.f / lg : 0.f;
+                const uint4 o = {pack_bf16x2(st.acc[0][j] * inv, st.acc[1][j] * inv),
+                                 pack_bf16x2(st.acc[2][j] * inv, st.acc[3][j] * inv),
+                                 pack_bf16x2(st.acc[4][j] * inv, st.acc[5][j] * inv),
+                                 pack_bf16x2(st.acc[6][j] * inv, st.acc[7][j] * inv)};
+                uint16_t* dst = (uint16_t*)a.out + (int64_t)r * a.o_st +
+                                (int64_t)(kh * a.G + g) * a.o_hs + d0;
+                if (out16) {
+                    *reinterpret_cast<uint4*>(dst) = o;
+                } else {
+                    uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+                    d32[0] = o.x; d32[1] = o.y; d32[2] = o.z; d32[3] = o.w;
+                }
+            }
         }
-    }
-    __syncthreads();
-    // merge the waves: (M, L, sum_w wt acc_w) per (g, d pair)
-    const int64_t ubase = ((int64_t)r * a.n_kv + kh) * a.split;   // partial slots of the unit
-    const int items = a.G * (DEC_D / 2);
-    for (int idx = threadIdx.x; idx < items; idx += blockDim.x) {
-        const int g = idx / (DEC_D / 2), d = 2 * (idx % (DEC_D / 2));
-        float M = -INFINITY;
-#pragma unroll
-        for (int x = 0; x < DEC_WAVES; ++x) M = fmaxf(M, sm_m[x][g]);
-        float lsum = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-        for (int x = 0; x < DEC_WAVES; ++x) {
-            const float ls = sm_l[x][g];
-            const float wt = ls > 0.f ? __expf(sm_m[x][g] - M) : 0.f;
-            lsum += ls * wt;
-            o0 += sm_acc[x][g][d] * wt;
-            o1 += sm_acc[x][g][d + 1] * wt;
+    } else {
+        const int64_t pg0 = (((int64_t)r * a.n_kv + kh) * a.split + s) * a.G;   // slot s
+        if (lane < a.G) {
+            a.m_part[pg0 + lane] = st.m;
+            a.l_part[pg0 + lane] = lt;
         }
-        if (S == 1) {
-            const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-            uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
-                                                        (int64_t)(kh * a.G + g) * a.o_hs + d);
-            *out = pack_bf16x2(o0 * inv, o1 * inv);
-        } else {
-            const int64_t pg = (ubase + s) * a.G + g;
-            *reinterpret_cast<float2*>(a.acc_part + pg * DEC_D + d) = make_float2(o0, o1);
-            if (d == 0) {
-                a.m_part[pg] = M;
-                a.l_part[pg] = lsum;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int g = 4 * (lane >> 4) + j;
+            if (g < a.G) {
+                float4* dst = reinterpret_cast<float4*>(a.acc_part + (pg0 + g) * DEC_D + d0);
+                dst[0] = make_float4(st.acc[0][j], st.acc[1][j], st.acc[2][j], st.acc[3][j]);
+                dst[1] = make_float4(st.acc[4][j], st.acc[5][j], st.acc[6][j], st.acc[7][j]);
             }
         }
     }
@@ -305,12 +407,15 @@ __global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_de
 // m_s over the non-empty partials, w_s = exp(m_s - m*), out = sum w_s acc_s / sum w_s l_s
 // (attention/merge.py:21-50).  Units the decode served with one workgroup (S_eff = 1)
 // were written directly and are skipped.
-__global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a) {
+__global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a, int balanced,
+                                                    int sarg) {
     const int kh = blockIdx.x, r = blockIdx.y;
-    const int sl = a.seq_lens[r];
-    const int cnt = a.dense ? (sl > 0 ? (sl + DEC_PAGE - 1) / DEC_PAGE : 0)
-                            : a.page_cnt[(int64_t)r * a.pc_sr + kh];
-    const int S = unit_workgroups(cnt, a.split, a.pps_min);
+    const int hw = a.n_kv < DEC_WAVES ? a.n_kv : DEC_WAVES;
+    const int kh0 = (kh / hw) * hw;
+    const int smax = balanced ? a.split : min(sarg, a.split);
+    const int w0 = lane_work(a, 0, kh0, hw);
+    const int tpw = plan_tpw(a, w0, kh0, hw, balanced, sarg, smax);
+    const int S = req_splits(req_work(a, r, kh0, hw), tpw, smax);
     if (S <= 1) return;
     const int64_t ubase = ((int64_t)r * a.n_kv + kh) * a.split;
     for (int idx = threadIdx.x; idx < a.G * (DEC_D / 2); idx += blockDim.x) {
@@ -340,47 +445,51 @@ __global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a) {
 }
 
 // Workgroups of the decode kernel resident per CU (queried once per instance).
+// Resident workgroups of `waves` waves per CU (cached per wave count) and the CU count.
 template <int VSRC, bool DENSE>
-static int decode_resident(int& cus) {
-    static int per_cu = 0, ncu = 0;
-    if (per_cu == 0) {
+static int decode_resident(int waves, int& cus) {
+    static int per_cu[DEC_WAVES + 1] = {0};
+    static int ncu = 0;
+    if (per_cu[waves] == 0) {
         int dev = 0, p = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&p, decode_kernel<VSRC, DENSE>,
-                                                         DEC_WAVES * WAVE, 0) != hipSuccess ||
+                                                         waves * WAVE, 0) != hipSuccess ||
             p < 1) {
             cus = 256;
             return 1;
         }
         ncu = n;
-        per_cu = p;
+        per_cu[waves] = p;
     }
     cus = ncu;
-    return per_cu;
+    return per_cu[waves];
 }
 
 template <int VSRC, bool DENSE>
 static int launch_decode(amass_decode_args a, int path, hipStream_t s) {
-    int S = 1;
-    if (path == 1) {
-        S = a.split;
-    } else if (path == 0) {
-        // one resident round of workgroups over the units
+    const int hw = a.n_kv < DEC_WAVES ? a.n_kv : DEC_WAVES;     // heads (waves) per workgroup
+    const int hg = (a.n_kv + hw - 1) / hw;                       // head groups
+    int balanced = 0, sarg = 1, grid = a.n_req;
+    if (path == 0) {
+        // balanced plan over one resident round of workgroups per head group
         int cus = 0;
-        const int resident = decode_resident<VSRC, DENSE>(cus) * cus;
-        const int units = a.n_req * a.n_kv;
-        S = (resident + units - 1) / units;
-        S = S < a.split ? S : a.split;
-        S = S < 1 ? 1 : S;
+        const int resident = decode_resident<VSRC, DENSE>(hw, cus) * cus;
+        balanced = 1;
+        sarg = (resident + hg - 1) / hg;
+        grid = sarg > a.n_req ? sarg : a.n_req;   // >= sum_r S_r (<= target, or n_req)
+    } else {
+        sarg = path == 1 ? a.split : 1;
+        grid = (sarg < a.split ? sarg : a.split) * a.n_req;
     }
-    if (S > 1 && (!a.m_part || !a.l_part || !a.acc_part)) return AMASS_ERR_NULL;
-    a.split = S;
-    hipLaunchKernelGGL((decode_kernel<VSRC, DENSE>), dim3(S, a.n_kv, a.n_req),
-                       dim3(DEC_WAVES * WAVE), 0, s, a);
+    const bool may_split = path == 0 ? a.split > 1 : (path == 1 && a.split > 1);
+    if (may_split && (!a.m_part || !a.l_part || !a.acc_part)) return AMASS_ERR_NULL;
+    hipLaunchKernelGGL((decode_kernel<VSRC, DENSE>), dim3(grid, hg), dim3(hw * WAVE), 0, s, a,
+                       balanced, sarg);
     int rc = check_launch();
-    if (rc || S == 1) return rc;
-    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req), dim3(256), 0, s, a);
+    if (rc || !may_split) return rc;
+    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req), dim3(256), 0, s, a, balanced, sarg);
     return check_launch();
 }
 

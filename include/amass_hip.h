@@ -219,15 +219,17 @@ int amass_coverage_select(const amass_select_args* a, void* stream);  /* forces 
  * and LSE merge) and attention/decode_cuda.py:1376-1501 (hand-CUDA split / fused).
  * Per (request r, kv-head kh) attend the pages page_table[r,kh,0:page_cnt) (dense = 1:
  * every page 0..ceil(sl/page)) with an online softmax; tokens >= seq_len are masked.
- * Work: S workgroups of 8 waves per (request, kv-head) unit; a unit of cnt pages uses
- * S_eff = min(S, max(1, ceil(cnt / (8 * pps_min)))) of them, wave w of workgroup s taking
- * pages s*8 + w, s*8 + w + 8*S_eff, ...  S_eff = 1: the workgroup merges its waves through
- * LDS and writes out.  S_eff > 1 (split-K): each workgroup writes its LSE partial
- * (m_part, l_part, acc_part, (R,n_kv,S,G[,d]) fp32 contiguous) and a second launch
- * merges each unit's S_eff partials (m* = max m_s, w_s = exp(m_s - m*) for l_s > 0,
+ * Work: a workgroup is (request, split s) with one wave per kv head (up to 8 heads per
+ * workgroup).  Request r, whose heads attend at most W_r pages, gets S_r = min(smax,
+ * max(1, ceil(W_r / tpw))) splits, split s taking pages s, s + S_r, ... of every head.
+ * path 2: smax = 1 (fused single pass); path 1: smax = split, tpw = pps_min; path 0
+ * (balanced): smax = split, tpw = max(pps_min, ceil(sum_r W_r / resident workgroups)),
+ * computed on the device.  S_r = 1: the wave normalises and writes out.  S_r > 1
+ * (split-K): each split writes its LSE partial into slot s of (m_part, l_part, acc_part,
+ * (R,n_kv,split,G[,d]) fp32 contiguous, split = the slot capacity) and a second launch
+ * merges each unit's S_r partials (m* = max m_s, w_s = exp(m_s - m*) for l_s > 0,
  * out = sum w_s acc_s / sum w_s l_s, 0 when empty).  Both launches are fixed-shape and
- * capturable.  path 2: S = 1 (fused single pass); path 1: S = split (<= the partial
- * capacity); path 0: S chosen from the unit count and the kernel's occupancy, <= split.
+ * capturable.
  * G <= 8.
  * v_src 0: V from the resident paged cache; v_src 1: mem-v tier, V per page from the hot
  * buffer (complete page resident in page2slot), else the staged pool (vbo[blk] >= 0,
