@@ -4,11 +4,12 @@ Same contract as the reference ``sparse_paged_decode_batched`` (attention/decode
 247-304): consumes st.page_table / st.page_cnt and writes rows [0, n_req) of ``out``
 (T, H, d) in place, reading K from the resident paged cache and V through an injected
 V source (the fast / mem-v seam, attention/decode.py:44-95).  No allocation, no host
-sync.  A workgroup is (request, split s) with one wave per kv head; wave h attends pages
-s, s + S, ... of head h.  A head served by more than one split writes split-K partials
-and a second launch does the LSE merge.  ``path``: "split" (S up to the partial capacity,
-at least pps_min pages per split), "fused" (S = 1: one wave per head attends all of its
-pages and writes the output), "auto" (S sized so the workgroups fill the GPU).
+sync.  A latency-bound batch (few selected pages) gets one workgroup per (request, kv
+head) whose waves split the head's pages and merge in LDS; otherwise each request gets S
+workgroups with one wave per kv head (split s attends pages s, s + S, ...) that write
+split-K partials for a second launch, the LSE merge.  ``path``: "auto" (layout and S chosen on the device so the
+workgroups fill the GPU), "split" (every request split, at least pps_min pages per
+split, S below the partial capacity), "fused" (every request one workgroup per head).
 ``dense_paged_decode`` attends every page of every request (the dense baseline).
 """
 from __future__ import annotations

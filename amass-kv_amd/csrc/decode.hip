@@ -237,14 +237,25 @@ __device__ __forceinline__ int unit_count(const amass_decode_args& a, int r, int
 }
 
 // ------------------------------------------------------------------ split plan
-// A workgroup serves one (request, split) of one head group (hw = min(n_kv, 8) kv heads,
-// one wave each).  Request r's work is W_r = the most pages any head of the group attends;
-// it gets S_r = min(smax, max(1, ceil(W_r / tpw))) splits.  Balanced plan (path 0): tpw is
-// the smallest value >= max(pps_min, ceil(sum W / target)) with sum_r S_r <= target (a
-// binary search), so a ragged batch gives long requests more splits and the grid stays
-// one resident round; fixed plan (paths 1, 2): tpw = pps_min, smax = S.  Workgroup x walks
-// the requests' split counts in order.  All of it is computed on the device by every wave
-// (no host knowledge of the lengths, so the launch stays capturable).
+// A workgroup serves one head group (hw = min(n_kv, 8) kv heads) of one request, in one of
+// two layouts chosen per launch.  Request r's work W_r is the most pages any head of the
+// group attends.
+//   whole (one head per workgroup): the group's nh heads get a workgroup each, whose
+//     waves split the head's pages and merge through LDS into the output (no partials).
+//     Path 2 (the fused single pass), and path 0 when the batch is latency-bound (on
+//     average <= DEC_WHOLE_PPS pages per resident workgroup): the merge launch it saves
+//     costs more than the streaming it loses.
+//   split (one wave per head): S_r = min(smax, max(1, ceil(W_r / tpw))) workgroups, split
+//     s taking pages s, s + S_r, ... of every head; S_r > 1 writes LSE partials.  The
+//     waves of a workgroup read the slices of different heads of (often) the same blocks,
+//     which keeps the non-temporal loads streaming.
+// Balanced plan (path 0, split): tpw is the smallest value >= max(pps_min, ceil(sum W /
+// target)) whose split total fits `target` resident workgroups (a binary search, skipped
+// when the first value fits); path 1: tpw = pps_min, smax = S.  Workgroup x walks the
+// requests' workgroup counts in order.  Every wave computes the plan on the device (no
+// host knowledge of the lengths, so the launch stays capturable).
+constexpr int DEC_WHOLE_PPS = 16;
+
 struct SplitPlan {
     int req, s, S;
 };
@@ -268,6 +279,10 @@ __device__ __forceinline__ int req_work(const amass_decode_args& a, int r, int k
 __device__ __forceinline__ int req_splits(int W, int tpw, int smax) {
     return W <= 0 ? 1 : min(smax, (W + tpw - 1) / tpw);
 }
+// workgroups of a request
+__device__ __forceinline__ int req_units(int W, bool whole, int tpw, int smax, int nh) {
+    return whole ? nh : req_splits(W, tpw, smax);
+}
 
 // W of requests base + lane (0 past the batch)
 __device__ __forceinline__ int lane_work(const amass_decode_args& a, int base, int kh0, int hw) {
@@ -275,6 +290,7 @@ __device__ __forceinline__ int lane_work(const amass_decode_args& a, int base, i
     return r < a.n_req ? req_work(a, r, kh0, hw) : 0;
 }
 
+// Workgroups the whole batch takes at `tpw` (every lane gets the sum).  w0 = lane_work(0).
 // Splits the whole batch takes at `tpw` (every lane gets the sum).  w0 = lane_work(0).
 __device__ __forceinline__ int plan_total(const amass_decode_args& a, int w0, int kh0, int hw,
                                           int tpw, int smax) {
@@ -286,17 +302,28 @@ __device__ __forceinline__ int plan_total(const amass_decode_args& a, int w0, in
     return tot;
 }
 
-__device__ __forceinline__ int plan_tpw(const amass_decode_args& a, int w0, int kh0, int hw,
-                                        bool balanced, int target, int smax) {
-    if (!balanced) return a.pps_min;
+// The launch's layout (whole) and pages per split (tpw).
+__device__ __forceinline__ void plan_setup(const amass_decode_args& a, int w0, int kh0, int hw,
+                                           int plan, int target, int smax, bool& whole,
+                                           int& tpw) {
+    whole = plan == 2;
+    tpw = a.pps_min;
+    if (plan != 0) return;
     int total = wave_sum_uniform(w0), wmax = wave_max_uniform(w0);
     for (int base = WAVE; base < a.n_req; base += WAVE) {
         const int w = lane_work(a, base, kh0, hw);
         total += wave_sum_uniform(w);
         wmax = max(wmax, wave_max_uniform(w));
     }
+    if (total <= DEC_WHOLE_PPS * target) {
+        whole = true;
+        return;
+    }
     int lo = max(a.pps_min, (total + target - 1) / target);
-    if (plan_total(a, w0, kh0, hw, lo, smax) <= target) return lo;   // uniform batches
+    if (plan_total(a, w0, kh0, hw, lo, smax) <= target) {   // uniform batches
+        tpw = lo;
+        return;
+    }
     int hi = max(lo, wmax);                  // at hi every request takes one split
     ++lo;
     while (lo < hi) {
@@ -304,17 +331,18 @@ __device__ __forceinline__ int plan_tpw(const amass_decode_args& a, int w0, int 
         if (plan_total(a, w0, kh0, hw, mid, smax) <= target) hi = mid;
         else lo = mid + 1;
     }
-    return lo;
+    tpw = lo;
 }
 
 __device__ __forceinline__ bool split_walk(const amass_decode_args& a, int w0, int kh0, int hw,
-                                           int tpw, int smax, int x, SplitPlan& p) {
+                                           int nh, bool whole, int tpw, int smax, int x,
+                                           SplitPlan& p) {
     const int lane = threadIdx.x & 63;
-    int before = 0;                                     // splits of earlier batches
+    int before = 0;                                     // workgroups of earlier batches
     for (int base = 0; base < a.n_req; base += WAVE) {
         const int r = base + lane;
         const int w = base == 0 ? w0 : lane_work(a, base, kh0, hw);
-        const int n = r < a.n_req ? req_splits(w, tpw, smax) : 0;
+        const int n = r < a.n_req ? req_units(w, whole, tpw, smax, nh) : 0;
         const int incl = wave_incl_scan(n);
         const int in_batch = __builtin_amdgcn_readlane(incl, WAVE - 1);
         if (x < before + in_batch) {
@@ -330,33 +358,96 @@ __device__ __forceinline__ bool split_walk(const amass_decode_args& a, int w0, i
     return false;
 }
 
-// Workgroup x = blockIdx.x of head group blockIdx.y: split p.s of request p.req; wave w
-// attends pages s, s + S_r, ... of kv head blockIdx.y * hw + w.  S_r = 1: normalise and
-// write out.  S_r > 1: write the split's LSE partial (slot s of the unit's a.split slots)
-// for merge_kernel.  `sarg` is the plan's target (balanced) or its fixed S.
+// The last partial slot of a unit holds its split count (int32) for merge_kernel.
+__device__ __forceinline__ int* split_count_slot(const amass_decode_args& a, int r, int kh) {
+    return reinterpret_cast<int*>(a.m_part) +
+           (((int64_t)r * a.n_kv + kh) * a.split + (a.split - 1)) * a.G;
+}
+
+// Workgroup x = blockIdx.x of head group blockIdx.y, request p.req:
+//   whole: head kh0 + p.s; wave w attends pages w, w + waves, ...; LDS merge; output.
+//   split: split p.s; wave w attends pages s, s + S_r, ... of head kh0 + w.  S_r = 1:
+//     normalise and write out; S_r > 1: write the split's LSE partial (slot s).
+// `sarg` is the plan's target (path 0) or its fixed S (path 1).
 template <int VSRC, bool DENSE>
 __global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_decode_args a,
-                                                                  int balanced, int sarg) {
+                                                                  int plan, int sarg) {
+    __shared__ float sm_m[DEC_WAVES][8];
+    __shared__ float sm_l[DEC_WAVES][8];
+    __shared__ float sm_acc[DEC_WAVES][8][DEC_D];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int hw = blockDim.x >> 6;
     const int kh0 = blockIdx.y * hw;
-    const int smax = balanced ? a.split : min(sarg, a.split);
+    const int nh = min(hw, a.n_kv - kh0);
+    const int cap = plan == 2 ? 1 : a.split - 1;     // partial slots besides the count slot
+    const int smax = plan == 1 ? min(sarg, cap) : cap;
     const int w0 = lane_work(a, 0, kh0, hw);
-    const int tpw = plan_tpw(a, w0, kh0, hw, balanced, sarg, smax);
+    bool whole;
+    int tpw;
+    plan_setup(a, w0, kh0, hw, plan, sarg, smax, whole, tpw);
     SplitPlan pl;
-    if (!split_walk(a, w0, kh0, hw, tpw, smax, blockIdx.x, pl)) return;
-    const int kh = kh0 + w;
-    if (kh >= a.n_kv) return;
-    const int r = pl.req, s = pl.s, S = pl.S;
+    if (!split_walk(a, w0, kh0, hw, nh, whole, tpw, smax, blockIdx.x, pl)) return;
+    const int r = pl.req;
     const int sl = a.seq_lens[r];
-    const int cnt = unit_count<DENSE>(a, r, kh, sl);
     WaveState st;
     init_state(st);
+
+    if (whole) {
+        // ---- one head, the workgroup's waves split its pages, LDS merge ---------------
+        const int kh = kh0 + pl.s;
+        const int cnt = unit_count<DENSE>(a, r, kh, sl);
+        if (w < cnt) {
+            bf16x4_t qb[8];
+            load_q(a, r, kh, lane, qb);
+            attend_run<VSRC, DENSE>(a, r, kh, sl, w, cnt, hw, lane, qb, st);
+        }
+        float lt = st.l + __shfl_xor(st.l, 16, WAVE);
+        lt += __shfl_xor(lt, 32, WAVE);
+        if (lane < a.G) {
+            sm_m[w][lane] = st.m;
+            sm_l[w][lane] = lt;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int g = 4 * (lane >> 4) + j;
+            if (g < a.G) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sm_acc[w][g][8 * (lane & 15) + e] = st.acc[e][j];
+            }
+        }
+        if (plan != 2 && threadIdx.x == 0) *split_count_slot(a, r, kh) = 1;
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < a.G * (DEC_D / 2); idx += blockDim.x) {
+            const int g = idx / (DEC_D / 2), d = 2 * (idx % (DEC_D / 2));
+            float M = -INFINITY;
+            for (int x = 0; x < hw; ++x) M = fmaxf(M, sm_m[x][g]);
+            float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+            for (int x = 0; x < hw; ++x) {
+                const float ls = sm_l[x][g];
+                const float wt = ls > 0.f ? __expf(sm_m[x][g] - M) : 0.f;
+                lsum += ls * wt;
+                o0 += sm_acc[x][g][d] * wt;
+                o1 += sm_acc[x][g][d + 1] * wt;
+            }
+            const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+            uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
+                                                        (int64_t)(kh * a.G + g) * a.o_hs + d);
+            *out = pack_bf16x2(o0 * inv, o1 * inv);
+        }
+        return;
+    }
+
+    // ---- split layout: one wave per head --------------------------------------------------
+    const int kh = kh0 + w;
+    if (kh >= a.n_kv) return;
+    const int s = pl.s, S = pl.S;
+    const int cnt = unit_count<DENSE>(a, r, kh, sl);
     if (s < cnt) {
         bf16x4_t qb[8];
         load_q(a, r, kh, lane, qb);
         attend_run<VSRC, DENSE>(a, r, kh, sl, s, cnt, S, lane, qb, st);
     }
+    if (plan != 2 && s == 0 && lane == 0) *split_count_slot(a, r, kh) = S;
     float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
     lt += __shfl_xor(lt, 32, WAVE);
     // this lane holds rows g = 4 (l/16) + j, columns d = 8 (l%16) .. +8 of the O tiles
@@ -405,37 +496,53 @@ __global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_de
 
 // LSE merge of the split-K partials of unit (kh = blockIdx.x, r = blockIdx.y): m* = max
 // m_s over the non-empty partials, w_s = exp(m_s - m*), out = sum w_s acc_s / sum w_s l_s
-// (attention/merge.py:21-50).  Units the decode served with one workgroup (S_eff = 1)
-// were written directly and are skipped.
-__global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a, int balanced,
-                                                    int sarg) {
+// (attention/merge.py:21-50).  The unit's split count comes from its count slot; units
+// written directly (count 1) are skipped.  Up to 8 partials are loaded in one round.
+__global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a) {
     const int kh = blockIdx.x, r = blockIdx.y;
-    const int hw = a.n_kv < DEC_WAVES ? a.n_kv : DEC_WAVES;
-    const int kh0 = (kh / hw) * hw;
-    const int smax = balanced ? a.split : min(sarg, a.split);
-    const int w0 = lane_work(a, 0, kh0, hw);
-    const int tpw = plan_tpw(a, w0, kh0, hw, balanced, sarg, smax);
-    const int S = req_splits(req_work(a, r, kh0, hw), tpw, smax);
+    const int S = *split_count_slot(a, r, kh);
     if (S <= 1) return;
     const int64_t ubase = ((int64_t)r * a.n_kv + kh) * a.split;
     for (int idx = threadIdx.x; idx < a.G * (DEC_D / 2); idx += blockDim.x) {
         const int g = idx / (DEC_D / 2), d = 2 * (idx % (DEC_D / 2));
-        float M = -INFINITY;
+        float M = -INFINITY, lsum = 0.f, o0 = 0.f, o1 = 0.f;
+        if (S <= 8) {
+            float mm[8], ll[8];
+            float2 vv[8];
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                const int64_t pg = (ubase + x) * a.G + g;
+                mm[x] = x < S ? a.m_part[pg] : -INFINITY;
+                ll[x] = x < S ? a.l_part[pg] : 0.f;
+                vv[x] = x < S ? *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + d)
+                              : make_float2(0.f, 0.f);
+            }
+#pragma unroll
+            for (int x = 0; x < 8; ++x)
+                if (ll[x] > 0.f) M = fmaxf(M, mm[x]);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                const float wt = ll[x] > 0.f ? __expf(mm[x] - M) : 0.f;
+                lsum += ll[x] * wt;
+                o0 += vv[x].x * wt;
+                o1 += vv[x].y * wt;
+            }
+        } else {
 #pragma unroll 4
-        for (int x = 0; x < S; ++x) {
-            const int64_t pg = (ubase + x) * a.G + g;
-            if (a.l_part[pg] > 0.f) M = fmaxf(M, a.m_part[pg]);
-        }
-        float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+            for (int x = 0; x < S; ++x) {
+                const int64_t pg = (ubase + x) * a.G + g;
+                if (a.l_part[pg] > 0.f) M = fmaxf(M, a.m_part[pg]);
+            }
 #pragma unroll 4
-        for (int x = 0; x < S; ++x) {
-            const int64_t pg = (ubase + x) * a.G + g;
-            const float ls = a.l_part[pg];
-            const float wt = ls > 0.f ? __expf(a.m_part[pg] - M) : 0.f;
-            const float2 v = *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + d);
-            lsum += ls * wt;
-            o0 += v.x * wt;
-            o1 += v.y * wt;
+            for (int x = 0; x < S; ++x) {
+                const int64_t pg = (ubase + x) * a.G + g;
+                const float ls = a.l_part[pg];
+                const float wt = ls > 0.f ? __expf(a.m_part[pg] - M) : 0.f;
+                const float2 v = *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + d);
+                lsum += ls * wt;
+                o0 += v.x * wt;
+                o1 += v.y * wt;
+            }
         }
         const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
         uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
@@ -443,6 +550,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a, i
         *out = pack_bf16x2(o0 * inv, o1 * inv);
     }
 }
+
 
 // Workgroups of the decode kernel resident per CU (queried once per instance).
 // Resident workgroups of `waves` waves per CU (cached per wave count) and the CU count.
@@ -471,25 +579,26 @@ template <int VSRC, bool DENSE>
 static int launch_decode(amass_decode_args a, int path, hipStream_t s) {
     const int hw = a.n_kv < DEC_WAVES ? a.n_kv : DEC_WAVES;     // heads (waves) per workgroup
     const int hg = (a.n_kv + hw - 1) / hw;                       // head groups
-    int balanced = 0, sarg = 1, grid = a.n_req;
-    if (path == 0) {
+    // paths 0, 1 keep the last partial slot of a unit for its split count: splitting
+    // needs at least 3 slots, otherwise the fused single pass serves every head
+    const int plan = (path != 2 && a.split < 3) ? 2 : path;
+    int sarg = 1, grid = a.n_req * hw;
+    if (plan == 0) {
         // balanced plan over one resident round of workgroups per head group
         int cus = 0;
         const int resident = decode_resident<VSRC, DENSE>(hw, cus) * cus;
-        balanced = 1;
         sarg = (resident + hg - 1) / hg;
-        grid = sarg > a.n_req ? sarg : a.n_req;   // >= sum_r S_r (<= target, or n_req)
-    } else {
-        sarg = path == 1 ? a.split : 1;
-        grid = (sarg < a.split ? sarg : a.split) * a.n_req;
+        grid = sarg > grid ? sarg : grid;   // >= the plan's total (<= target, or n_req * hw)
+    } else if (plan == 1) {
+        sarg = a.split - 1;
+        grid = a.n_req * sarg;
     }
-    const bool may_split = path == 0 ? a.split > 1 : (path == 1 && a.split > 1);
-    if (may_split && (!a.m_part || !a.l_part || !a.acc_part)) return AMASS_ERR_NULL;
+    if (plan != 2 && (!a.m_part || !a.l_part || !a.acc_part)) return AMASS_ERR_NULL;
     hipLaunchKernelGGL((decode_kernel<VSRC, DENSE>), dim3(grid, hg), dim3(hw * WAVE), 0, s, a,
-                       balanced, sarg);
+                       plan, sarg);
     int rc = check_launch();
-    if (rc || !may_split) return rc;
-    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req), dim3(256), 0, s, a, balanced, sarg);
+    if (rc || plan == 2) return rc;
+    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req), dim3(256), 0, s, a);
     return check_launch();
 }
 

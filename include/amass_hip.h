@@ -219,16 +219,21 @@ int amass_coverage_select(const amass_select_args* a, void* stream);  /* forces 
  * and LSE merge) and attention/decode_cuda.py:1376-1501 (hand-CUDA split / fused).
  * Per (request r, kv-head kh) attend the pages page_table[r,kh,0:page_cnt) (dense = 1:
  * every page 0..ceil(sl/page)) with an online softmax; tokens >= seq_len are masked.
- * Work: a workgroup is (request, split s) with one wave per kv head (up to 8 heads per
- * workgroup).  Request r, whose heads attend at most W_r pages, gets S_r = min(smax,
- * max(1, ceil(W_r / tpw))) splits, split s taking pages s, s + S_r, ... of every head.
- * path 2: smax = 1 (fused single pass); path 1: smax = split, tpw = pps_min; path 0
- * (balanced): smax = split, tpw = max(pps_min, ceil(sum_r W_r / resident workgroups)),
- * computed on the device.  S_r = 1: the wave normalises and writes out.  S_r > 1
- * (split-K): each split writes its LSE partial into slot s of (m_part, l_part, acc_part,
- * (R,n_kv,split,G[,d]) fp32 contiguous, split = the slot capacity) and a second launch
- * merges each unit's S_r partials (m* = max m_s, w_s = exp(m_s - m*) for l_s > 0,
- * out = sum w_s acc_s / sum w_s l_s, 0 when empty).  Both launches are fixed-shape and
+ * Work (per head group of up to 8 kv heads; W_r = the most pages a head of request r
+ * attends): "whole" requests get one workgroup per head whose waves split the head's
+ * pages and merge through LDS into the output; "split" requests get S_r = min(smax,
+ * max(1, ceil(W_r / tpw))) workgroups with one wave per head, split s taking pages s,
+ * s + S_r, ... of every head.  path 2: every request whole (fused single pass); path 1:
+ * every request split, tpw = pps_min, smax = split - 1; path 0 (balanced): every
+ * request whole when sum_r W_r <= 16 * resident workgroups (latency-bound), else every
+ * request split with smax = split - 1 and tpw = the smallest value >= max(pps_min,
+ * ceil(sum_r W_r / resident workgroups)) whose split total fits one resident round,
+ * computed on the device.  S_r = 1: the wave normalises and writes out.
+ * S_r > 1 (split-K): each split writes its LSE partial into slot s of (m_part, l_part,
+ * acc_part, (R,n_kv,split,G[,d]) fp32 contiguous; slot split-1 of m_part holds the unit's
+ * split count) and a second launch merges each unit's S_r partials (m* = max m_s, w_s =
+ * exp(m_s - m*) for l_s > 0, out = sum w_s acc_s / sum w_s l_s, 0 when empty).  Paths 0
+ * and 1 need split >= 3 (else they run as path 2).  Both launches are fixed-shape and
  * capturable.
  * G <= 8.
  * v_src 0: V from the resident paged cache; v_src 1: mem-v tier, V per page from the hot

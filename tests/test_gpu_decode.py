@@ -132,6 +132,31 @@ def test_split_equals_fused_and_padded_rows():
     assert np.allclose(outs[0], outs[1], atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("frac", [0.02, 0.9])
+def test_auto_plan_layouts(frac):
+    """path "auto" plans on the device: a latency-bound batch (2 % of the pages) runs one
+    workgroup per (request, head) with the waves merged in LDS; a bandwidth-bound ragged
+    batch (90 %, more than 16 pages per resident workgroup) runs the balanced split layout
+    (one wave per head, LSE partials, the merge launch).  Both match the fp64 oracle."""
+    announce(f"auto plan layouts frac={frac}")
+    B, G = 8, 4
+    case = make_case(B=B, ctx=(4000, 24000), n_kv=8, G=G, heavy=0.0, table="perm", seed=61)
+    tab, cnt = _selection(case, frac, seed=6, empty_unit=True)
+    q, K, V, bt, sl = _np_inputs(case)
+    ref = odec.attend(q, K, V, bt, sl, tab, cnt, scale=case.scale, G=G)
+    kv = case.kv_cache.to(DEV)
+    st = _st(case, tab, cnt)
+    out = torch.full((B, 8 * G, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    sparse_paged_decode_batched(case.q.to(DEV), kv, case.block_table.to(DEV),
+                                case.seq_lens.to(DEV), st, out, ResidentVSource(kv),
+                                scale=case.scale, path="auto")
+    torch.cuda.synchronize()
+    got = npf(out)
+    assert np.isfinite(got).all()
+    assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
+    assert np.all(got[0, :G] == 0)
+
+
 @pytest.mark.parametrize("dense", [False, True])
 def test_split_merge_repeatable_across_launches_and_graph_replays(dense):
     """Split-K partials + merge launch: eager launches and HIP-graph replays (with eager
