@@ -18,7 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
-ABI_VERSION = 4     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
+ABI_VERSION = 5     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):
@@ -112,6 +112,28 @@ class CopyRun(C.Structure):
     _fields_ = _fields("dst:p src:p dpitch:i64 spitch:i64 width:i64 height:i64")
 
 
+class InvalidateArgs(C.Structure):
+    _fields_ = _fields(
+        "block_table:p bt_st:i64 seq_lens:p query_start_loc:p page2slot:p slot2page:p "
+        "pool_valid:p n_req:i32 n_layers:i32 nb:i32 n_kv:i32 slots:i32 page:i32 "
+        "max_pages:i32")
+
+
+class StageArgs(C.Structure):
+    _fields_ = _fields(
+        "block_table:p bt_st:i64 seq_lens:p query_start_loc:p vbo:p v_flushed:p "
+        "free_stack:p free_top:p v_slot:p flush_list:p flush_cnt:p overflow:p mark:p first:p "
+        "v_pool:p vp_sl:i64 vp_sb:i64 vp_st:i64 vp_sh:i64 pool:p pool_valid:p "
+        "n_req:i32 n_tokens:i32 max_pages:i32 n_layers:i32 nb:i32 nv:i32 n_kv:i32 page:i32 "
+        "d:i32 maxf:i32")
+
+
+class ScatterArgs(C.Structure):
+    _fields_ = _fields(
+        "value:p v_st:i64 v_sh:i64 v_slot:p v_pool:p vp_sb:i64 vp_st:i64 vp_sh:i64 "
+        "n_tokens:i32 n_kv:i32 d:i32 page:i32 nv:i32")
+
+
 STRUCTS = {
     "amass_quad_score_args": (0, QuadScoreArgs),
     "amass_r8_score_args": (1, R8ScoreArgs),
@@ -124,6 +146,9 @@ STRUCTS = {
     "amass_copy_run": (8, CopyRun),
     "amass_build_args": (9, BuildArgs),
     "amass_clse_score_args": (10, ClseScoreArgs),
+    "amass_invalidate_args": (11, InvalidateArgs),
+    "amass_stage_args": (12, StageArgs),
+    "amass_scatter_args": (13, ScatterArgs),
 }
 
 # entry point -> argument struct (None = custom signature)
@@ -141,6 +166,9 @@ ENTRY_POINTS = {
     "amass_tier_fetch": TierFetchArgs,
     "amass_summary_build": BuildArgs,
     "amass_clse_score": ClseScoreArgs,
+    "amass_tier_invalidate": InvalidateArgs,
+    "amass_stage_begin_step": StageArgs,
+    "amass_stage_scatter": ScatterArgs,
 }
 
 _LIB: Optional[C.CDLL] = None

@@ -7,7 +7,10 @@ attention impl calls the select / decode functions with the layer-index-free sig
 one implementation of every kernel (libamass_hip.so); nothing here falls back to
 another kernel family -- an unsupported configuration is refused up front and the
 impl then leaves the step to the stock vLLM attention, as the reference does for every
-path it does not handle (``backend/attn.py:45-59``).
+path it does not handle (``backend/attn.py:45-59``).  mem-v runs the tier in shadow, as
+the reference's backend does: the builder runs the tier's per-step lifecycle, the impl
+writes each layer's V into the staging pool and attends with the stock attention while
+the engine cache still holds V.
 """
 from __future__ import annotations
 
@@ -35,9 +38,8 @@ def unsupported_reason(cfg: Optional[AmassConfig], *, head_size: int, block_size
     """Why this build's decode path does not serve a layer (None = it does)."""
     if cfg is None:
         return "no AmassConfig registered"
-    if cfg.variant != "fast":
-        return (f"variant {cfg.variant!r}: the tier's write path (staging / flush) is not "
-                "part of this build, so mem variants keep the stock attention")
+    if cfg.offload_k:
+        return "variant 'mem-kv': K offload is not part of this build"
     if head_size != HEAD_DIM or block_size != PAGE:
         return f"head_size {head_size} / block_size {block_size} (built for 128 / 16)"
     if not 1 <= G <= 8:
@@ -66,6 +68,15 @@ def make_state(cfg: AmassConfig, device, *, num_layers: int, num_blocks: int, n_
     st.scale = None
     ensure_stage_b_buffers(st, device)
     return st
+
+
+def make_tier(cfg: AmassConfig, device, *, num_layers: int, num_blocks: int, n_kv: int,
+              max_reqs: int, max_pages: int, max_tokens: int, dtype):
+    """The mem-v tier (pinned V pool, hot buffer, staging) of reference builder.py:245-288."""
+    from ..tier import Tier
+    return Tier.from_config(cfg, num_layers=num_layers, num_blocks=num_blocks, n_kv=n_kv,
+                            page=PAGE, d=HEAD_DIM, max_reqs=max_reqs, max_pages=max_pages,
+                            max_tokens=max_tokens, dtype=dtype, device=device)
 
 
 def layer_index(st, kv_cache) -> int:

@@ -11,6 +11,10 @@ runs the stock implementation unchanged.  A pure decode step runs
 
 with K and V read from the resident paged cache.  ``forward`` has the reference's
 signature and returns ``output``.
+
+mem-v (reference attn.py:84-118, shadow): every step writes the layer's V into the
+tier's staging pool (the write path, ``tier.write_kv``; the builder ran the step's
+lifecycle) and attends with the stock attention, the engine cache still holding V.
 """
 from __future__ import annotations
 
@@ -49,9 +53,24 @@ class AmassAttentionImplMixin:
                     or getattr(self, "dcp_world_size", 1) > 1
                     or _quantized(getattr(self, "kv_cache_dtype", "auto")))
 
+    def _amass_write_v(self, m, value, kv_cache) -> None:
+        """mem-v write path of this layer: the step's V -> the tier's staging pool."""
+        tier = getattr(m, "amass_tier", None) if m is not None else None
+        if tier is None or value is None or kv_cache is None:
+            return
+        lidx = _runtime.layer_index(tier, kv_cache)
+        v3 = value if value.dim() == 3 else value.view(value.shape[0], self.num_kv_heads, -1)
+        tier.write_kv(lidx, v3, v3.shape[0])
+
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
                 output_scale=None, output_block_scale=None):
         m = attn_metadata
+        cfg = _runtime.get_config()
+        if cfg is not None and cfg.is_mem:
+            self._amass_write_v(m, value, kv_cache)
+            return super().forward(layer, query, key, value, kv_cache, m, output,
+                                   output_scale=output_scale,
+                                   output_block_scale=output_block_scale)
         if not self._amass_pure_decode(m, kv_cache, output):
             return super().forward(layer, query, key, value, kv_cache, m, output,
                                    output_scale=output_scale,

@@ -16,7 +16,13 @@ picked.  It owns the Stage-A lifecycle:
   cudagraph-capture dummy batches skip this;
 * ``derive_page_params`` runs once per step (one launch), only on steps where
   ceil(seq_len / page) can have changed;
-* the state is attached as ``md.amass`` for the impl.
+* the state is attached as ``md.amass`` for the impl;
+* mem-v (reference builder.py:243-330, shadow): the Tier is allocated lazily like the
+  state, and every step -- prefill and decode -- runs ``tier.begin_step`` outside the
+  graph (invalidate the rewritten pages, flush complete staged pages to the pinned pool,
+  allocate staging blocks, token slots) over the padded token count; the tier is attached
+  as ``md.amass_tier`` (also on capture batches, where begin_step is skipped, so the
+  captured forward contains the impl's V scatter).
 
 With the HIP kernels the pure-decode pipeline is fixed-shape, allocation-free and
 host-sync-free, so the builder declares UNIFORM_SINGLE_TOKEN_DECODE graph support
@@ -86,7 +92,7 @@ class AmassMetadataBuilderMixin:
         cg = _cg_support()
         cfg = _runtime.get_config()
         n_kv, G, head, block = _geometry(vllm_config, kv_cache_spec)
-        if (cfg is not None and not cfg.force_eager
+        if (cfg is not None and cfg.variant == "fast" and not cfg.force_eager
                 and _runtime.unsupported_reason(cfg, head_size=head, block_size=block,
                                                 G=G) is None):
             return cg.UNIFORM_SINGLE_TOKEN_DECODE
@@ -101,6 +107,9 @@ class AmassMetadataBuilderMixin:
         self._amass_n_kv, self._amass_G, head, block = _geometry(vllm_config,
                                                                  kv_cache_spec)
         self._amass_state = None
+        self._amass_tier = None
+        self._amass_tier_tried = False
+        self._amass_mem = self._amass_cfg is not None and self._amass_cfg.is_mem
         self._amass_layer_k = None
         self._amass_prev = None
         self._amass_built_once = False
@@ -112,6 +121,64 @@ class AmassMetadataBuilderMixin:
             _notice(f"stock attention kept: {why}")
 
     # ---- lazy state (num_gpu_blocks is known only once the cache is allocated) ------- #
+    def _amass_layer_map(self):
+        """(per-layer resident KV tensors, data_ptr -> layer), or None before binding."""
+        sfc = self._amass_vllm_config.compilation_config.static_forward_context
+        layer_kv, ptr2layer = [], {}
+        for lidx, name in enumerate(self._amass_layers):
+            kvc = _kv_tensor(sfc.get(name))
+            if kvc is None:
+                return None
+            layer_kv.append(kvc)
+            ptr2layer[kvc.data_ptr()] = lidx
+        return layer_kv, ptr2layer
+
+    def _amass_ensure_tier(self):
+        if self._amass_tier is not None or self._amass_tier_tried or not self._amass_enabled:
+            return self._amass_tier
+        vc = self._amass_vllm_config
+        nb = getattr(vc.cache_config, "num_gpu_blocks", None)
+        bound = self._amass_layer_map() if nb else None
+        if bound is None:
+            return None                          # profiling run / not bound: retry
+        self._amass_tier_tried = True
+        layer_kv, ptr2layer = bound
+        try:
+            sched, comp = vc.scheduler_config, vc.compilation_config
+            max_reqs = sched.max_num_seqs
+            max_tokens = max(int(getattr(sched, "max_num_batched_tokens", 0) or 0),
+                             int(getattr(comp, "max_cudagraph_capture_size", 0) or 0),
+                             max_reqs) + 8
+            tier = _runtime.make_tier(
+                self._amass_cfg, self._amass_device, num_layers=len(self._amass_layers),
+                num_blocks=int(nb), n_kv=self._amass_n_kv, max_reqs=max_reqs,
+                max_pages=-(-vc.model_config.max_model_len // _runtime.PAGE),
+                max_tokens=max_tokens, dtype=layer_kv[0].dtype)
+            tier._layer_of = ptr2layer
+            self._amass_tier = tier
+            _notice(f"Tier allocated (mem-v shadow): {tier.bytes_report()}")
+        except Exception as e:  # noqa: BLE001 - mem-v keeps the stock attention
+            print("[amass] Tier allocation failed; stock attention kept:", flush=True)
+            traceback.print_exception(type(e), e, e.__traceback__)
+        return self._amass_tier
+
+    def _amass_tier_step(self, md, cam):
+        tier = self._amass_ensure_tier()
+        if tier is None:
+            return md
+        if not self._amass_capturing:
+            sm = getattr(md, "slot_mapping", None)
+            n_tok = int(sm.shape[0]) if sm is not None else int(cam.num_actual_tokens)
+            try:
+                tier.begin_step(md.block_table, md.seq_lens, md.query_start_loc, n_tok)
+            except Exception as e:  # noqa: BLE001
+                print("[amass] tier.begin_step failed (this step keeps the stock "
+                      "attention):", flush=True)
+                traceback.print_exception(type(e), e, e.__traceback__)
+                return md
+        md.amass_tier = tier
+        return md
+
     def _amass_ensure_state(self):
         if self._amass_state is not None or not self._amass_enabled:
             return self._amass_state
@@ -119,14 +186,10 @@ class AmassMetadataBuilderMixin:
         nb = getattr(vc.cache_config, "num_gpu_blocks", None)
         if not nb:
             return None
-        sfc = vc.compilation_config.static_forward_context
-        layer_kv, ptr2layer = [], {}
-        for lidx, name in enumerate(self._amass_layers):
-            kvc = _kv_tensor(sfc.get(name))
-            if kvc is None:
-                return None                      # not bound yet: retry next build
-            layer_kv.append(kvc)
-            ptr2layer[kvc.data_ptr()] = lidx
+        bound = self._amass_layer_map()
+        if bound is None:
+            return None                          # not bound yet: retry next build
+        layer_kv, ptr2layer = bound
         try:
             from ..attention.decode import _split_kv
             cfg = self._amass_cfg
@@ -159,6 +222,8 @@ class AmassMetadataBuilderMixin:
 
     def build(self, common_prefix_len, common_attn_metadata, fast_build=False):
         md = super().build(common_prefix_len, common_attn_metadata, fast_build)
+        if self._amass_mem:
+            return self._amass_tier_step(md, common_attn_metadata)
         st = self._amass_ensure_state()
         if st is None or getattr(md, "max_query_len", None) != 1:
             return md

@@ -85,3 +85,46 @@ def register(overrides: dict | None = None) -> None:
     target.get_attn_backend_cls = classmethod(get_attn_backend_cls)
     _APPLIED = True
     print("[amass] registered (patched RocmPlatform.get_attn_backend_cls)", flush=True)
+
+
+_ATTENTION_LAYERS = ("vllm.attention.layer.Attention",
+                     "vllm.model_executor.layers.attention.Attention")
+
+
+def patch_kv_cache_spec_k_only() -> None:
+    """Opt-in for mem variants whose every attention reads V from the tier: the engine's
+    block pool holds K only, so ``num_gpu_blocks`` doubles at the same memory budget
+    (reference backend/register.py:90-101, a documented follow-up there).  Wraps the
+    attention layer's ``get_kv_cache_spec`` to return the plain full-attention spec with
+    ``head_size_v = 0``; any other spec (sliding window, MLA, asymmetric heads) raises.
+    register() does not call it: this build's mem-v backend attends with the stock
+    attention, which still reads V from the engine cache."""
+    import dataclasses
+    cls = None
+    for qualname in _ATTENTION_LAYERS:
+        try:
+            cls = _resolve(qualname)
+            break
+        except (ImportError, AttributeError):
+            continue
+    if cls is None:
+        raise RuntimeError("vLLM's attention layer class was not found")
+    orig = cls.get_kv_cache_spec
+    if getattr(orig, "_amass_k_only", False):
+        return
+
+    def get_kv_cache_spec(self, *args, **kwargs):
+        spec = orig(self, *args, **kwargs)
+        if spec is None:
+            return spec
+        if type(spec).__name__ != "FullAttentionSpec" or not dataclasses.is_dataclass(spec):
+            raise ValueError(f"K-only KV cache: {type(spec).__name__} layers are not "
+                             "supported (plain full attention only)")
+        hv = getattr(spec, "head_size_v", spec.head_size)
+        if hv != spec.head_size:
+            raise ValueError(f"K-only KV cache: asymmetric heads (head_size "
+                             f"{spec.head_size}, head_size_v {hv})")
+        return dataclasses.replace(spec, head_size_v=0)
+
+    get_kv_cache_spec._amass_k_only = True
+    cls.get_kv_cache_spec = get_kv_cache_spec

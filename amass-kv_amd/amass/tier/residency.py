@@ -21,7 +21,8 @@ from __future__ import annotations
 
 import torch
 
-from .._hip import CopyRun, TierFetchArgs, TierPlanArgs, call, current_stream, ptr
+from .._hip import (CopyRun, InvalidateArgs, TierFetchArgs, TierPlanArgs, call,
+                     current_stream, ptr)
 
 I32_MAX = 2 ** 31 - 1
 
@@ -56,6 +57,20 @@ class Residency:
         self.fetch_grid = 1024
         elem = torch.empty(0, dtype=dtype).element_size()
         self.hot_gib = self.hot.numel() * elem / 2**30
+
+    # ---- per step (once, before staging) ---------------------------------------------
+    def invalidate_written(self, block_table, seq_lens, query_start_loc) -> None:
+        """Every page (re)written this step leaves the pinned pool's validity and the hot
+        buffer in every layer and kv head (tier/residency.py:251-278,352-367): block reuse
+        and chunked prefill make both copies stale."""
+        n_req = seq_lens.shape[0]
+        a = InvalidateArgs(
+            block_table=ptr(block_table), bt_st=block_table.stride(0),
+            seq_lens=ptr(seq_lens), query_start_loc=ptr(query_start_loc),
+            page2slot=ptr(self.page2slot), slot2page=ptr(self.slot2page),
+            pool_valid=ptr(self.pool_valid), n_req=n_req, n_layers=self.L, nb=self.NB,
+            n_kv=self.n_kv, slots=self.S, page=self.page, max_pages=block_table.shape[1])
+        call("amass_tier_invalidate", a, current_stream(self.device))
 
     # ---- per step, per layer -------------------------------------------------------
     def gather_plan(self, layer, page_table, page_cnt, block_table, seq_lens, n_req) -> None:

@@ -2,7 +2,9 @@
 
 Mirror of the reference ``tier/tier.py:37-265``.  ``step`` is the per-layer residency
 gather run before the layer's Stage-B decode (plan + fetch, both graph capturable);
-``step_dma`` is the copy-engine variant (host-planned, not capturable); ``vsource``
+``step_dma`` is the copy-engine variant (host-planned, not capturable); ``begin_step`` /
+``write_kv`` are the write path (invalidate + staging lifecycle once per step, the V
+scatter per layer); ``vsource``
 returns the ``TierVSource`` the decode consumes (V_SRC = 1: per page hot slot if the page
 is complete and resident, else the staging pool, else the pinned pool over the host link).
 """
@@ -33,9 +35,10 @@ class Tier:
         self.residency = Residency(num_layers=num_layers, num_blocks=num_blocks, n_kv=n_kv,
                                    hot_slots=hot_slots, page=page, d=d, max_reqs=max_reqs,
                                    max_pages=max_pages, dtype=dtype, device=device)
-        nv = v_blocks if v_blocks is not None else max(max_reqs, 1)
         self.staging = Staging(num_layers=num_layers, num_blocks=num_blocks, n_kv=n_kv,
-                               page=page, d=d, v_blocks=nv, dtype=dtype, device=device)
+                               page=page, d=d, dtype=dtype, device=device, max_reqs=max_reqs,
+                               max_pages=max_pages, max_tokens=max(max_tokens, max_reqs),
+                               v_blocks=v_blocks)
         self._copy_engine = None
 
     @classmethod
@@ -48,6 +51,29 @@ class Tier:
                    dtype=dtype, device=device, v_blocks=cfg.v_blocks,
                    max_pool_gb=cfg.max_pool_gb, offload_k=cfg.offload_k,
                    max_tokens=max_tokens)
+
+    def begin_step(self, block_table, seq_lens, query_start_loc, n_tokens: int) -> None:
+        """The one per-step entry (tier/tier.py:86-104), before the layers: pages written
+        this step leave the hot buffer and the pool's validity, then the staging
+        lifecycle (flush complete pages, allocate staging blocks, token slots)."""
+        self.residency.invalidate_written(block_table, seq_lens, query_start_loc)
+        self.staging.begin_step(block_table, seq_lens, query_start_loc, n_tokens, self.pool,
+                                self.residency.pool_valid)
+
+    def write_kv(self, lidx: int, value: torch.Tensor, n_tokens: int, key=None) -> None:
+        """Write path of layer ``lidx`` (after begin_step): this step's V into the
+        staging pool (tier/tier.py:125-130)."""
+        self.staging.scatter_kv(lidx, key, value, n_tokens)
+
+    def assert_invariants(self, block_table, seq_lens, query_start_loc) -> None:
+        """I1 / I3 checks (host-synchronising; debug), tier/tier.py:106-120."""
+        if int(self.staging.overflow.item()) != 0:
+            raise AssertionError("I1 capacity: the staging free stack underflowed (a written "
+                                 "page got no staging block); raise v_blocks")
+        self.staging.assert_free_partition()
+        self.residency.assert_maps_inverse()
+        self.staging.assert_no_lost_v(block_table, seq_lens, query_start_loc,
+                                      self.residency.pool_valid)
 
     def flush_layer(self, layer: int, v_blocks: torch.Tensor, valid: bool = True) -> None:
         """Write a layer's full V (NB, page, n_kv, d) to the pinned pool and mark every

@@ -44,6 +44,9 @@ extern "C" size_t amass_abi_struct_size(int which) {
         case 8: return sizeof(amass_copy_run);
         case 9: return sizeof(amass_build_args);
         case 10: return sizeof(amass_clse_score_args);
+        case 11: return sizeof(amass_invalidate_args);
+        case 12: return sizeof(amass_stage_args);
+        case 13: return sizeof(amass_scatter_args);
         default: return 0;
     }
 }

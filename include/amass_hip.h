@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 4
+#define AMASS_ABI_VERSION 5
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -322,10 +322,84 @@ int amass_tier_dma(const amass_copy_run* runs, int32_t n, void* stream);
 int amass_host_pool_alloc(size_t bytes, void** host_ptr, void** dev_ptr);
 int amass_host_pool_free(void* host_ptr);
 
+/* ---- mem-v write path ---------------------------------------------------------------- */
+/* Request r of a step holds seq_lens[r] tokens after the step, of which the last
+ * ql = query_start_loc[r+1] - query_start_loc[r] are written this step: written pages
+ * (sl - ql) / page .. (sl - 1) / page, complete settled pages [0, (sl - ql) / page).
+ * A request's block-table row (max_pages wide) maps its pages to distinct blocks; pages at
+ * or beyond max_pages and blocks outside [0, NB) are skipped.  All three entries are
+ * fixed-shape launches with no host synchronisation (capturable). */
+
+/* Replaces tier/residency.py:251-278,352-367 (_invalidate_kernel / invalidate_written):
+ * for every request with sl > 0 and every written page, all layers and kv heads:
+ * pool_valid = 0 and a resident block leaves the hot buffer (page2slot, slot2page = -1). */
+typedef struct amass_invalidate_args {
+    const int32_t* block_table; int64_t bt_st;
+    const int32_t* seq_lens;
+    const int32_t* query_start_loc;
+    int32_t* page2slot;      /* (L,n_kv,NB) */
+    int32_t* slot2page;      /* (L,n_kv,S)  */
+    int8_t*  pool_valid;     /* (L,n_kv,NB) */
+    int32_t  n_req, n_layers, nb, n_kv, slots, page, max_pages;
+} amass_invalidate_args;
+int amass_tier_invalidate(const amass_invalidate_args* a, void* stream);
+
+/* Replaces tier/staging.py:87-232,312-343 (Staging.begin_step: _vflush_clear,
+ * _flush_collect, _flush_copy, _valloc, _vslot) for requests with sl > 0 and ql > 0, in
+ * (request, page) order:
+ *   1. v_flushed[blk] = 0 for written pages;
+ *   2. every complete page whose block is staged (vbo >= 0) and not flushed is claimed
+ *      while the flush list has room (entry (blk, vb), v_flushed = 1; beyond maxf it
+ *      stays staged for the next step); every staged page not left over is freed
+ *      (vbo = -1, vb pushed on the free stack); a block shared by several requests
+ *      counts once (first occurrence);
+ *   3. each list entry's staged V is copied to the pinned pool for all layers and kv
+ *      heads, pool_valid = 1 (before step 4 may reuse the staging block);
+ *   4. every written page without a staging block pops the free stack (top - 1 first);
+ *      an empty stack sets overflow and leaves vbo = -1;
+ *   5. v_slot[t] = vbo[blk] * page + pos % page for this step's tokens, -1 otherwise
+ *      (every t < n_tokens is written).
+ * Five launches on `stream`; the collect and alloc launches are one workgroup each, the
+ * others parallel.  Scratch: mark (R, ceil(max_pages/256)) int32; first (NB,) int32,
+ * INT32_MAX at rest (restored before the call returns on the device). */
+typedef struct amass_stage_args {
+    const int32_t* block_table; int64_t bt_st;
+    const int32_t* seq_lens;
+    const int32_t* query_start_loc;  /* (R+1,) */
+    int32_t* vbo;            /* (NB,)         staging block of a physical block or -1 */
+    int32_t* v_flushed;      /* (NB,)                                                 */
+    int32_t* free_stack;     /* (NV,)         free staging blocks are [0, free_top)   */
+    int32_t* free_top;       /* (1,)                                                  */
+    int64_t* v_slot;         /* (>= n_tokens,)                                        */
+    int32_t* flush_list;     /* (maxf,2)      (blk, vb)                               */
+    int32_t* flush_cnt;      /* (1,)                                                  */
+    int32_t* overflow;       /* (1,)          latch                                   */
+    int32_t* mark;           /* scratch (R, ceil(max_pages/256))                      */
+    int32_t* first;          /* scratch (NB,), INT32_MAX at rest                      */
+    const void* v_pool; int64_t vp_sl, vp_sb, vp_st, vp_sh;  /* (L,NV,page,n_kv,d) bf16 */
+    void*    pool;           /* pinned pool device pointer (L,NB,n_kv,page,d)         */
+    int8_t*  pool_valid;     /* (L,n_kv,NB)                                           */
+    int32_t  n_req, n_tokens, max_pages, n_layers, nb, nv, n_kv, page, d, maxf;
+} amass_stage_args;
+int amass_stage_begin_step(const amass_stage_args* a, void* stream);
+
+/* Replaces tier/staging.py:51-80,348-364 (_scatter_kv_kernel / scatter_kv): the write
+ * path of one layer: v_pool[v_slot[t] / page, v_slot[t] % page] = value[t] (n_kv x d
+ * bf16) for every t < n_tokens with v_slot[t] >= 0; a bitwise copy. */
+typedef struct amass_scatter_args {
+    const void*    value; int64_t v_st, v_sh;            /* (T,n_kv,d) bf16             */
+    const int64_t* v_slot;                               /* (T,)                        */
+    void*          v_pool; int64_t vp_sb, vp_st, vp_sh;  /* this layer (NV,page,n_kv,d) */
+    int32_t n_tokens, n_kv, d, page, nv;
+} amass_scatter_args;
+int amass_stage_scatter(const amass_scatter_args* a, void* stream);
+
 /* ---- introspection (host only, no GPU needed) --------------------------------------- */
 int         amass_abi_version(void);
 size_t      amass_abi_struct_size(int which); /* 0 quad,1 r8,2 derive,3 nrm,4 select,
-                                                 5 decode,6 plan,7 fetch,8 copy_run */
+                                                 5 decode,6 plan,7 fetch,8 copy_run,
+                                                 9 build,10 clse,11 invalidate,
+                                                 12 stage,13 scatter */
 const char* amass_status_string(int status);
 int         amass_last_hip_error(void);      /* last hipError_t seen by the library */
 

@@ -35,6 +35,12 @@ Modules and what pins each function (beyond "it restates the reference"):
   tier.py    plan (residency.py:45-139)                 pinned: hand-worked LRU example,
                                                         page2slot/slot2page inverse,
                                                         victims are the oldest untouched
+  stage.py   invalidate (residency.py:251-278)          pinned: hand-worked example
+             begin_step (staging.py:87-232,312-343)     pinned: hand-worked two steps;
+             scatter (staging.py:51-80)                 simulations: every written token's
+                                                        V reads back (I1), free stack is a
+                                                        partition (I3), shared block,
+                                                        small flush list, exhaustion
 
 The reference ships no tests, fixtures or golden vectors for this path (its own tests
 directory is absent), so every check above is a closed form, an invariant or a brute

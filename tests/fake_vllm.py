@@ -4,6 +4,7 @@ platform's backend selection, one decoder attention backend (impl + metadata bui
 AttentionCGSupport and the config objects the builder reads."""
 from __future__ import annotations
 
+import dataclasses
 import enum
 import sys
 import types
@@ -53,7 +54,10 @@ class TritonAttentionMetadataBuilder:
     def build(self, common_prefix_len, common_attn_metadata, fast_build=False):
         cam = common_attn_metadata
         return Metadata(seq_lens=cam.seq_lens, block_table=cam.block_table_tensor,
-                        max_query_len=cam.max_query_len, causal=True)
+                        max_query_len=cam.max_query_len, causal=True,
+                        query_start_loc=getattr(cam, "query_start_loc", None),
+                        slot_mapping=getattr(cam, "slot_mapping", None),
+                        num_actual_tokens=getattr(cam, "num_actual_tokens", None))
 
     def build_for_cudagraph_capture(self, common_attn_metadata):
         return self.build(0, common_attn_metadata)
@@ -78,6 +82,32 @@ class RocmPlatform:
     def get_attn_backend_cls(cls, selected_backend, head_size, dtype, kv_cache_dtype,
                              block_size, use_v1=True, use_mla=False, **kw):
         return MLA_PATH if use_mla else TRITON_PATH
+
+
+@dataclasses.dataclass(frozen=True)
+class FullAttentionSpec:
+    block_size: int
+    num_kv_heads: int
+    head_size: int
+    head_size_v: int
+
+
+@dataclasses.dataclass(frozen=True)
+class SlidingWindowSpec:
+    block_size: int
+    num_kv_heads: int
+    head_size: int
+    sliding_window: int
+
+
+class Attention:
+    """The attention layer: get_kv_cache_spec as vLLM's layer returns it."""
+
+    def __init__(self, spec):
+        self.spec = spec
+
+    def get_kv_cache_spec(self, vllm_config):
+        return self.spec
 
 
 def vllm_config(*, num_gpu_blocks, layers, max_num_seqs=4, max_model_len=4096,
@@ -115,6 +145,8 @@ def install():
     mod("vllm.v1.attention.backend", AttentionCGSupport=AttentionCGSupport,
         AttentionType=AttentionType)
     mod("vllm.v1.attention.backends")
+    mod("vllm.attention")
+    mod("vllm.attention.layer", Attention=Attention)
     mod("vllm.v1.attention.backends.triton_attn", TritonAttentionBackend=TritonAttentionBackend,
         TritonAttentionImpl=TritonAttentionImpl,
         TritonAttentionMetadataBuilder=TritonAttentionMetadataBuilder)

@@ -65,6 +65,7 @@ def test_disable_env_makes_register_inert(vllm, monkeypatch):
     ({}, "UNIFORM_SINGLE_TOKEN_DECODE"),
     ({"force_eager": True}, "NEVER"),
     ({"variant": "mem-v"}, "NEVER"),
+    ({"variant": "mem-kv"}, "NEVER"),
     ({"score": "clse"}, "UNIFORM_SINGLE_TOKEN_DECODE"),
     ({"score": "r8"}, "UNIFORM_SINGLE_TOKEN_DECODE"),
 ])
@@ -185,3 +186,80 @@ def test_builder_skips_refresh_during_capture(vllm, monkeypatch):
                                             torch.zeros(2, 16, dtype=torch.int32)))
     assert type(md.amass).__name__ == "R8State" and md.amass.coverage is None
     assert rec == ["derive"]
+
+
+class _RecTier:
+    """Stands in for amass.tier.Tier: records the write-path calls."""
+
+    def __init__(self, rec):
+        self.rec = rec
+
+    def begin_step(self, bt, sl, qsl, n_tok):
+        self.rec.append(("begin", n_tok))
+
+    def write_kv(self, lidx, value, n_tokens, key=None):
+        self.rec.append(("write", lidx, tuple(value.shape), n_tokens))
+
+    def bytes_report(self):
+        return "rec"
+
+
+def test_mem_v_runs_the_tier_in_shadow(vllm, monkeypatch):
+    """mem-v (reference builder.py:243-330, attn.py:84-118): the builder allocates the tier
+    lazily and runs its lifecycle on every step -- prefill and decode, over the padded
+    token count -- skipping it on capture batches; the impl writes each layer's V into
+    the staging pool and attends with the stock attention."""
+    _, be = _backend(vllm, variant="mem-v")
+    rec = []
+    made = {}
+
+    def make_tier(cfg, device, **kw):
+        made.update(kw)
+        return _RecTier(rec)
+
+    monkeypatch.setattr(_runtime, "make_tier", make_tier)
+    kv = {f"l{i}": torch.zeros(40, 2, 16, 8, 128, dtype=torch.bfloat16) for i in range(2)}
+    vc = vllm.vllm_config(num_gpu_blocks=0, layers=kv, max_num_seqs=4, max_model_len=512)
+    b = be.get_builder_cls()(vllm.kv_spec(), list(kv), vc, "cpu")
+    bt = torch.arange(8, dtype=torch.int32).view(2, 4)
+
+    def cam(sl, qsl, max_q, n_pad):
+        c = _cam(torch.tensor(sl), bt, max_q)
+        c.query_start_loc = torch.tensor(qsl, dtype=torch.int32)
+        c.slot_mapping = torch.full((n_pad,), -1, dtype=torch.int64)
+        c.num_actual_tokens = qsl[-1]
+        return c
+
+    md = b.build(0, cam([20, 9], [0, 20, 29], 20, 29))
+    assert not hasattr(md, "amass_tier") and not rec              # cache not allocated
+    vc.cache_config.num_gpu_blocks = 40
+    md = b.build(0, cam([20, 9], [0, 20, 29], 20, 29))           # prefill step
+    assert rec == [("begin", 29)] and isinstance(md.amass_tier, _RecTier)
+    assert made["num_blocks"] == 40 and made["num_layers"] == 2 and made["max_pages"] == 32
+    assert md.amass_tier._layer_of == {kv["l0"].data_ptr(): 0, kv["l1"].data_ptr(): 1}
+    assert not hasattr(md, "amass")                               # no selection in shadow
+    rec.clear()
+    md = b.build(0, cam([21, 10], [0, 1, 2], 1, 4))              # decode step, padded to 4
+    assert rec == [("begin", 4)]
+    rec.clear()
+    md_cap = b.build_for_cudagraph_capture(cam([1, 1], [0, 1, 2], 1, 2))
+    assert rec == [] and isinstance(md_cap.amass_tier, _RecTier)
+    impl = be.get_impl_cls()(32, 128, 0.1, 8)
+    out = torch.zeros(4, 32, 128)
+    value = torch.zeros(4, 8 * 128, dtype=torch.bfloat16)
+    impl.forward(None, out, None, value, kv["l1"], md, out)
+    assert rec == [("write", 1, (4, 8, 128), 4)] and impl.calls == ["stock"]
+    assert be.get_builder_cls().get_cudagraph_support(vc, vllm.kv_spec()).name == "NEVER"
+
+
+def test_k_only_kv_cache_spec_patch(vllm):
+    """The opt-in K-only spec (reference register.py:90-101): a plain full-attention spec
+    gets head_size_v = 0; sliding-window and asymmetric specs are refused."""
+    register.patch_kv_cache_spec_k_only()
+    register.patch_kv_cache_spec_k_only()                         # idempotent
+    full = vllm.Attention(vllm.FullAttentionSpec(16, 8, 128, 128))
+    assert full.get_kv_cache_spec(None) == vllm.FullAttentionSpec(16, 8, 128, 0)
+    with pytest.raises(ValueError, match="SlidingWindowSpec"):
+        vllm.Attention(vllm.SlidingWindowSpec(16, 8, 128, 4096)).get_kv_cache_spec(None)
+    with pytest.raises(ValueError, match="asymmetric"):
+        vllm.Attention(vllm.FullAttentionSpec(16, 8, 128, 64)).get_kv_cache_spec(None)
