@@ -183,13 +183,17 @@ static inline int score_target(int resident, int head_groups) {
 }
 
 // ---- balanced split of a (ragged) batch's page tiles over the grid ---------------------
-// Request r has tiles_r = ceil(n_sel_hi[r] / 16) tiles.  Every wave computes the batch's
-// total T and the target tiles per workgroup tpw = ceil(T / target); request r gets
+// Request r has tiles_r = ceil(n_sel_hi[r] / 16) tiles.  At tpw tiles per workgroup it takes
 // n_r = ceil(tiles_r / tpw) workgroups, numbered consecutively over the batch, and its
-// workgroup j walks tiles j, j + n_r, j + 2 n_r, ... (a uniform batch is the plain
-// strided split).  Nothing depends on host-side knowledge of the lengths (the launch
-// stays graph-capturable); the grid is target + n_req workgroups, an upper bound of
-// sum n_r, and workgroups past the last one exit at once.
+// workgroup j walks tiles j, j + n_r, j + 2 n_r, ... (a uniform batch is the plain strided
+// split).  tpw is the smallest value >= ceil(T / target) whose total sum n_r fits `target`
+// (a binary search, skipped when the first value fits): `target` is what stays resident
+// at once, so every workgroup starts in the first round and the launch takes tpw tile
+// steps.  (With tpw = ceil(T / target) alone, the per-request rounding can push sum n_r
+// past the resident slots on a ragged batch; the surplus workgroups then run as a second
+// round and the launch takes up to twice as long.)  Nothing depends on host-side
+// knowledge of the lengths (the launch stays graph-capturable); the grid is target + n_req
+// workgroups, an upper bound of sum n_r, and workgroups past the last one exit at once.
 struct TileWalk {
     int req;       // request
     int first;     // first tile
@@ -201,27 +205,52 @@ __device__ __forceinline__ int tiles_of(int nsh) {
     return nsh > 0 ? (nsh + SC_TILE - 1) / SC_TILE : 0;
 }
 
+// tiles of requests base + lane (0 past the batch)
+__device__ __forceinline__ int lane_tiles(const int32_t* nsh, int n_req, int base) {
+    const int r = base + (threadIdx.x & 63);
+    return r < n_req ? tiles_of(nsh[r]) : 0;
+}
+
+// workgroups the batch takes at tpw tiles per workgroup (every lane gets the sum);
+// t0 = lane_tiles(0)
+__device__ __forceinline__ int walk_total(const int32_t* nsh, int n_req, int t0, int tpw) {
+    int tot = wave_sum_uniform((t0 + tpw - 1) / tpw);
+    for (int base = WAVE; base < n_req; base += WAVE)
+        tot += wave_sum_uniform((lane_tiles(nsh, n_req, base) + tpw - 1) / tpw);
+    return tot;
+}
+
+__device__ __forceinline__ int walk_tpw(const int32_t* nsh, int n_req, int target, int t0) {
+    int total = wave_sum_uniform(t0), tmax = wave_max_uniform(t0);
+    for (int base = WAVE; base < n_req; base += WAVE) {
+        const int t = lane_tiles(nsh, n_req, base);
+        total += wave_sum_uniform(t);
+        tmax = max(tmax, wave_max_uniform(t));
+    }
+    if (total <= 0) return 1;
+    int lo = (total + target - 1) / target;
+    if (walk_total(nsh, n_req, t0, lo) <= target) return lo;
+    int hi = max(lo, tmax);                 // at hi every request takes one workgroup
+    ++lo;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (walk_total(nsh, n_req, t0, mid) <= target) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
 __device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int target, int x,
                                           TileWalk& w) {
     const int lane = threadIdx.x & 63;
-    int total = 0;
-    for (int base = 0; base < n_req; base += WAVE) {
-        const int r = base + lane;
-        total += wave_sumi(r < n_req ? tiles_of(nsh[r]) : 0);
-    }
-    const int tpw = total > 0 ? (total + target - 1) / target : 1;
+    const int t0 = lane_tiles(nsh, n_req, 0);
+    const int tpw = walk_tpw(nsh, n_req, target, t0);
     int before = 0;                                     // workgroups of earlier batches
     for (int base = 0; base < n_req; base += WAVE) {
-        const int r = base + lane;
-        const int t = r < n_req ? tiles_of(nsh[r]) : 0;
+        const int t = base == 0 ? t0 : lane_tiles(nsh, n_req, base);
         const int nw = (t + tpw - 1) / tpw;
-        int incl = nw;                                  // inclusive scan over the lanes
-#pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-            const int y = __shfl_up(incl, o, WAVE);
-            if (lane >= o) incl += y;
-        }
-        const int in_batch = __shfl(incl, WAVE - 1, WAVE);
+        const int incl = wave_incl_scan(nw);
+        const int in_batch = __builtin_amdgcn_readlane(incl, WAVE - 1);
         if (x < before + in_batch) {
             const unsigned long long hit = __ballot(before + incl > x);
             const int src = __ffsll((long long)hit) - 1;
