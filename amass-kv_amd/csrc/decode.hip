@@ -494,61 +494,63 @@ __global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_de
     }
 }
 
-// LSE merge of the split-K partials of unit (kh = blockIdx.x, r = blockIdx.y): m* = max
-// m_s over the non-empty partials, w_s = exp(m_s - m*), out = sum w_s acc_s / sum w_s l_s
-// (attention/merge.py:21-50).  The unit's split count comes from its count slot; units
-// written directly (count 1) are skipped.  Up to 8 partials are loaded in one round.
-__global__ __launch_bounds__(256) void merge_kernel(const amass_decode_args a) {
-    const int kh = blockIdx.x, r = blockIdx.y;
+// LSE merge of the split-K partials of head g = blockIdx.z of unit (kh = blockIdx.x,
+// r = blockIdx.y): m* = max m_s over the non-empty partials, w_s = exp(m_s - m*),
+// out = sum w_s acc_s / sum w_s l_s (attention/merge.py:21-50).  The unit's split count
+// comes from its count slot; units written directly (count 1) are skipped.  Each of the
+// four waves merges every fourth partial (lane = a pair of d) with a running maximum, so
+// all of a thread's loads are independent of the others' results; the four (m, l, acc)
+// then combine through LDS the same way.
+constexpr int MG_WAVES = 4;
+
+__global__ __launch_bounds__(MG_WAVES * WAVE) void merge_kernel(const amass_decode_args a) {
+    const int kh = blockIdx.x, r = blockIdx.y, g = blockIdx.z;
     const int S = *split_count_slot(a, r, kh);
     if (S <= 1) return;
+    const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
     const int64_t ubase = ((int64_t)r * a.n_kv + kh) * a.split;
-    for (int idx = threadIdx.x; idx < a.G * (DEC_D / 2); idx += blockDim.x) {
-        const int g = idx / (DEC_D / 2), d = 2 * (idx % (DEC_D / 2));
-        float M = -INFINITY, lsum = 0.f, o0 = 0.f, o1 = 0.f;
-        if (S <= 8) {
-            float mm[8], ll[8];
-            float2 vv[8];
-#pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                const int64_t pg = (ubase + x) * a.G + g;
-                mm[x] = x < S ? a.m_part[pg] : -INFINITY;
-                ll[x] = x < S ? a.l_part[pg] : 0.f;
-                vv[x] = x < S ? *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + d)
-                              : make_float2(0.f, 0.f);
-            }
-#pragma unroll
-            for (int x = 0; x < 8; ++x)
-                if (ll[x] > 0.f) M = fmaxf(M, mm[x]);
-#pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                const float wt = ll[x] > 0.f ? __expf(mm[x] - M) : 0.f;
-                lsum += ll[x] * wt;
-                o0 += vv[x].x * wt;
-                o1 += vv[x].y * wt;
-            }
-        } else {
+    __shared__ float sh_m[MG_WAVES], sh_l[MG_WAVES];
+    __shared__ float2 sh_o[MG_WAVES][WAVE];
+    float m = -INFINITY, lsum = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll 4
-            for (int x = 0; x < S; ++x) {
-                const int64_t pg = (ubase + x) * a.G + g;
-                if (a.l_part[pg] > 0.f) M = fmaxf(M, a.m_part[pg]);
-            }
-#pragma unroll 4
-            for (int x = 0; x < S; ++x) {
-                const int64_t pg = (ubase + x) * a.G + g;
-                const float ls = a.l_part[pg];
-                const float wt = ls > 0.f ? __expf(a.m_part[pg] - M) : 0.f;
-                const float2 v = *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + d);
-                lsum += ls * wt;
-                o0 += v.x * wt;
-                o1 += v.y * wt;
-            }
+    for (int x = grp; x < S; x += MG_WAVES) {
+        const int64_t pg = (ubase + x) * a.G + g;
+        const float ls = a.l_part[pg], ms = a.m_part[pg];
+        const float2 v = *reinterpret_cast<const float2*>(a.acc_part + pg * DEC_D + 2 * lane);
+        if (ls > 0.f) {                                 // empty partials carry no weight
+            const float mn = fmaxf(m, ms);
+            const float al = __expf(m - mn), be = __expf(ms - mn);
+            lsum = lsum * al + ls * be;
+            o0 = o0 * al + v.x * be;
+            o1 = o1 * al + v.y * be;
+            m = mn;
         }
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
-                                                    (int64_t)(kh * a.G + g) * a.o_hs + d);
-        *out = pack_bf16x2(o0 * inv, o1 * inv);
     }
+    sh_o[grp][lane] = make_float2(o0, o1);
+    if (lane == 0) {
+        sh_m[grp] = m;
+        sh_l[grp] = lsum;
+    }
+    __syncthreads();
+    if (grp != 0) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < MG_WAVES; ++w)
+        if (sh_l[w] > 0.f) M = fmaxf(M, sh_m[w]);
+    float l = 0.f;
+    o0 = 0.f;
+    o1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < MG_WAVES; ++w) {
+        const float wt = sh_l[w] > 0.f ? __expf(sh_m[w] - M) : 0.f;
+        l += sh_l[w] * wt;
+        o0 += sh_o[w][lane].x * wt;
+        o1 += sh_o[w][lane].y * wt;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint32_t* out = reinterpret_cast<uint32_t*>((uint16_t*)a.out + (int64_t)r * a.o_st +
+                                                (int64_t)(kh * a.G + g) * a.o_hs + 2 * lane);
+    *out = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 
@@ -598,7 +600,7 @@ static int launch_decode(amass_decode_args a, int path, hipStream_t s) {
                        plan, sarg);
     int rc = check_launch();
     if (rc || plan == 2) return rc;
-    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(merge_kernel, dim3(a.n_kv, a.n_req, a.G), dim3(MG_WAVES * WAVE), 0, s, a);
     return check_launch();
 }
 
