@@ -391,7 +391,7 @@ def run_config4(args, boost="sigma", steps=64):
     NB = case.kv_cache.shape[0]
     slots = (B * MP) // 10
     tier = Tier(num_layers=1, num_blocks=NB, n_kv=n_kv, page=16, d=128, hot_slots=slots,
-                max_reqs=B, max_pages=MP, device="cuda", v_blocks=4)
+                max_reqs=B, max_pages=MP, device="cuda", v_blocks=2 * B + 8)
     tier.flush_layer(0, case.kv_cache[:, 1])
     log(f"config 4 ({boost}): inputs, summaries, pinned pool {time.time() - t0:.1f}s")
     bt, sl = case.block_table, case.seq_lens
@@ -440,6 +440,7 @@ def run_config4(args, boost="sigma", steps=64):
     torch.cuda.synchronize()
     us_res = a.elapsed_time(b) / steps * 1e3
     host_bytes = miss * 16 * 128 * 2 / steps
+    wp = write_path_times(tier, case, args)
     res = dict(workload=f"config4: mem-v B={B} ctx 32768 quad r'=8 int8 nrm coverage 0.95, "
                         f"hot buffer {slots} slots per kv head (10 %), {steps} steps, fresh "
                         f"N(0,1) queries, boost {boost}",
@@ -447,10 +448,48 @@ def run_config4(args, boost="sigma", steps=64):
                hit_rate=round(1.0 - miss / max(sel, 1), 4),
                selected_pages_per_step=round(sel / steps, 1),
                host_bytes_per_step=int(host_bytes),
-               host_link_gb_s=round(host_bytes / (us_step * 1e-6) / 1e9, 2))
+               host_link_gb_s=round(host_bytes / (us_step * 1e-6) / 1e9, 2),
+               write_path=wp)
     log(f"config 4 ({boost}): {us_step:.1f} us/step (resident {us_res:.1f}), "
-        f"hit rate {res['hit_rate']}")
+        f"hit rate {res['hit_rate']}; write path {wp}")
     return res
+
+
+def write_path_times(tier, case, args):
+    """The mem-v write path at the config-4 shape: every request appends one token per
+    decode step.  Sixteen consecutive steps fill each request's last page (positions
+    32752..32767, the last step completing it); one graph replays the sixteen
+    begin_step calls (invalidate + the five lifecycle launches), another the sixteen
+    per-layer V scatters.  us per step and per layer-scatter, HIP-graph replay."""
+    import torch
+
+    B, n_kv = case.q.shape[0], case.n_kv
+    bt, sl0 = case.block_table, case.seq_lens
+    base = sl0 - 16                                   # the last page starts empty
+    qsl = torch.arange(B + 1, dtype=torch.int32, device="cuda")
+    sls = [(base + k + 1).to(torch.int32) for k in range(16)]
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 505)
+    vals = torch.randn(B, n_kv, 128, generator=gen, device="cuda").to(torch.bfloat16)
+
+    def steps():
+        for k in range(16):
+            tier.begin_step(bt, sls[k], qsl, B)
+
+    def scatters():
+        for _ in range(16):
+            tier.write_kv(0, vals, B)
+
+    steps()
+    scatters()
+    torch.cuda.synchronize()
+    g_b, g_s = graph_of(steps), graph_of(scatters)
+    us_b = time_graph(g_b, 20, 3) * 1e3 / 16
+    us_s = time_graph(g_s, 20, 3) * 1e3 / 16
+    torch.cuda.synchronize()
+    ok = int(tier.staging.overflow.item()) == 0
+    del g_b, g_s
+    return dict(begin_step_us=round(us_b, 2), scatter_us_per_layer=round(us_s, 2),
+                requests=B, staging_ok=ok)
 
 
 def main():
