@@ -24,7 +24,7 @@ def quad_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> N
     v_code, v_s = _quant_vk(Vk, st.v_grain, st.v_bits)
     st.quad_mu[layer, blocks] = mu_code
     st.mu_scale[layer, blocks] = mu_s
-    st.quad_V[layer, blocks] = v_to_device(v_code, st.v_bits)
+    st.quad_V[layer, blocks] = v_to_device(v_code, st.v_bits, tiled=st.v_tiled)
     st.V_scale[layer, blocks] = v_s
     if getattr(st, "coords", "none") == "lse":
         # CLSE extras (reference selection/quad_build.py:38-54): c = U8 * S8 quantised per

@@ -6,8 +6,10 @@ into it.  Per (layer, block), REC = r' * CB + 192 bytes per kv head:
 
   quad_rec   (L, NB, n_kv * REC)  int8, per block:
     n_kv records of VM = r' * CB + 128 bytes, head h at h * VM:
-      quad_V   (L, NB, n_kv, r', CB) int8  column-major: column k holds CB bytes;
-               int8 CB = d (byte j = code[j]); int4 CB = d/2, byte j = code[j] | code[j+d/2] << 4
+      quad_V   (L, NB, n_kv, r', CB) int8  (r' * CB bytes) tiled for the score kernel's
+               column groups: 16 bytes per (K-step t, d group kg, column k) at
+               ((t * 4 + kg) * r' + k) * 16, byte i = code[64 t + 16 kg + i]; int8 CB = d,
+               int4 CB = d/2 with byte i of (kg, k) = code[16 kg + i] | code[16 kg + i + 64] << 4
                (the reference keeps (.., d, r') with two columns per int4 byte)
       quad_mu  (L, NB, n_kv, d)      int8  page-mean codes
     then n_kv scale blocks of 64 bytes (fp16 halves), head h at n_kv * VM + 64 h:
@@ -16,12 +18,12 @@ into it.  Per (layer, block), REC = r' * CB + 192 bytes per kv head:
       mu_scale (L, NB, n_kv)         half 16; the other halves are zero
   quad_tag   (L, NB, n_kv, TAGW)  bf16  NaN-init content tag (separate)
 
-Every V / mu record is whole 128-byte lines and a block's n_kv records are contiguous,
-so the gfx950 score kernel (one wave per kv head of a block, all on one CU) streams whole
-lines, feeds each 16-byte load of a V column straight into an int8 matrix-core
-instruction, and reads a page's scales with one more 16-byte load per lane.
-``v_to_device`` / ``v_to_reference`` convert V between this and the reference layout;
-``load_reference`` and ``reference_V`` use them.
+Every V / mu record is whole 128-byte lines and a block's n_kv records are contiguous.
+The tiled V lets the gfx950 score kernel feed an int8 matrix-core instruction whose 16
+columns are 16 / r' pages x r' ranks with loads that each read 64 r' contiguous bytes
+of every page they touch.  ``v_to_device`` / ``v_to_reference`` convert V between this
+and the reference layout; ``load_reference`` and ``reference_V`` use them.  CLSE keeps
+V column-major (column k at k * CB), the layout of the r8 records.
 
 CLSE (``coords="lse"``, the reference's ``score="clse"``) keeps the per-key coordinates
 and the residual scatter energy instead of sig2, in the r8 record layout
@@ -49,21 +51,50 @@ def _unpack_pairs(packed: torch.Tensor) -> torch.Tensor:
     return lo, hi
 
 
-def v_to_device(v_ref: torch.Tensor, v_bits: int) -> torch.Tensor:
-    """Reference quad_V (..., d, r') int8 or (..., d, r'/2) packed int4 (lo nibble = even
-    column) -> the kernel layout (..., r', d) int8 or (..., r', d/2) packed halves."""
+def _tile(col: torch.Tensor, v_bits: int) -> torch.Tensor:
+    """Column-major (..., r', CB) -> the quad kernel's tiled bytes, same shape: 16 bytes
+    per (K-step t, d group kg, column k) at ((t * 4 + kg) * r' + k) * 16, d = 64 t + 16 kg
+    + i (int4: byte i of (kg, k) packs d = 16 kg + i and d + 64, so t is folded)."""
+    *lead, r, cb = col.shape
+    nl = len(lead)
     if v_bits == 8:
-        return v_ref.transpose(-1, -2).contiguous()
+        t = col.reshape(*lead, r, 2, 4, 16).permute(*range(nl), nl + 1, nl + 2, nl, nl + 3)
+    else:
+        t = col.reshape(*lead, r, 4, 16).permute(*range(nl), nl + 1, nl, nl + 2)
+    return t.reshape(*lead, r, cb).contiguous()
+
+
+def _untile(tiled: torch.Tensor, v_bits: int) -> torch.Tensor:
+    """Inverse of :func:`_tile`."""
+    *lead, r, cb = tiled.shape
+    nl = len(lead)
+    if v_bits == 8:
+        c = tiled.reshape(*lead, 2, 4, r, 16).permute(*range(nl), nl + 2, nl, nl + 1, nl + 3)
+    else:
+        c = tiled.reshape(*lead, 4, r, 16).permute(*range(nl), nl + 1, nl, nl + 2)
+    return c.reshape(*lead, r, cb).contiguous()
+
+
+def v_to_device(v_ref: torch.Tensor, v_bits: int, tiled: bool = False) -> torch.Tensor:
+    """Reference quad_V (..., d, r') int8 or (..., d, r'/2) packed int4 (lo nibble = even
+    column) -> the kernel layout: column-major (..., r', d) int8 or (..., r', d/2) packed
+    halves (r8, CLSE), or those bytes tiled for the quad kernel (``tiled``)."""
+    if v_bits == 8:
+        col = v_ref.transpose(-1, -2).contiguous()
+        return _tile(col, v_bits) if tiled else col
     lo, hi = _unpack_pairs(v_ref)                       # columns 2c, 2c+1
     code = torch.stack([lo, hi], dim=-1).flatten(-2)    # (..., d, r')
     code = code.transpose(-1, -2)                       # (..., r', d)
     half = code.shape[-1] // 2
     packed = (code[..., :half] & 0xF) | ((code[..., half:] & 0xF) << 4)
-    return packed.to(torch.uint8).view(torch.int8).contiguous()
+    col = packed.to(torch.uint8).view(torch.int8).contiguous()
+    return _tile(col, v_bits) if tiled else col
 
 
-def v_to_reference(v_dev: torch.Tensor, v_bits: int) -> torch.Tensor:
+def v_to_reference(v_dev: torch.Tensor, v_bits: int, tiled: bool = False) -> torch.Tensor:
     """Inverse of :func:`v_to_device`."""
+    if tiled:
+        v_dev = _untile(v_dev, v_bits)
     if v_bits == 8:
         return v_dev.transpose(-1, -2).contiguous()
     lo, hi = _unpack_pairs(v_dev)                       # d = j, j + d/2
@@ -107,6 +138,7 @@ class QuadState:
         self.v_grain = v_grain
         self.v_bits, self.mu_bits = int(v_bits), 8
         self.coords, self.c_bits, self.c_grain = coords, int(c_bits), c_grain
+        self.v_tiled = coords == "none"                   # the quad kernel's V layout
         self.combine = combine
         self.device = device
         i8, f16, bf16 = torch.int8, torch.float16, torch.bfloat16
@@ -170,7 +202,7 @@ class QuadState:
         t = lambda x: torch.as_tensor(x).to(dev)  # noqa: E731
         self.quad_mu[layer].copy_(t(mu))
         self.mu_scale[layer].copy_(t(mu_scale))
-        self.quad_V[layer].copy_(v_to_device(t(V), self.v_bits))
+        self.quad_V[layer].copy_(v_to_device(t(V), self.v_bits, tiled=self.v_tiled))
         self.V_scale[layer].copy_(t(V_scale))
         if self.coords == "lse":
             self.quad_c[layer].copy_(t(c))
@@ -183,4 +215,4 @@ class QuadState:
 
     def reference_V(self, layer: int) -> torch.Tensor:
         """quad_V of ``layer`` in the reference layout (NB, n_kv, d, r'[/2])."""
-        return v_to_reference(self.quad_V[layer], self.v_bits)
+        return v_to_reference(self.quad_V[layer], self.v_bits, tiled=self.v_tiled)

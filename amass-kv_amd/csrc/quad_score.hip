@@ -15,24 +15,30 @@
 // the recipe of selection/quad_score_cuda.py:902-935 with IEEE divides) and every
 // contraction is an exact int32 sum: comb = 128 * (hi . x) + (lo . x).
 //
-// Layout.  Per block, the n_kv heads' records [quad_V column-major (r' columns of CB
-// bytes) | 128 mu codes], then the n_kv heads' 64-byte fp16 scale blocks (V_scale at
-// half 0, sig2 at half 8, mu_scale at half 16) -- AMASS_QUAD_REC_BYTES per head.  The 16
-// bytes a lane feeds to one MFMA (16 consecutive d of one column of one page) are one
-// dwordx4 load, the two K-steps of a column read one whole 128-byte line, every V / mu
-// record is whole 128-byte lines, and a page's scales are one more 16-byte load per lane
-// spread over the tile's four lane groups and exchanged with ds_bpermute.  int4 V
-// (CB = 64) has byte j = code[j] | code[j + 64] << 4: shifting the low nibble up and
-// masking gives 16 * code as a signed byte for d = j (K-step 0) and d = j + 64 (K-step
-// 1) with two ALU ops per word; the sums are divided by 16 exactly.
+// Layout.  Per block, the n_kv heads' records [quad_V tiled (r' CB bytes) | 128 mu
+// codes], then the n_kv heads' 64-byte fp16 scale blocks (V_scale at half 0, sig2 at half
+// 8, mu_scale at half 16) -- AMASS_QUAD_REC_BYTES per head.  quad_V holds 16 bytes per
+// (K-step t, d group kg, column k) at ((t * 4 + kg) * r' + k) * 16 (byte i = code of
+// d = 64 t + 16 kg + i); int4 (CB = 64) folds t into the nibbles (byte i of (kg, k) =
+// code[16 kg + i] | code[16 kg + i + 64] << 4; shifting the low nibble up and masking
+// gives 16 * code as a signed byte with two ALU ops per word, the sums divided by 16
+// exactly).
 //
-// Lanes.  lane = 16 kg + n: column n of the MFMA is page n of the tile, kg the 16-d
-// group of each K-step (d = 64 t + 16 kg + s for slot s).  A workgroup holds one wave per
-// kv head (up to 8) of one request and all its waves walk the same 16-page tiles, so a
-// block's records are read by one CU together; each tile is two load groups (columns
-// [0, r'/2) + mu + scales, then [r'/2, r')), double-buffered so one group streams in
-// while the other is multiplied.  Result rows 4kg..4kg+3 of lane (kg, n) are limbs
-// (hi, lo) of g = 2kg and 2kg+1, so the fp32 epilogue runs on every lane with 2kg < G.
+// Lanes.  lane = 16 kg + n.  The V product's 16 columns are PP = 16 / r' pages x r'
+// ranks (a tile of 16 pages is r' column groups): lane (kg, n) of group j feeds d group kg
+// of rank n % r' of page j PP + n / r', so one 16-byte load per lane reads, for each of
+// the group's PP pages, 64 r' contiguous bytes -- with the non-temporal hint this streams
+// at ~6.6 TB/s where one column of 16 pages (64 bytes each) streams at ~5.8 (measured
+// gathers of 1344-byte records).  A lane's rank terms sig2_k qh_k^2 of its r' groups are
+// summed over the r' lanes of each page by a DPP butterfly (rank_sum) that leaves lane n
+// with the page of group n % r' -- lane_page(n), whose mu codes, scales and score the lane
+// then carries (the mu product keeps pages on the columns).  Per-(page, rank) scales
+// reach the lanes through a 512-byte LDS transpose per wave.  A workgroup holds one wave
+// per kv head (up to 8) of one request; all its waves walk the same 16-page tiles, and
+// each tile is two load groups (column groups [0, r'/2) + mu + scales, then [r'/2, r')),
+// double-buffered so one group streams in while the other is multiplied.  Result rows
+// 4kg..4kg+3 of lane (kg, n) are limbs (hi, lo) of g = 2kg and 2kg+1, so the fp32
+// epilogue runs on every lane with 2kg < G.
 #include "score_mfma.h"
 
 namespace amass {
@@ -56,146 +62,215 @@ struct QuadParams {
 
 template <int RP, int VB> constexpr int vm_bytes() { return RP * col_bytes<VB>() + 128; }
 
+// Column groups: an MFMA's 16 columns are PP = 16 / r' pages x r' ranks, so a tile is r'
+// groups; lane (kg, n) of group j holds rank k = n % r' of page j PP + n / r'.
+template <int RP> constexpr int group_pages() { return SC_TILE / RP; }
+// the page whose mu, scales and score lane n carries (where the rank sums of the groups
+// land, see rank_sum): lane n holds group n % r' of its r'-lane set n / r'
+template <int RP>
+__device__ __forceinline__ int lane_page(int n) {
+    return (n % RP) * group_pages<RP>() + n / RP;
+}
+
 template <int RP, int VB>
-struct QuadGroupA {                       // columns [0, RP/2), mu, the page's scales
-    static constexpr int NC = RP / 2;
-    i32x4_t v[NC * loads_per_col<VB>()];
+struct QuadGroupA {                       // groups [0, RP/2), mu, the page's scales
+    static constexpr int NG = RP / 2;
+    i32x4_t v[NG * loads_per_col<VB>()];
     i32x4_t mu[2];
     i32x4_t meta;                         // 16 bytes kg of the 64-byte scale block
 };
 template <int RP, int VB>
-struct QuadGroupB {                       // columns [RP/2, RP)
-    static constexpr int NC = RP - RP / 2;
-    i32x4_t v[NC * loads_per_col<VB>()];
+struct QuadGroupB {                       // groups [RP/2, RP)
+    static constexpr int NG = RP - RP / 2;
+    i32x4_t v[NG * loads_per_col<VB>()];
 };
 
-// fp16 scales of one page, gathered to every lane of the page
-struct PageScales {
-    uint32_t vs[4], sg[4];                // halves k of V_scale / sig2
-    uint32_t mus;                         // mu_scale in the low half
-};
-
-// `lr` = the lane's record (block + head * VM + 16 kg); `moff` = its scale block - lr
-template <int RP, int VB>
-__device__ __forceinline__ void load_a(const int8_t* lr, QuadGroupA<RP, VB>& a, int moff) {
-    constexpr int CB = col_bytes<VB>();
-#pragma unroll
-    for (int c = 0; c < QuadGroupA<RP, VB>::NC; ++c) {
-        if constexpr (VB == 8) {
-            a.v[2 * c] = ld16(lr + c * CB);
-            a.v[2 * c + 1] = ld16(lr + c * CB + 64);
-        } else {
-            a.v[c] = ld16(lr + c * CB);
-        }
-    }
-    a.mu[0] = ld16(lr + RP * CB);
-    a.mu[1] = ld16(lr + RP * CB + 64);
-    a.meta = ld16(lr + moff);
+// V codes stream once per step: non-temporal 16-byte loads (each instruction reads PP
+// runs of 64 r' contiguous bytes; the hint measured +10 % over plain loads on this
+// pattern, and -10 % on one of 16 pages x 64 bytes)
+__device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
 }
 
-template <int RP, int VB>
-__device__ __forceinline__ void load_b(const int8_t* lr, QuadGroupB<RP, VB>& b) {
-    constexpr int CB = col_bytes<VB>();
-    constexpr int C0 = RP / 2;
-#pragma unroll
-    for (int c = 0; c < QuadGroupB<RP, VB>::NC; ++c) {
-        if constexpr (VB == 8) {
-            b.v[2 * c] = ld16(lr + (C0 + c) * CB);
-            b.v[2 * c + 1] = ld16(lr + (C0 + c) * CB + 64);
-        } else {
-            b.v[c] = ld16(lr + (C0 + c) * CB);
-        }
-    }
-}
-
-// lane n (kg 0) holds V_scale, lane n + 16 (kg 1) sig2, lane n + 32 (kg 2) mu_scale
+// block id of every group's page for this lane: lane m of a row carries page
+// lane_page(m); group j's page for lane n is lane_page((n / RP) RP + j)
 template <int RP>
-__device__ __forceinline__ PageScales gather_scales(i32x4_t meta, int n) {
-    PageScales s;
-    constexpr int NW = (RP + 1) / 2;      // dwords holding r' halves
+__device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) {
+    constexpr int PP = group_pages<RP>();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        s.vs[i] = i < NW ? (uint32_t)__shfl(meta[i], n, WAVE) : 0u;
-        s.sg[i] = i < NW ? (uint32_t)__shfl(meta[i], n + 16, WAVE) : 0u;
+    for (int j = 0; j < RP; ++j) {
+        int b = __builtin_amdgcn_readlane(blk_own, j);
+#pragma unroll
+        for (int pp = 1; pp < PP; ++pp) {
+            const int c = __builtin_amdgcn_readlane(blk_own, pp * RP + j);
+            b = n / RP == pp ? c : b;
+        }
+        gb[j] = b;
     }
-    s.mus = (uint32_t)__shfl(meta[0], n + 32, WAVE);
+}
+
+// `base` = rec + h * VM + the lane's V offset (16 (kg r' + n % r')); group j of block b
+template <int RP, int VB, int J0, int NG>
+__device__ __forceinline__ void load_groups(const int8_t* base, int64_t rec_sb,
+                                            const int (&gb)[RP], i32x4_t* v) {
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        const int8_t* p = base + (int64_t)gb[J0 + j] * rec_sb;
+        if constexpr (VB == 8) {
+            v[2 * j] = ld16_stream(p);
+            v[2 * j + 1] = ld16_stream(p + 64 * RP);
+        } else {
+            v[j] = ld16_stream(p);
+        }
+    }
+}
+
+// Per-(page, rank) V_scale and sig2 for this lane's groups, through an LDS transpose:
+// lanes (kg 0, m) / (kg 1, m) hold V_scale / sig2 of page lane_page(m) (halves 0..7 of
+// their 16 scale-block bytes); T[kg][k][m] is written, and lane n reads the r' halves
+// T[.][n % r'][(n / r') r' + j], j = 0..r'-1, in one load each.
+struct __align__(16) QuadLds {
+    uint16_t t[QS_MAXW][2][8][SC_TILE];
+};
+
+template <int RP>
+struct GroupScales {
+    uint32_t vs[(RP + 1) / 2], sg[(RP + 1) / 2];   // halves j
+};
+
+template <int RP>
+__device__ __forceinline__ GroupScales<RP> group_scales(QuadLds& L, int wave, i32x4_t meta,
+                                                        int n, int kg) {
+    if (kg < 2) {
+#pragma unroll
+        for (int k = 0; k < RP; ++k)
+            L.t[wave][kg][k][n] = (uint16_t)(((uint32_t)meta[k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
+    }
+    GroupScales<RP> s;
+    const int k = n % RP, m0 = (n / RP) * RP;
+    if constexpr (RP == 8) {
+        const uint4 a = *reinterpret_cast<const uint4*>(&L.t[wave][0][k][m0]);
+        const uint4 b = *reinterpret_cast<const uint4*>(&L.t[wave][1][k][m0]);
+        s.vs[0] = a.x; s.vs[1] = a.y; s.vs[2] = a.z; s.vs[3] = a.w;
+        s.sg[0] = b.x; s.sg[1] = b.y; s.sg[2] = b.z; s.sg[3] = b.w;
+    } else if constexpr (RP == 4) {
+        const uint2 a = *reinterpret_cast<const uint2*>(&L.t[wave][0][k][m0]);
+        const uint2 b = *reinterpret_cast<const uint2*>(&L.t[wave][1][k][m0]);
+        s.vs[0] = a.x; s.vs[1] = a.y;
+        s.sg[0] = b.x; s.sg[1] = b.y;
+    } else {
+        s.vs[0] = *reinterpret_cast<const uint32_t*>(&L.t[wave][0][k][m0]);
+        s.sg[0] = *reinterpret_cast<const uint32_t*>(&L.t[wave][1][k][m0]);
+    }
     return s;
 }
 
-// Running fp32 epilogue of one tile for g = 2kg + e: the quad sum in column order and
-// the mu term (the same operations, in the same order, as one pass over all columns).
-struct QuadAcc {
-    float quad[2];
-    float qmu[2];
-};
+template <int RP>
+__device__ __forceinline__ float group_half(const uint32_t (&w)[(RP + 1) / 2], int j) {
+    return fp16_to_f32((uint16_t)((w[j >> 1] >> (16 * (j & 1))) & 0xFFFFu));
+}
 
-template <int NC, int VB>
-__device__ __forceinline__ void cols_epilogue(const i32x4_t (&qa)[2], const i32x4_t* v,
-                                              const PageScales& sc, int col0, float qs0,
-                                              float qs1, QuadAcc& acc, int32_t* co, int co_g,
-                                              bool co_on) {
+// Sum over the r' lanes of each set n / r' (the ranks of one page) of q[j], leaving
+// lane n with group j = n % r': a butterfly in which each stage halves the registers a
+// lane keeps (the half of j its lane bit selects) and adds the partner's copy of them.
+// Partners: lane ^ 7 (row half mirror), ^ 2, ^ 1 -- opposite in the stage's bit.
+template <int C>
+__device__ __forceinline__ void rank_stage(float* q, int n) {
+    constexpr int H = C / 2;
+    constexpr int CTRL = C == 8 ? DPP_HALF_MIRROR : (C == 4 ? DPP_XOR2 : DPP_XOR1);
+    const bool up = (n & H) != 0;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        int x[2];
-        comb2<VB>(col_mfma<VB>(qa, &v[c * loads_per_col<VB>()]), x[0], x[1]);
-        const float vsc = half_at(sc.vs, col0 + c), sgc = half_at(sc.sg, col0 + c);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const float qhk = (float)x[e] * (e ? qs1 : qs0) * vsc;
-            acc.quad[e] += sgc * qhk * qhk;
-        }
-        if (co_on) {
-            co[col0 + c] = x[0];
-            co[co_g + col0 + c] = x[1];
-        }
+    for (int m = 0; m < H; ++m) {
+        const float keep = up ? q[m + H] : q[m];
+        const float send = up ? q[m] : q[m + H];
+        q[m] = keep + dpp_f<CTRL>(send);
     }
 }
 
-// comb_out row of (request, head, page, g = 2kg); the row of g + 1 follows at +RP+1.
+template <int RP>
+__device__ __forceinline__ float rank_sum(float (&q)[RP], int n) {
+    if constexpr (RP >= 8) rank_stage<8>(q, n);
+    if constexpr (RP >= 4) rank_stage<4>(q, n);
+    if constexpr (RP >= 2) rank_stage<2>(q, n);
+    return q[0];
+}
+
+// comb_out row of (request, head, page, g); the row of g + 1 follows at +RP+1.
 template <int RP>
 __device__ __forceinline__ int32_t* comb_row(const QuadParams& p, int req, int h, int page,
-                                             int kg) {
+                                             int g) {
     return p.comb_out + (((int64_t)req * p.n_kv + h) * p.max_pages + page) * (p.G * (RP + 1)) +
-           (int64_t)(2 * kg) * (RP + 1);
+           (int64_t)g * (RP + 1);
+}
+
+// Groups [J0, J0 + NG): the r'-rank products of lane (kg, n)'s page of each group, for
+// g = 2kg + e, into q[e][j] = sig2_k qh_k^2 (qh_k = comb * qs * V_scale_k).
+template <int RP, int VB, int J0, int NG, bool COMB>
+__device__ __forceinline__ void group_terms(const QuadParams& p, const i32x4_t (&qa)[2],
+                                            const i32x4_t* v, const GroupScales<RP>& sc,
+                                            float qs0, float qs1, float (&q)[2][RP], int req,
+                                            int h, int tile, int nsh, int n, int kg) {
+    constexpr int PP = group_pages<RP>();
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        int x[2];
+        comb2<VB>(col_mfma<VB>(qa, &v[j * loads_per_col<VB>()]), x[0], x[1]);
+        const float vsc = group_half<RP>(sc.vs, J0 + j), sgc = group_half<RP>(sc.sg, J0 + j);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float qhk = (float)x[e] * (e ? qs1 : qs0) * vsc;
+            q[e][J0 + j] = sgc * qhk * qhk;
+        }
+        if constexpr (COMB) {
+            const int page = tile * QS_TILE + (J0 + j) * PP + n / RP;
+            if (page < nsh) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (2 * kg + e < p.G) comb_row<RP>(p, req, h, page, 2 * kg + e)[n % RP] = x[e];
+            }
+        }
+    }
 }
 
 template <int RP, int VB, bool COMB>
 __device__ __forceinline__ void tile_start(const QuadParams& p, const i32x4_t (&qa)[2],
-                                           const QuadGroupA<RP, VB>& a, const PageScales& sc,
-                                           float qs0, float qs1, QuadAcc& acc, int req, int h,
-                                           int page, bool valid, int kg) {
-    constexpr int CA = RP / 2;
-    const bool co_on = COMB && valid && 2 * kg < p.G;
-    const bool co1 = 2 * kg + 1 < p.G;
-    int32_t* co = co_on ? comb_row<RP>(p, req, h, page, kg) : nullptr;
-    acc.quad[0] = acc.quad[1] = 0.f;
-    cols_epilogue<CA, VB>(qa, a.v, sc, 0, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on);
+                                           const QuadGroupA<RP, VB>& a, const GroupScales<RP>& sc,
+                                           float qs0, float qs1, float (&q)[2][RP],
+                                           float (&qmu)[2], int req, int h, int tile,
+                                           int nsh, int n, int kg) {
+    group_terms<RP, VB, 0, RP / 2, COMB>(p, qa, a.v, sc, qs0, qs1, q, req, h, tile, nsh, n, kg);
     i32x4_t m = {0, 0, 0, 0};
     m = mfma_i8(qa[0], a.mu[0], m);
     m = mfma_i8(qa[1], a.mu[1], m);
     const int cmu[2] = {m[0] * 128 + m[1], m[2] * 128 + m[3]};
-    const float musf = fp16_to_f32((uint16_t)(sc.mus & 0xFFFFu));
+    const uint32_t mus = (uint32_t)__shfl(a.meta[0], n + 32, WAVE);   // lane (2, n): half 16
+    const float musf = fp16_to_f32((uint16_t)(mus & 0xFFFFu));
 #pragma unroll
-    for (int e = 0; e < 2; ++e) acc.qmu[e] = (float)cmu[e] * (e ? qs1 : qs0) * musf * p.scale;
-    if (co_on) {
-        co[RP] = cmu[0];
-        if (co1) co[2 * RP + 1] = cmu[1];
+    for (int e = 0; e < 2; ++e) qmu[e] = (float)cmu[e] * (e ? qs1 : qs0) * musf * p.scale;
+    if constexpr (COMB) {
+        const int page = tile * QS_TILE + lane_page<RP>(n);
+        if (page < nsh) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                if (2 * kg + e < p.G) comb_row<RP>(p, req, h, page, 2 * kg + e)[RP] = cmu[e];
+        }
     }
 }
 
 template <int RP, int VB, bool NRM, bool COMB>
 __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (&qa)[2],
-                                            const QuadGroupB<RP, VB>& b, const PageScales& sc,
-                                            QuadAcc& acc, int req, int h, int page, bool valid,
-                                            int kg, float qs0, float qs1, float qcoef) {
-    constexpr int CA = RP / 2;
-    const bool co_on = COMB && valid && 2 * kg < p.G;
-    const bool co1 = 2 * kg + 1 < p.G;
-    int32_t* co = co_on ? comb_row<RP>(p, req, h, page, kg) : nullptr;
-    cols_epilogue<RP - CA, VB>(qa, b.v, sc, CA, qs0, qs1, acc, co, co1 ? RP + 1 : 0, co_on);
+                                            const QuadGroupB<RP, VB>& b,
+                                            const GroupScales<RP>& sc, float (&q)[2][RP],
+                                            const float (&qmu)[2], int req, int h, int tile,
+                                            int nsh, int n, int kg, float qs0, float qs1,
+                                            float qcoef) {
+    group_terms<RP, VB, RP / 2, RP - RP / 2, COMB>(p, qa, b.v, sc, qs0, qs1, q, req, h, tile,
+                                                   nsh, n, kg);
+    const int page = tile * QS_TILE + lane_page<RP>(n);
+    const bool valid = page < nsh;
     float S[2];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) S[e] = acc.qmu[e] + qcoef * acc.quad[e];
+    for (int e = 0; e < 2; ++e) S[e] = qmu[e] + qcoef * rank_sum<RP>(q[e], n);
     const int g0 = 2 * kg, g1 = 2 * kg + 1;
     if constexpr (NRM) {
         const int64_t row = (int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh;
@@ -225,6 +300,7 @@ template <int RP, int VB, bool NRM, bool COMB>
 __global__ __launch_bounds__(QS_MAXW * WAVE)
 void quad_score_kernel(const QuadParams p) {
     constexpr int VM = vm_bytes<RP, VB>();
+    __shared__ QuadLds lds;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kg = lane >> 4;
@@ -242,30 +318,32 @@ void quad_score_kernel(const QuadParams p) {
     uint32_t qw[2][8];          // bf16 pairs, d = 64 t + 16 kg + 2 i (+1)
     load_q_rows(p.q, p.q_st, p.q_hs, req, h, p.G, n, kg, false, qw);
 
-    // tile addressing: lane n owns page 16 tile + n; clamped pages load valid data and
-    // are never written
-    auto page_of = [&](int tile) { return tile * QS_TILE + n; };
-    auto lane_blk = [&](int tile) -> int64_t {
-        const int page = page_of(tile);
-        const int pc = page < nsh ? page : nsh - 1;
-        return (int64_t)p.bt[(int64_t)req * p.bt_st + pc];
+    // lane n's own page (mu, scales, score) is lane_page(n) of the tile; clamped pages
+    // load valid data and are never written
+    const int own = lane_page<RP>(n);
+    auto own_blk = [&](int tile) -> int {
+        const int page = tile * QS_TILE + own;
+        return p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)];
     };
-    // the loop carries block ids, not record pointers: carried pointers made the
-    // compiler double the load buffers and copy them at the loop head
+    const int8_t* hrec = p.rec + (int64_t)h * VM;
+    const int8_t* vbase = hrec + 16 * (kg * RP + n % RP);          // + block * rec_sb
     const int64_t rhead = (int64_t)h * VM + 16 * kg;
     const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
-    auto lane_rec = [&](int64_t blk) { return p.rec + blk * p.rec_sb + rhead; };
+    auto lane_rec = [&](int blk) { return p.rec + (int64_t)blk * p.rec_sb + rhead; };
 
     int tile = t0;
-    const int8_t* lr = lane_rec(lane_blk(tile));
+    int blk = own_blk(tile);
+    int gb[RP];
+    group_blocks<RP>(blk, n, gb);
     QuadGroupA<RP, VB> ga;
-    QuadGroupB<RP, VB> gb;
-    load_a<RP, VB>(lr, ga, moff);
-    int64_t bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
-    // issue order A, next block id, B -- the order the loop keeps, so the loop's wait
-    // counts hold on entry as well
+    QuadGroupB<RP, VB> gbuf;
+    load_groups<RP, VB, 0, RP / 2>(vbase, p.rec_sb, gb, ga.v);
+    ga.mu[0] = ld16(lane_rec(blk) + RP * col_bytes<VB>());
+    ga.mu[1] = ld16(lane_rec(blk) + RP * col_bytes<VB>() + 64);
+    ga.meta = ld16(lane_rec(blk) + moff);
+    int blk_next = own_blk(cnt > 1 ? tile + wstride : tile);
     __builtin_amdgcn_sched_barrier(0);
-    load_b<RP, VB>(lr, gb);
+    load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, p.rec_sb, gb, gbuf.v);
 
     i32x4_t qa[2];
     const float qs = quantize_q_rows(qw, n, qa);
@@ -276,28 +354,29 @@ void quad_score_kernel(const QuadParams p) {
     // ---- tile loop: group A of tile i+1 streams in while group B of tile i is used,
     // and group B of tile i+1 while group A of tile i+1 is used.  Every load in the
     // steady state is unconditional so the wait counts stay exact. -----------------------
-    QuadAcc acc;
+    float q[2][RP];
+    float qmu[2];
     for (int i = 0; i + 1 < cnt; ++i) {
-        const int page = page_of(tile);
-        const bool valid = page < nsh;
-        const PageScales sc = gather_scales<RP>(ga.meta, n);
-        tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, kg);
+        const GroupScales<RP> sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
+        tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);
         // keep the refill of a buffer after its last use (bounds the live registers)
         __builtin_amdgcn_sched_barrier(0);
-        const int8_t* ln = lane_rec(bn_next);
-        load_a<RP, VB>(ln, ga, moff);
-        bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
-        tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1,
-                                       qcoef);
+        group_blocks<RP>(blk_next, n, gb);
+        load_groups<RP, VB, 0, RP / 2>(vbase, p.rec_sb, gb, ga.v);
+        ga.mu[0] = ld16(lane_rec(blk_next) + RP * col_bytes<VB>());
+        ga.mu[1] = ld16(lane_rec(blk_next) + RP * col_bytes<VB>() + 64);
+        ga.meta = ld16(lane_rec(blk_next) + moff);
+        blk_next = own_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
+        tile_finish<RP, VB, NRM, COMB>(p, qa, gbuf, sc, q, qmu, req, h, tile, nsh, n, kg, qs0,
+                                       qs1, qcoef);
         __builtin_amdgcn_sched_barrier(0);
-        load_b<RP, VB>(ln, gb);
+        load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, p.rec_sb, gb, gbuf.v);
         tile += wstride;
     }
-    const int page = page_of(tile);
-    const bool valid = page < nsh;
-    const PageScales sc = gather_scales<RP>(ga.meta, n);
-    tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, kg);
-    tile_finish<RP, VB, NRM, COMB>(p, qa, gb, sc, acc, req, h, page, valid, kg, qs0, qs1, qcoef);
+    const GroupScales<RP> sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
+    tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);
+    tile_finish<RP, VB, NRM, COMB>(p, qa, gbuf, sc, q, qmu, req, h, tile, nsh, n, kg, qs0, qs1,
+                                   qcoef);
 }
 
 template <int RP, int VB, bool NRM, bool COMB>

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 5
+#define AMASS_ABI_VERSION 6
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -48,9 +48,10 @@ extern "C" {
  * Summary records.  The reference's five per-(block, kv-head) slabs (quad_mu, mu_scale,
  * quad_V, V_scale, quad_sig2) are packed per block, AMASS_QUAD_REC_BYTES(rank, v_bits)
  * bytes per kv head (VM = r'*CB + 128 of them first, in head order, then 64 per head):
- *   head h at h*VM:         quad_V column-major, column k = CB bytes; int8 CB = d = 128
- *                           (byte j = code[j]); int4 CB = 64 (byte j = code[j] | code[j+64] << 4),
- *                           then the 128 quad_mu int8 codes
+ *   head h at h*VM:         quad_V tiled, r'*CB bytes: 16 bytes per (K-step t, d group kg,
+ *                           column k) at ((t*4 + kg)*r' + k)*16, byte i = code[64t + 16kg + i]
+ *                           (int8, CB = 128); int4 (CB = 64): t = 0 only, byte i of (kg, k) =
+ *                           code[16kg+i] | code[16kg+i+64] << 4; then the 128 quad_mu int8 codes
  *   head h at n_kv*VM+64h:  fp16 V_scale[0..r') at half 0, sig2[0..r') at half 8,
  *                           mu_scale at half 16, the rest zero
  * rec points at block 0 of the layer, rec_sb is the block stride in bytes (at least

@@ -1,4 +1,5 @@
-"""Column-major quad_V layout of the gfx950 score kernel vs the reference layout.
+"""quad_V layouts of the gfx950 score kernels vs the reference layout (column-major for
+r8 / CLSE records, tiled for the quad kernel).
 
 The kernel reads quad_V as (.., r', d) int8 or (.., r', d/2) int4 with byte
 j = code[j] | code[j + d/2] << 4; the reference stores (.., d, r') int8 or (.., d, r'/2)
@@ -32,6 +33,32 @@ def test_round_trip_and_positions(bits, r):
         lo, hi = b & 0xF, b >> 4
         lo, hi = (lo - 16 if lo >= 8 else lo), (hi - 16 if hi >= 8 else hi)
         assert lo == int(code[2, 0, 5, r - 1]) and hi == int(code[2, 0, 69, r - 1])
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("r", [2, 4, 8])
+def test_tiled_round_trip_and_positions(bits, r):
+    """The quad kernel's tiled V: 16 bytes per (K-step t, d group kg, column k) at
+    ((t * 4 + kg) * r + k) * 16, byte i = code[64 t + 16 kg + i] (int4: t folded into the
+    nibbles of (kg, k)); every code checked against that formula."""
+    g = torch.Generator().manual_seed(r * 10 + bits + 1)
+    lvl = 127 if bits == 8 else 7
+    code = torch.randint(-lvl, lvl + 1, (2, 3, 128, r), generator=g, dtype=torch.int8)
+    ref = code if bits == 8 else torch.from_numpy(oq.pack_i4(code.numpy()))
+    dev = v_to_device(ref, bits, tiled=True)
+    assert torch.equal(v_to_reference(dev, bits, tiled=True), ref)
+    flat = dev.reshape(2, 3, -1).view(torch.uint8).to(torch.int32)
+    for d in range(128):
+        for k in range(r):
+            t, kg, i = d // 64, (d % 64) // 16, d % 16
+            if bits == 8:
+                got = flat[..., ((t * 4 + kg) * r + k) * 16 + i]
+                got = torch.where(got >= 128, got - 256, got)
+            else:
+                b = flat[..., (kg * r + k) * 16 + i]
+                nib = (b >> (4 * t)) & 0xF
+                got = torch.where(nib >= 8, nib - 16, nib)
+            assert torch.equal(got, code[..., d, k].to(torch.int32)), (d, k)
 
 
 def test_state_load_reference_round_trip():
