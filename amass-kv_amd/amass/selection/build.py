@@ -126,7 +126,7 @@ def r8_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> Non
     c_code, c_s = _quant_c(c, st.c_grain, st.c_bits)
     st.r8_mu[layer, blocks] = mu_code
     st.mu_scale[layer, blocks] = mu_s
-    st.r8_Vk[layer, blocks] = v_to_device(vk_code, st.vk_bits)
+    st.r8_Vk[layer, blocks] = v_to_device(vk_code, st.vk_bits, tiled=True)
     st.Vk_scale[layer, blocks] = vk_s
     st.r8_c[layer, blocks] = c_code
     st.c_scale[layer, blocks] = c_s

@@ -4,7 +4,7 @@ Restates selection/quad_build.py:56-198 of the reference: the same page-gram eig
 r8 builder (:mod:`amass.selection.build`), storing the top-r' eigenvalues ``sig2`` instead
 of the per-key coordinates.  Per (block, kv-head): quad_mu/mu_scale = int8 page mean,
 quad_V/V_scale = Vk = dc^T U8 / S8 quantised per column (int8 or packed int4, stored
-in the column-major kernel layout),
+in the tiled kernel layout),
 quad_sig2 = fp16(S2r), quad_tag = leading TAGW channels of the page's last key.  A device
 K is summarised by the HIP builder (``amass_summary_build``), a host K by the torch
 restatement below.

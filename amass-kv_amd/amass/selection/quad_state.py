@@ -22,13 +22,13 @@ Every V / mu record is whole 128-byte lines and a block's n_kv records are conti
 The tiled V lets the gfx950 score kernel feed an int8 matrix-core instruction whose 16
 columns are 16 / r' pages x r' ranks with loads that each read 64 r' contiguous bytes
 of every page they touch.  ``v_to_device`` / ``v_to_reference`` convert V between this
-and the reference layout; ``load_reference`` and ``reference_V`` use them.  CLSE keeps
-V column-major (column k at k * CB), the layout of the r8 records.
+and the reference layout; ``load_reference`` and ``reference_V`` use them.  CLSE and
+the r8 records keep V in the same tiled order.
 
 CLSE (``coords="lse"``, the reference's ``score="clse"``) keeps the per-key coordinates
 and the residual scatter energy instead of sig2, in the r8 record layout
 (AMASS_R8_REC_BYTES, see :mod:`amass.selection.state`): per head
-``[quad_V column-major | quad_mu | quad_c (page, r'[/2])]`` and a 64-byte scale block
+``[quad_V tiled | quad_mu | quad_c (page, r'[/2])]`` and a 64-byte scale block
 with V_scale at half 0, c_scale at halves 8..23 (``c_grain="page"``: one scale per
 (block, head), kept in all 16 halves and exposed as half 8), mu_scale at half 24 and
 quad_resid at half 25; ``quad_sig2`` is None there.
@@ -138,7 +138,7 @@ class QuadState:
         self.v_grain = v_grain
         self.v_bits, self.mu_bits = int(v_bits), 8
         self.coords, self.c_bits, self.c_grain = coords, int(c_bits), c_grain
-        self.v_tiled = coords == "none"                   # the quad kernel's V layout
+        self.v_tiled = True                               # the score kernels' V layout
         self.combine = combine
         self.device = device
         i8, f16, bf16 = torch.int8, torch.float16, torch.bfloat16
@@ -187,7 +187,7 @@ class QuadState:
         return self.quad_rec[0].numel() + 2 * self.quad_tag[0].numel()
 
     def layer_state(self, layer: int):
-        """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer`` (V column-major)."""
+        """(mu, mu_scale, V, V_scale, sig2, tag) views of ``layer`` (V tiled)."""
         sig2 = self.quad_sig2[layer] if self.quad_sig2 is not None else None   # None: CLSE
         return (self.quad_mu[layer], self.mu_scale[layer], self.quad_V[layer],
                 self.V_scale[layer], sig2, self.quad_tag[layer])

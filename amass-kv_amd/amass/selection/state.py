@@ -8,8 +8,10 @@ per kv head:
 
   r8_rec   (L, NB, n_kv * REC)  int8, per block:
     n_kv records of VM = r*CB + 128 + 16*r*c_bits/8 bytes, head h at h * VM:
-      r8_Vk    (L, NB, n_kv, r, CB)   int8  column-major: column k holds CB bytes;
-               int8 CB = d (byte j = code[j]); int4 CB = d/2, byte j = code[j] | code[j+d/2] << 4
+      r8_Vk    (L, NB, n_kv, r, CB)   int8  (r * CB bytes) tiled like quad_V: 16 bytes per
+               (K-step t, d group kg, column k) at ((t * 4 + kg) * r + k) * 16, byte i =
+               code[64 t + 16 kg + i]; int8 CB = d, int4 CB = d/2 with byte i of (kg, k) =
+               code[16 kg + i] | code[16 kg + i + 64] << 4
                (the reference keeps (.., d, r) with two columns per int4 byte)
       r8_mu    (L, NB, n_kv, d)       int8  page-mean codes
       r8_c     (L, NB, n_kv, page, r) int8  per-key coordinates (int4: (.., page, r/2),
@@ -20,10 +22,10 @@ per kv head:
       mu_scale (L, NB, n_kv)          half 24; the other halves are zero
   r8_tag   (L, NB, n_kv, TAGW)  bf16  NaN-init content tag (separate)
 
-A block's records are contiguous and the score kernel feeds each 16-byte load of a Vk
-column straight into an int8 matrix-core instruction (the quad record's reasoning,
-:mod:`amass.selection.quad_state`).  ``reference_Vk`` / ``load_reference`` convert Vk
-between this and the reference layout.
+A block's records are contiguous and the score kernel's loads each read 64 r contiguous
+Vk bytes of every page they touch, fed straight into int8 matrix-core instructions (the
+quad record's reasoning, :mod:`amass.selection.quad_state`).  ``reference_Vk`` /
+``load_reference`` convert Vk between this and the reference layout.
 
 Per-step outputs (request-row keyed): score (R, n_kv, MP) fp32, page_table (R, n_kv, MP)
 int32, page_cnt (R, n_kv) int32, n_pages / n_sel_hi / b_fix (R,) int32, budget64.
@@ -93,8 +95,8 @@ class R8State:
         return self.r8_rec[0].numel() + 2 * self.r8_tag[0].numel()
 
     def layer_state(self, layer: int):
-        """(mu, mu_scale, Vk, Vk_scale, c, c_scale, tag) views of ``layer`` (Vk
-        column-major; :meth:`reference_Vk` gives the reference layout)."""
+        """(mu, mu_scale, Vk, Vk_scale, c, c_scale, tag) views of ``layer`` (Vk tiled;
+        :meth:`reference_Vk` gives the reference layout)."""
         return (self.r8_mu[layer], self.mu_scale[layer], self.r8_Vk[layer],
                 self.Vk_scale[layer], self.r8_c[layer], self.c_scale[layer],
                 self.r8_tag[layer])
@@ -106,7 +108,8 @@ class R8State:
         dev = self.r8_rec.device
         self.r8_mu[layer].copy_(torch.as_tensor(mu).to(dev))
         self.mu_scale[layer].copy_(torch.as_tensor(mu_scale).to(dev))
-        self.r8_Vk[layer].copy_(v_to_device(torch.as_tensor(Vk).to(dev), self.vk_bits))
+        self.r8_Vk[layer].copy_(v_to_device(torch.as_tensor(Vk).to(dev), self.vk_bits,
+                                            tiled=True))
         self.Vk_scale[layer].copy_(torch.as_tensor(Vk_scale).to(dev))
         self.r8_c[layer].copy_(torch.as_tensor(c).to(dev))
         self.c_scale[layer].copy_(torch.as_tensor(c_scale).to(dev))
@@ -114,4 +117,4 @@ class R8State:
     def reference_Vk(self, layer: int) -> torch.Tensor:
         """r8_Vk of ``layer`` in the reference layout (NB, n_kv, d, r[/2])."""
         from .quad_state import v_to_reference
-        return v_to_reference(self.r8_Vk[layer], self.vk_bits)
+        return v_to_reference(self.r8_Vk[layer], self.vk_bits, tiled=True)

@@ -264,18 +264,17 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
 #pragma unroll
         for (int k = 0; k < 8; ++k) vsc[k] = quant_scale(amx[k], vlvl);
     }
-    // quad: the tiled layout of the score kernel's column groups, 16 bytes per (K-step t,
-    // d group kg, column k) at ((t * 4 + kg) * r + k) * 16 (int4: t folded into the
-    // nibbles); r8 / CLSE: column-major, column k at k * CB
+    // the tiled layout of the score kernels' column groups: 16 bytes per (K-step t, d
+    // group kg, column k) at ((t * 4 + kg) * r + k) * 16 (int4: t folded into the nibbles)
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         if (k < r) {
             const int c0 = quant_code(vk[0][k], vsc[k], vlvl);
             const int c1 = quant_code(vk[1][k], vsc[k], vlvl);
-            const int o0 = R8 ? k * CB + lane : ((lane >> 4) * r + k) * 16 + (lane & 15);
+            const int o0 = ((lane >> 4) * r + k) * 16 + (lane & 15);
             if (a.v_bits == 8) {
                 rec[o0] = (int8_t)c0;
-                rec[o0 + (R8 ? 64 : 64 * r)] = (int8_t)c1;
+                rec[o0 + 64 * r] = (int8_t)c1;
             } else {
                 rec[o0] = (int8_t)((c0 & 0xF) | ((c1 & 0xF) << 4));
             }

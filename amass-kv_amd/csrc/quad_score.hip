@@ -62,16 +62,6 @@ struct QuadParams {
 
 template <int RP, int VB> constexpr int vm_bytes() { return RP * col_bytes<VB>() + 128; }
 
-// Column groups: an MFMA's 16 columns are PP = 16 / r' pages x r' ranks, so a tile is r'
-// groups; lane (kg, n) of group j holds rank k = n % r' of page j PP + n / r'.
-template <int RP> constexpr int group_pages() { return SC_TILE / RP; }
-// the page whose mu, scales and score lane n carries (where the rank sums of the groups
-// land, see rank_sum): lane n holds group n % r' of its r'-lane set n / r'
-template <int RP>
-__device__ __forceinline__ int lane_page(int n) {
-    return (n % RP) * group_pages<RP>() + n / RP;
-}
-
 template <int RP, int VB>
 struct QuadGroupA {                       // groups [0, RP/2), mu, the page's scales
     static constexpr int NG = RP / 2;
@@ -84,46 +74,6 @@ struct QuadGroupB {                       // groups [RP/2, RP)
     static constexpr int NG = RP - RP / 2;
     i32x4_t v[NG * loads_per_col<VB>()];
 };
-
-// V codes stream once per step: non-temporal 16-byte loads (each instruction reads PP
-// runs of 64 r' contiguous bytes; the hint measured +10 % over plain loads on this
-// pattern, and -10 % on one of 16 pages x 64 bytes)
-__device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
-}
-
-// block id of every group's page for this lane: lane m of a row carries page
-// lane_page(m); group j's page for lane n is lane_page((n / RP) RP + j)
-template <int RP>
-__device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) {
-    constexpr int PP = group_pages<RP>();
-#pragma unroll
-    for (int j = 0; j < RP; ++j) {
-        int b = __builtin_amdgcn_readlane(blk_own, j);
-#pragma unroll
-        for (int pp = 1; pp < PP; ++pp) {
-            const int c = __builtin_amdgcn_readlane(blk_own, pp * RP + j);
-            b = n / RP == pp ? c : b;
-        }
-        gb[j] = b;
-    }
-}
-
-// `base` = rec + h * VM + the lane's V offset (16 (kg r' + n % r')); group j of block b
-template <int RP, int VB, int J0, int NG>
-__device__ __forceinline__ void load_groups(const int8_t* base, int64_t rec_sb,
-                                            const int (&gb)[RP], i32x4_t* v) {
-#pragma unroll
-    for (int j = 0; j < NG; ++j) {
-        const int8_t* p = base + (int64_t)gb[J0 + j] * rec_sb;
-        if constexpr (VB == 8) {
-            v[2 * j] = ld16_stream(p);
-            v[2 * j + 1] = ld16_stream(p + 64 * RP);
-        } else {
-            v[j] = ld16_stream(p);
-        }
-    }
-}
 
 // Per-(page, rank) V_scale and sig2 for this lane's groups, through an LDS transpose:
 // lanes (kg 0, m) / (kg 1, m) hold V_scale / sig2 of page lane_page(m) (halves 0..7 of

@@ -9,21 +9,24 @@
 //   score    = max_g S_g   (kv-union group max)
 //
 // Front end: the quad kernel's int8 matrix-core product (score_mfma.h) over the page's
-// column-major Vk and its mean codes -- exact int32 sums comb = sum_d qi * code.  For
-// G < 8 the unused M rows repeat the group's limb rows, so lane (kg, n) receives the sums
-// of heads g0 = 2 (kg % GP), g1 = g0 + 1 (GP = max(G/2, 1) head pairs) and the 4 / GP
-// lane groups holding the same pair split the page's 16 tokens between them (TPL tokens
-// each): the token tail needs no exchange of q~, only a max and a sum across those
-// groups for the logsumexp, and a max across pairs for the group max.
+// tiled Vk and its mean codes -- exact int32 sums comb = sum_d qi * code.  The Vk product
+// runs on column groups (16 / r pages x r ranks, loads of 64 r contiguous bytes per page,
+// non-temporal); its int32 pairs go through a per-wave LDS transpose back to one page
+// per lane -- lane n carries page lane_page(n) of the tile, whose mu codes, scales and c
+// rows it loads.  For G < 8 the unused M rows repeat the group's limb rows, so lane
+// (kg, n) receives the sums of heads g0 = 2 (kg % GP), g1 = g0 + 1 (GP = max(G/2, 1)
+// head pairs) and the 4 / GP lane groups holding the same pair split the page's 16 tokens
+// between them (TPL tokens each): the token tail needs no exchange of q~, only a max and
+// a sum across those groups for the logsumexp, and a max across pairs for the group max.
 //
 // Layout (AMASS_R8_REC_BYTES per kv head).  Per block, the n_kv heads' records
-// [Vk column-major: r columns of CB bytes | 128 mu codes | c: 16 token rows of
-// r * c_bits / 8 bytes], then the n_kv heads' 64-byte fp16 scale blocks (Vk_scale at
-// half 0, c_scale at halves 8..23, mu_scale at half 24).  Vk int8 column k is CB = 128
-// bytes (byte j = code[j]); int4 CB = 64 with byte j = code[j] | code[j + 64] << 4.  c
-// rows keep the reference order (int4: two columns per byte, low nibble = even column).
-// Each tile is two load groups -- columns [0, r/2) + mu + scales, then [r/2, r) + the
-// lane's c rows -- double-buffered as in the quad kernel.
+// [Vk tiled: 16 bytes per (K-step t, d group kg, column k) at ((t * 4 + kg) * r + k) * 16
+// (int4: t folded into the nibbles) | 128 mu codes | c: 16 token rows of r * c_bits / 8
+// bytes], then the n_kv heads' 64-byte fp16 scale blocks (Vk_scale at half 0, c_scale at
+// halves 8..23, mu_scale at half 24).  c rows keep the reference order (int4: two columns
+// per byte, low nibble = even column).  Each tile is two load groups -- column groups
+// [0, r/2) + mu + scales, then [r/2, r) + the lane's c rows -- double-buffered as in the
+// quad kernel.
 //
 // CLSE (reference selection/quad_score.py:156-276, score="clse") is the same computation
 // over the same record (its quad_V / quad_mu / quad_c / c_scale; the residual scatter
@@ -70,52 +73,39 @@ struct R8Split {
 };
 
 template <int RP, int VB>
-struct R8GroupA {                         // columns [0, RP/2), mu, the page's scales
-    static constexpr int NC = RP / 2;
-    i32x4_t v[NC * loads_per_col<VB>()];
+struct R8GroupA {                         // column groups [0, RP/2), mu, the page's scales
+    static constexpr int NG = RP / 2;
+    i32x4_t v[NG * loads_per_col<VB>()];
     i32x4_t mu[2];
     i32x4_t meta;                         // 16 bytes kg of the 64-byte scale block
 };
 template <int RP, int VB>
-struct R8GroupB {                         // columns [RP/2, RP)
-    static constexpr int NC = RP - RP / 2;
-    i32x4_t v[NC * loads_per_col<VB>()];
+struct R8GroupB {                         // column groups [RP/2, RP)
+    static constexpr int NG = RP - RP / 2;
+    i32x4_t v[NG * loads_per_col<VB>()];
 };
 template <int CL>
 struct R8GroupC {                         // the lane's c rows
     uint32_t c[CL / 4];
 };
 
+// `vbase` = rec + h * VM + the lane's V offset, `gb` the blocks of the lane's group
+// pages; `lr` = the lane's own-page record (block + head * VM + 16 kg), `moff` = its
+// scale block - lr
 template <int RP, int VB>
-__device__ __forceinline__ void r8_load_a(const int8_t* lr, R8GroupA<RP, VB>& a, int moff) {
-    constexpr int CB = col_bytes<VB>();
-#pragma unroll
-    for (int c = 0; c < R8GroupA<RP, VB>::NC; ++c) {
-        if constexpr (VB == 8) {
-            a.v[2 * c] = ld16(lr + c * CB);
-            a.v[2 * c + 1] = ld16(lr + c * CB + 64);
-        } else {
-            a.v[c] = ld16(lr + c * CB);
-        }
-    }
-    a.mu[0] = ld16(lr + RP * CB);
-    a.mu[1] = ld16(lr + RP * CB + 64);
+__device__ __forceinline__ void r8_load_a(const int8_t* vbase, int64_t rec_sb,
+                                          const int (&gb)[RP], const int8_t* lr,
+                                          R8GroupA<RP, VB>& a, int moff) {
+    load_groups<RP, VB, 0, RP / 2>(vbase, rec_sb, gb, a.v);
+    a.mu[0] = ld16(lr + RP * col_bytes<VB>());
+    a.mu[1] = ld16(lr + RP * col_bytes<VB>() + 64);
     a.meta = ld16(lr + moff);
 }
 
 template <int RP, int VB>
-__device__ __forceinline__ void r8_load_b(const int8_t* lr, R8GroupB<RP, VB>& b) {
-    constexpr int CB = col_bytes<VB>();
-    constexpr int C0 = RP / 2;
-#pragma unroll
-    for (int c = 0; c < R8GroupB<RP, VB>::NC; ++c) {
-        if constexpr (VB == 8) {
-            b.v[2 * c] = ld16(lr + (C0 + c) * CB);
-            b.v[2 * c + 1] = ld16(lr + (C0 + c) * CB + 64);
-        } else {
-            b.v[c] = ld16(lr + (C0 + c) * CB);
-        }
-    }
+__device__ __forceinline__ void r8_load_b(const int8_t* vbase, int64_t rec_sb,
+                                          const int (&gb)[RP], R8GroupB<RP, VB>& b) {
+    load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, rec_sb, gb, b.v);
 }
 
 template <int CL>
@@ -200,19 +190,22 @@ __device__ __forceinline__ int32_t* r8_comb_row(const R8Params& p, int G, int re
            (int64_t)g * (RP + 1);
 }
 
-template <int NC, int VB, int RP>
-__device__ __forceinline__ void r8_cols(const i32x4_t (&qa)[2], const i32x4_t* v,
-                                        const uint32_t (&vs)[4], int col0, float qs0, float qs1,
-                                        R8Acc<RP>& acc, int32_t* co0, int32_t* co1) {
+// The int32 contractions of the column groups pass through LDS back to one page per
+// lane: lane (kg, n) of group j stores its (g0, g1) pair at [kg][page j PP + n / r][rank
+// n % r]; after the last group, lane n reads the r ranks of its own page lane_page(n).
+struct __align__(16) R8Lds {
+    int2 x[R8_MAXW][4][SC_TILE][8];
+};
+
+template <int RP, int VB, int J0, int NG>
+__device__ __forceinline__ void r8_groups(const i32x4_t (&qa)[2], const i32x4_t* v,
+                                          int2 (&row)[SC_TILE][8], int n) {
+    constexpr int PP = group_pages<RP>();
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        int x[2];
-        comb2<VB>(col_mfma<VB>(qa, &v[c * loads_per_col<VB>()]), x[0], x[1]);
-        const float vsc = half_at(vs, col0 + c);
-        acc.qt[0][col0 + c] = (float)x[0] * qs0 * vsc;
-        acc.qt[1][col0 + c] = (float)x[1] * qs1 * vsc;
-        if (co0) co0[col0 + c] = x[0];
-        if (co1) co1[col0 + c] = x[1];
+    for (int j = 0; j < NG; ++j) {
+        int x0, x1;
+        comb2<VB>(col_mfma<VB>(qa, &v[j * loads_per_col<VB>()]), x0, x1);
+        row[(J0 + j) * PP + n / RP][n % RP] = make_int2(x0, x1);
     }
 }
 
@@ -220,21 +213,50 @@ template <int RP, int VB, int G, bool COMB>
 __device__ __forceinline__ void r8_tile_start(const R8Params& p, const i32x4_t (&qa)[2],
                                               const R8GroupA<RP, VB>& a,
                                               const R8Scales<RP, R8Split<G>::TPL>& sc, float qs0,
-                                              float qs1, R8Acc<RP>& acc, int req, int h,
-                                              int page, bool valid, int pair, int part) {
-    const bool co_on = COMB && valid && part == 0;
-    int32_t* co0 = co_on ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair) : nullptr;
-    int32_t* co1 = (co_on && G >= 2) ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair + 1)
-                                     : nullptr;
-    r8_cols<RP / 2, VB, RP>(qa, a.v, sc.vs, 0, qs0, qs1, acc, co0, co1);
+                                              float qs1, R8Acc<RP>& acc, int2 (&row)[SC_TILE][8],
+                                              int req, int h, int page, bool valid, int pair,
+                                              int part, int n) {
+    r8_groups<RP, VB, 0, RP / 2>(qa, a.v, row, n);
     i32x4_t m = {0, 0, 0, 0};
     m = mfma_i8(qa[0], a.mu[0], m);
     m = mfma_i8(qa[1], a.mu[1], m);
     const int cmu[2] = {m[0] * 128 + m[1], m[2] * 128 + m[3]};
     acc.qmu[0] = (float)cmu[0] * qs0 * sc.mus * p.scale;
     acc.qmu[1] = (float)cmu[1] * qs1 * sc.mus * p.scale;
-    if (co0) co0[RP] = cmu[0];
-    if (co1) co1[RP] = cmu[1];
+    if (COMB && valid && part == 0) {
+        r8_comb_row<RP>(p, G, req, h, page, 2 * pair)[RP] = cmu[0];
+        if (G >= 2) r8_comb_row<RP>(p, G, req, h, page, 2 * pair + 1)[RP] = cmu[1];
+    }
+}
+
+template <int RP, int VB, int G, bool COMB>
+__device__ __forceinline__ void r8_tile_mid(const R8Params& p, const i32x4_t (&qa)[2],
+                                            const R8GroupB<RP, VB>& b,
+                                            const R8Scales<RP, R8Split<G>::TPL>& sc, float qs0,
+                                            float qs1, R8Acc<RP>& acc, int2 (&row)[SC_TILE][8],
+                                            int req, int h, int page, bool valid, int pair,
+                                            int part, int n) {
+    r8_groups<RP, VB, RP / 2, RP - RP / 2>(qa, b.v, row, n);
+    int2 x[8];
+    const int own = lane_page<RP>(n);
+#pragma unroll
+    for (int k = 0; k < RP; k += 2) {
+        const int4 w = *reinterpret_cast<const int4*>(&row[own][k]);
+        x[k] = make_int2(w.x, w.y);
+        x[k + 1] = make_int2(w.z, w.w);
+    }
+    const bool co_on = COMB && valid && part == 0;
+    int32_t* co0 = co_on ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair) : nullptr;
+    int32_t* co1 = (co_on && G >= 2) ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair + 1)
+                                     : nullptr;
+#pragma unroll
+    for (int k = 0; k < RP; ++k) {
+        const float vsc = half_at(sc.vs, k);
+        acc.qt[0][k] = (float)x[k].x * qs0 * vsc;
+        acc.qt[1][k] = (float)x[k].y * qs1 * vsc;
+        if (co0) co0[k] = x[k].x;
+        if (co1) co1[k] = x[k].y;
+    }
 }
 
 // signed code k of token row t of the lane's c words
@@ -248,19 +270,6 @@ __device__ __forceinline__ float c_code(const uint32_t* cw, int t, int k) {
         const int nib = t * 2 * CROW + k;       // low nibble = even column
         return (float)(((int)(cw[nib >> 3] << (28 - 4 * (nib & 7)))) >> 28);
     }
-}
-
-template <int RP, int VB, int G, bool COMB>
-__device__ __forceinline__ void r8_tile_mid(const R8Params& p, const i32x4_t (&qa)[2],
-                                            const R8GroupB<RP, VB>& b,
-                                            const R8Scales<RP, R8Split<G>::TPL>& sc, float qs0,
-                                            float qs1, R8Acc<RP>& acc, int req, int h, int page,
-                                            bool valid, int pair, int part) {
-    const bool co_on = COMB && valid && part == 0;
-    int32_t* co0 = co_on ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair) : nullptr;
-    int32_t* co1 = (co_on && G >= 2) ? r8_comb_row<RP>(p, G, req, h, page, 2 * pair + 1)
-                                     : nullptr;
-    r8_cols<RP - RP / 2, VB, RP>(qa, b.v, sc.vs, RP / 2, qs0, qs1, acc, co0, co1);
 }
 
 template <int RP, int CBITS, int G, bool CLSE>
@@ -361,30 +370,38 @@ void r8_score_kernel(const R8Params p) {
     uint32_t qw[2][8];
     load_q_rows(p.q, p.q_st, p.q_hs, req, h, G, n, kg, true, qw);
 
-    auto page_of = [&](int tile) { return tile * SC_TILE + n; };
-    auto lane_blk = [&](int tile) -> int64_t {
+    // lane n carries page lane_page(n) of a tile (mu, scales, c rows, score); clamped
+    // pages load valid data and are never written
+    const int own = lane_page<RP>(n);
+    auto page_of = [&](int tile) { return tile * SC_TILE + own; };
+    auto lane_blk = [&](int tile) -> int {
         const int page = page_of(tile);
-        const int pc = page < nsh ? page : nsh - 1;
-        return (int64_t)p.bt[(int64_t)req * p.bt_st + pc];
+        return p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)];
     };
     const int64_t rhead = (int64_t)h * VM + 16 * kg;
     const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
     const int coff = RP * Geo::CB + 128 + part * CL - 16 * kg;
-    auto lane_rec = [&](int64_t blk) { return p.rec + blk * p.rec_sb + rhead; };
+    auto lane_rec = [&](int blk) { return p.rec + (int64_t)blk * p.rec_sb + rhead; };
+    const int8_t* vbase = p.rec + (int64_t)h * VM + 16 * (kg * RP + n % RP);
+    __shared__ R8Lds lds;
+    int2 (&row)[SC_TILE][8] = lds.x[wave][kg];
 
-    // Three load groups per tile, each refilled right after its last use: A (columns
-    // [0, r/2), mu, scales) and B (columns [r/2, r)) are consumed by the matrix-core
-    // product, C (the lane's c rows) by the token tail, so both column groups of the next
-    // tile are in flight during this tile's tail.
+    // Three load groups per tile, each refilled right after its last use: A (column
+    // groups [0, r/2), mu, scales) and B (groups [r/2, r)) are consumed by the
+    // matrix-core product, C (the lane's c rows) by the token tail, so both column groups
+    // of the next tile are in flight during this tile's tail.
     int tile = t0;
-    const int8_t* lr = lane_rec(lane_blk(tile));
+    int blk = lane_blk(tile);
+    int gbk[RP];
+    group_blocks<RP>(blk, n, gbk);
+    const int8_t* lr = lane_rec(blk);
     R8GroupA<RP, VB> ga;
     R8GroupB<RP, VB> gb;
     R8GroupC<CL> gc;
-    r8_load_a<RP, VB>(lr, ga, moff);
-    int64_t bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
+    r8_load_a<RP, VB>(vbase, p.rec_sb, gbk, lr, ga, moff);
+    int bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
     __builtin_amdgcn_sched_barrier(0);
-    r8_load_b<RP, VB>(lr, gb);
+    r8_load_b<RP, VB>(vbase, p.rec_sb, gbk, gb);
     __builtin_amdgcn_sched_barrier(0);
     r8_load_c<CL>(lr + coff, gc);
 
@@ -413,16 +430,17 @@ void r8_score_kernel(const R8Params p) {
         const int page = page_of(tile);
         const bool valid = page < nsh;
         const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part);
-        r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, pair,
-                                       part);
+        r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid,
+                                       pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
+        group_blocks<RP>(bn_next, n, gbk);
         const int8_t* ln = lane_rec(bn_next);
-        r8_load_a<RP, VB>(ln, ga, moff);
+        r8_load_a<RP, VB>(vbase, p.rec_sb, gbk, ln, ga, moff);
         bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
-        r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, req, h, page, valid, pair,
-                                     part);
+        r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, row, req, h, page, valid,
+                                     pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
-        r8_load_b<RP, VB>(ln, gb);
+        r8_load_b<RP, VB>(vbase, p.rec_sb, gbk, gb);
         r8_tile_tail<RP, CBITS, G, CLSE>(p, gc, sc, acc, req, h, page, valid, pair, part, kg, sl,
                                          qsq0, qsq1);
         __builtin_amdgcn_sched_barrier(0);
@@ -432,8 +450,10 @@ void r8_score_kernel(const R8Params p) {
     const int page = page_of(tile);
     const bool valid = page < nsh;
     const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part);
-    r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, req, h, page, valid, pair, part);
-    r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, req, h, page, valid, pair, part);
+    r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid, pair,
+                                   part, n);
+    r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, row, req, h, page, valid, pair,
+                                 part, n);
     r8_tile_tail<RP, CBITS, G, CLSE>(p, gc, sc, acc, req, h, page, valid, pair, part, kg, sl,
                                      qsq0, qsq1);
 }

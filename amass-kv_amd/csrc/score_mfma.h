@@ -1,11 +1,12 @@
 // Int8 matrix-core front end shared by the quad and r8 page-score kernels (gfx950).
 //
 // Both scores start with the same small integer product per page: the 2G int8 query
-// limbs of one kv head against the r' (or r) columns of the page's column-major code
-// matrix plus its mean codes, [2G x d] x [d x (r'+1)].  It runs on
-// v_mfma_i32_16x16x64_i8 with M = the limb rows, N = 16 pages of a tile and K = 64 d per
-// instruction; lane = 16 kg + n feeds 16 consecutive d (d = 64 t + 16 kg + s) of column
-// k of page n and receives result rows 4kg..4kg+3 of column n.
+// limbs of one kv head against the r' (or r) columns of the page's code matrix plus its
+// mean codes, [2G x d] x [d x (r'+1)].  It runs on v_mfma_i32_16x16x64_i8 with M = the
+// limb rows and K = 64 d per instruction; lane = 16 kg + n feeds 16 consecutive d
+// (d = 64 t + 16 kg + s) of column n and receives result rows 4kg..4kg+3 of column n.
+// The code columns come in groups of 16 / r' pages x r' ranks from the tiled records
+// (below); the mean codes keep one page per column.
 //
 // q limbs: qi = rint(q * inv) with inv = 16383 / max|q| and qs = max|q| / 16383 (both
 // correctly rounded divides), clamped to +-16383; hi = rint(qi / 128) clamped to +-127,
@@ -64,6 +65,57 @@ __device__ __forceinline__ void comb2(i32x4_t acc, int& x, int& y) {
 
 __device__ __forceinline__ float half_at(const uint32_t (&w)[4], int k) {
     return fp16_to_f32((uint16_t)((w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu));
+}
+
+// ---- tiled code records (quad_V / r8_Vk) ------------------------------------------------
+// Column groups: an MFMA's 16 columns are PP = 16 / r' pages x r' ranks, so a tile is r'
+// groups; lane (kg, n) of group j holds rank k = n % r' of page j PP + n / r'.
+template <int RP> constexpr int group_pages() { return SC_TILE / RP; }
+// the page whose mu, scales and score lane n carries (where the rank sums of the groups
+// land, see rank_sum): lane n holds group n % r' of its r'-lane set n / r'
+template <int RP>
+__device__ __forceinline__ int lane_page(int n) {
+    return (n % RP) * group_pages<RP>() + n / RP;
+}
+
+// V codes stream once per step: non-temporal 16-byte loads (each instruction reads PP
+// runs of 64 r' contiguous bytes; the hint measured +10 % over plain loads on this
+// pattern, and -10 % on one of 16 pages x 64 bytes)
+__device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
+}
+
+// block id of every group's page for this lane: lane m of a row carries page
+// lane_page(m); group j's page for lane n is lane_page((n / RP) RP + j)
+template <int RP>
+__device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) {
+    constexpr int PP = group_pages<RP>();
+#pragma unroll
+    for (int j = 0; j < RP; ++j) {
+        int b = __builtin_amdgcn_readlane(blk_own, j);
+#pragma unroll
+        for (int pp = 1; pp < PP; ++pp) {
+            const int c = __builtin_amdgcn_readlane(blk_own, pp * RP + j);
+            b = n / RP == pp ? c : b;
+        }
+        gb[j] = b;
+    }
+}
+
+// `base` = rec + h * VM + the lane's V offset (16 (kg r' + n % r')); group j of block b
+template <int RP, int VB, int J0, int NG>
+__device__ __forceinline__ void load_groups(const int8_t* base, int64_t rec_sb,
+                                            const int (&gb)[RP], i32x4_t* v) {
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        const int8_t* p = base + (int64_t)gb[J0 + j] * rec_sb;
+        if constexpr (VB == 8) {
+            v[2 * j] = ld16_stream(p);
+            v[2 * j + 1] = ld16_stream(p + 64 * RP);
+        } else {
+            v[j] = ld16_stream(p);
+        }
+    }
 }
 
 // Raw bf16 words of the A-row query of lane row n: row n holds limb (n & 1) of group

@@ -80,8 +80,9 @@ int amass_quad_score(const amass_quad_score_args* a, void* stream);
  * Vk_scale, r8_c, c_scale; selection/state.py:35-112) are packed per block,
  * AMASS_R8_REC_BYTES(rank, vk_bits, c_bits) bytes per kv head (VM of them first, in head
  * order, then 64 per head):
- *   head h at h*VM:         r8_Vk column-major, column k = CB bytes; int8 CB = 128 (byte j =
- *                           code[j]); int4 CB = 64 (byte j = code[j] | code[j+64] << 4),
+ *   head h at h*VM:         r8_Vk tiled as quad_V (16 bytes per (K-step t, d group kg,
+ *                           column k) at ((t*4 + kg)*r + k)*16; int8 CB = 128, int4 CB = 64
+ *                           with t folded into the nibbles),
  *                           then r8_mu (128 int8), then r8_c: 16 token rows of r*c_bits/8
  *                           bytes (int4: two columns per byte, low nibble = even column)
  *   at n_kv*VM + 64*h:      fp16 halves: Vk_scale[0..r), c_scale[0..16) at half 8,
@@ -137,7 +138,7 @@ int amass_summary_build(const amass_build_args* a, void* stream);
 /* Replaces clse_score (selection/quad_score.py:156-393, the reference's default score) and
  * its hand-CUDA clse_score_cuda (backend/_runtime.py:214-229).  Per (request, kv-head,
  * page p < n_sel_hi) and group head g, over the record of AMASS_R8_REC_BYTES layout
- * (quad_V column-major | quad_mu | quad_c rows; scale block: V_scale half 0, c_scale halves
+ * (quad_V tiled | quad_mu | quad_c rows; scale block: V_scale half 0, c_scale halves
  * 8..23 (a per-page "page" grain scale repeated 16 times), mu_scale half 24, quad_resid
  * half 25):
  *   q~[g,k] = (V_code[:,k] V_scale[k]) . q_g ; tok[g,t] = s c_scale[t] (c_code[t,:] . q~[g])

@@ -78,7 +78,7 @@ def test_state_load_reference_round_trip():
 @pytest.mark.parametrize("vk_bits,c_bits,r", [(8, 8, 8), (4, 4, 8), (8, 4, 4), (4, 8, 4)])
 def test_r8_record_positions(vk_bits, c_bits, r):
     """The packed r8 record (include/amass_hip.h, AMASS_R8_REC_BYTES): per block the n_kv
-    heads' [Vk column-major | mu | c rows], then 64-byte fp16 scale blocks with Vk_scale
+    heads' [Vk tiled | mu | c rows], then 64-byte fp16 scale blocks with Vk_scale
     at half 0, c_scale at halves 8..23, mu_scale at half 24.  Bytes are checked at their
     documented offsets in the raw buffer, so a view that drifts from the kernel's
     addressing fails here."""
@@ -107,10 +107,11 @@ def test_r8_record_positions(vk_bits, c_bits, r):
     raw = st.r8_rec[0].numpy().view(np.uint8)               # (NB, n_kv * REC)
     b, h, k, j, t = 2, 1, r - 1, 77, 13
     base = h * vm
-    if vk_bits == 8:
-        assert raw[b, base + k * cb + j].view(np.int8) == vcode[b, h, j, k]
-    else:
-        byte = int(raw[b, base + k * cb + 13])
+    if vk_bits == 8:                  # d = 77: K-step 1, d group 0, byte 13
+        off = ((1 * 4 + 0) * r + k) * 16 + 13
+        assert raw[b, base + off].view(np.int8) == vcode[b, h, j, k]
+    else:                             # d = 13 and 77 share byte 13 of (kg 0, column k)
+        byte = int(raw[b, base + k * 16 + 13])
         lo, hi = byte & 0xF, byte >> 4
         assert (lo - 16 if lo >= 8 else lo) == vcode[b, h, 13, k]
         assert (hi - 16 if hi >= 8 else hi) == vcode[b, h, 13 + 64, k]
