@@ -25,8 +25,8 @@ class _St:
     pass
 
 
-def _case(B, G, seed, partial=True):
-    case = make_case(B=B, ctx=(200, 3000), n_kv=8, G=G, heavy=0.0, table="perm", seed=seed)
+def _case(B, G, seed, partial=True, n_kv=8):
+    case = make_case(B=B, ctx=(200, 3000), n_kv=n_kv, G=G, heavy=0.0, table="perm", seed=seed)
     sl = case.seq_lens.clone()
     if partial:
         sl = sl - torch.arange(B, dtype=torch.int32) % 13   # ragged partial last pages
@@ -90,6 +90,27 @@ def test_sparse_decode(G, path, frac):
     assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
     # the empty unit (req 0, kv-head 0) writes zeros
     assert np.all(got[0, :G] == 0)
+
+
+@pytest.mark.parametrize("n_kv,G", [(1, 8), (2, 2), (4, 1), (16, 4)])
+@pytest.mark.parametrize("path", ["auto", "split", "fused"])
+def test_sparse_decode_head_layouts(n_kv, G, path):
+    """Workgroups of fewer than 8 kv heads, two head groups, GQA groups 1 and 2."""
+    announce(f"sparse decode heads n_kv={n_kv} G={G} path={path}")
+    case = _case(3, G, seed=70 + n_kv + G, n_kv=n_kv)
+    tab, cnt = _selection(case, 0.3, seed=2)
+    q, K, V, bt, sl = _np_inputs(case)
+    ref = odec.attend(q, K, V, bt, sl, tab, cnt, scale=case.scale, G=G)
+    kv = case.kv_cache.to(DEV)
+    st = _st(case, tab, cnt)
+    out = torch.full((3, n_kv * G, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    sparse_paged_decode_batched(case.q.to(DEV), kv, case.block_table.to(DEV),
+                                case.seq_lens.to(DEV), st, out, ResidentVSource(kv),
+                                scale=case.scale, path=path)
+    torch.cuda.synchronize()
+    got = npf(out)
+    assert np.isfinite(got).all()
+    assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
 
 
 @pytest.mark.parametrize("G", [4, 8])

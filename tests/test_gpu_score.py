@@ -149,3 +149,67 @@ def test_r8_comb_exact_and_scores(rank, vk_bits, c_bits, G):
     for r in range(B):
         n = int(nsh[r])
         assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3
+
+
+HEAD_CASES = [(1, 8), (2, 2), (4, 1), (16, 4)]
+
+
+@pytest.mark.parametrize("n_kv,G", HEAD_CASES)
+@pytest.mark.parametrize("rank,v_bits", [(8, 8), (2, 4)])
+def test_quad_head_layouts(n_kv, G, rank, v_bits):
+    """Workgroups of fewer than 8 kv heads (n_kv 1, 2, 4) and two head groups (n_kv 16),
+    and GQA groups 1 and 2 (spare limb rows zero): int32 contractions exact, max scores
+    within the limb oracle's 2e-5."""
+    announce(f"quad heads n_kv={n_kv} G={G} rank={rank} v_bits={v_bits}")
+    case = make_case(B=2, ctx=(300, 900), n_kv=n_kv, G=G, heavy=0.05, table="perm",
+                     seed=31 + n_kv + G)
+    st = build_quad_state(case, rank=rank, v_bits=v_bits, combine="max", budget=0.05)
+    to_device(st, DEV)
+    case_to(case, DEV)
+    B, MP = 2, st.max_pages
+    derive_page_params(st, case.seq_lens, B)
+    comb = torch.zeros(B, n_kv, MP, G, rank + 1, dtype=torch.int32, device=DEV)
+    quad_score_launch(st, 0, case.q, case.block_table, B, case.scale, comb_out=comb)
+    torch.cuda.synchronize()
+    o = _oracle_inputs(case, st)
+    nsh = npi(st.n_sel_hi)
+    ref_comb = osc.quad_comb(o["q"], o["mu"], o["V"], o["block_table"], o["n_sel_hi"], G=G,
+                             v_bits=v_bits, max_pages=MP)
+    got = npi(comb).astype(np.int64)
+    ref_l = osc.quad_score(**o, scale=case.scale, page=16, G=G, v_bits=v_bits, max_pages=MP,
+                           combine="max", q_mode="limbs")
+    sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n]), f"comb mismatch req {r}"
+        assert rel_close(sc[r, :, :n], ref_l[r, :, :n], 1) <= 2e-5
+
+
+@pytest.mark.parametrize("n_kv,G", HEAD_CASES)
+def test_r8_head_layouts(n_kv, G):
+    """The r8 kernel over the same head layouts: contractions exact, scores within 1e-3 of
+    the fp64 oracle."""
+    announce(f"r8 heads n_kv={n_kv} G={G}")
+    case = make_case(B=2, ctx=(300, 900), n_kv=n_kv, G=G, seed=41 + n_kv + G)
+    st = build_r8_state(case, rank=8, vk_bits=8, c_bits=8)
+    to_device(st, DEV)
+    case_to(case, DEV)
+    B, MP = 2, st.max_pages
+    derive_page_params(st, case.seq_lens, B)
+    comb = torch.zeros(B, n_kv, MP, G, 9, dtype=torch.int32, device=DEV)
+    r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
+    torch.cuda.synchronize()
+    mu, mus, _, Vks, c, cs, _ = st.layer_state(0)
+    Vk = st.reference_Vk(0)
+    nsh = npi(st.n_sel_hi)
+    ref_comb = osc.r8_comb(npf(case.q), npi(mu), npi(Vk), npi(case.block_table), nsh, G=G,
+                           vk_bits=8, max_pages=MP)
+    ref = osc.r8_score(npf(case.q), npi(mu), npf(mus), npi(Vk), npf(Vks), npi(c), npf(cs),
+                       npi(case.block_table), npi(case.seq_lens), nsh, scale=case.scale,
+                       page=16, G=G, vk_bits=8, c_bits=8, max_pages=MP)
+    got = npi(comb).astype(np.int64)
+    sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
+        assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3
