@@ -149,3 +149,36 @@ def test_select_pages_clse_end_to_end():
     ref = odec.attend(inp["q"], npf(case.kv_cache[:, 0]), npf(case.kv_cache[:, 1]),
                       inp["block_table"], inp["seq_lens"], tab, cnt, scale=case.scale, G=4)
     assert np.allclose(npf(out), ref, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("n_kv,G", [(1, 8), (2, 2), (4, 1), (16, 4)])
+@pytest.mark.parametrize("rank,v_bits,c_bits,c_grain", [(2, 4, 4, "token"), (8, 8, 8, "page")])
+def test_clse_head_layouts(n_kv, G, rank, v_bits, c_bits, c_grain):
+    """Fewer than 8 kv heads per workgroup, two head groups, GQA groups 1 and 2, with the
+    summaries written by the HIP builder (device K): contractions exact, per-head scores
+    within 1e-3 of the oracle."""
+    announce(f"CLSE heads n_kv={n_kv} G={G} r'={rank}")
+    B = 2
+    case = make_case(B=B, ctx=(300, 900), n_kv=n_kv, G=G, heavy=0.05, table="perm",
+                     seed=90 + n_kv + G + rank, device=DEV)
+    st = build_quad_state(case, rank=rank, v_bits=v_bits, combine="nrm", coords="lse",
+                          c_bits=c_bits, c_grain=c_grain, budget=0.05)
+    derive_page_params(st, case.seq_lens, B)
+    MP = st.max_pages
+    comb = torch.zeros(B, n_kv, MP, G, rank + 1, dtype=torch.int32, device=DEV)
+    clse_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
+    torch.cuda.synchronize()
+    inp = _oracle_inputs(case, st)
+    nsh = inp["n_sel_hi"]
+    ref_comb = osc.quad_comb(inp["q"], inp["mu"], inp["V"], inp["block_table"], nsh, G=G,
+                             v_bits=v_bits, max_pages=MP)
+    ref = osc.clse_score(inp["q"], inp["mu"], inp["mu_scale"], inp["V"], inp["V_scale"],
+                         inp["c"], inp["c_scale"], inp["resid"], inp["block_table"],
+                         inp["seq_lens"], nsh, scale=case.scale, page=16, G=G, v_bits=v_bits,
+                         c_bits=c_bits, max_pages=MP, combine="nrm")
+    got_comb = npi(comb).astype(np.int64)
+    got = npf(st.score_h)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(got_comb[r, :, :n], ref_comb[r, :, :n])
+        assert rel_close(got[r, :, :, :n], ref[r, :, :, :n], 1) <= 1e-3
