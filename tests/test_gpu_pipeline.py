@@ -98,3 +98,55 @@ def test_coverage_batch_and_graph_replay():
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
         assert torch.equal(st.page_table, eager_tab), f"replay {i}"
+
+
+def _replay_matches_eager(step, outs):
+    """Capture `step` in one HIP graph, replay it four times (the outputs poisoned before
+    each replay, eager work in between) and compare every replay with the eager run."""
+    step()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for i in range(4):
+        for o in outs:
+            o.fill_(-5 if o.dtype == torch.int32 else float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {i}"
+
+
+@pytest.mark.parametrize("score", ["r8", "clse"])
+def test_r8_and_clse_steps_graph_replay(score):
+    """The r8 (top-b) and CLSE (coverage) steps -- score, select, decode -- replayed from
+    one HIP graph equal the eager step bit for bit."""
+    announce(f"{score} step graph replay")
+    from amass.bench.synth import build_r8_state
+    from amass.selection import select_pages_clse, select_pages_r8
+    case = make_case(B=3, ctx=(1500, 4000), n_kv=8, G=4, heavy=0.05, seed=12)
+    if score == "r8":
+        st = build_r8_state(case, rank=8, vk_bits=8, c_bits=8, budget=0.05)
+    else:
+        st = build_quad_state(case, rank=2, v_bits=4, combine="nrm", coverage=0.95,
+                              coords="lse", c_bits=4, c_grain="token")
+    to_device(st, DEV)
+    case_to(case, DEV)
+    B = 3
+    derive_page_params(st, case.seq_lens, B)
+    out = torch.zeros(B, 32, 128, dtype=torch.bfloat16, device=DEV)
+    sel = select_pages_r8 if score == "r8" else select_pages_clse
+
+    def step():
+        sel(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, derive=False)
+        sparse_paged_decode_batched(case.q, case.kv_cache, case.block_table, case.seq_lens,
+                                    st, out, ResidentVSource(case.kv_cache), scale=case.scale)
+
+    _replay_matches_eager(step, [out, st.page_table, st.page_cnt])
