@@ -206,3 +206,54 @@ def test_tiered_decode_reads_written_path_v():
         outs.append(out)
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def test_write_path_graph_replay_matches_eager():
+    """Decode steps (every request appends one token) through begin_step + write_kv:
+    one tier runs them eagerly, a second replays one captured step from static input
+    buffers refreshed between replays; after every step the staging map, flush state,
+    token slots, staged pool, pinned pool and pool validity agree bit for bit (the
+    lifecycle crosses a page boundary, so flushes replay too)."""
+    announce("write path graph replay vs eager")
+    from amass.tier.tier import Tier
+    R, n_kv, d, page, NB, MP = 3, 2, 128, 16, 48, 8
+    gen = torch.Generator().manual_seed(17)
+    bt = torch.randperm(NB, generator=gen)[:R * MP].view(R, MP).to(torch.int32).to(DEV)
+    mk = lambda: Tier(num_layers=1, num_blocks=NB, n_kv=n_kv, page=page, d=d,  # noqa: E731
+                      hot_slots=4, max_reqs=R, max_pages=MP, device=DEV, max_tokens=R,
+                      v_blocks=2 * R + 4)
+    ta, tb = mk(), mk()
+    sl0 = torch.tensor([20, 9, 31], dtype=torch.int32)
+    qsl = torch.arange(R + 1, dtype=torch.int32, device=DEV)
+    sl_buf = torch.zeros(R, dtype=torch.int32, device=DEV)
+    v_buf = torch.zeros(R, n_kv, d, dtype=torch.bfloat16, device=DEV)
+
+    def step(t):
+        t.begin_step(bt, sl_buf, qsl, R)
+        t.write_kv(0, v_buf, R)
+
+    sl_buf.copy_(sl0 + 1)
+    step(tb)                                    # warm-up outside capture, mirrored on ta
+    step(ta)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step(tb)
+    torch.cuda.synchronize()
+    for k in range(2, 20):
+        sl_buf.copy_(sl0 + k)
+        v_buf.copy_(torch.randn(R, n_kv, d, generator=gen).to(torch.bfloat16))
+        step(ta)
+        g.replay()
+        torch.cuda.synchronize()
+        sa, sb = ta.staging, tb.staging
+        for name in ("vbo", "v_flushed", "v_free_top", "flush_cnt", "overflow", "v_pool"):
+            assert torch.equal(getattr(sa, name), getattr(sb, name)), (k, name)
+        top = int(sa.v_free_top.item())
+        assert torch.equal(sa.v_free_stack[:top], sb.v_free_stack[:top]), k
+        assert torch.equal(sa.v_slot_mapping[:R], sb.v_slot_mapping[:R]), k
+        assert torch.equal(ta.pool.host, tb.pool.host), k
+        assert torch.equal(ta.residency.pool_valid, tb.residency.pool_valid), k
+    assert int(ta.residency.pool_valid.sum().item()) > 0     # some page was flushed
