@@ -510,7 +510,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path has no "
-                                   "cross-GPU component (see DESIGN.md, sharding note); "
+                                   "cross-GPU component (each (request, kv-head) unit is "
+                                   "scored, selected and attended on one GPU); "
                                    "run with --gpus 1"}))
         sys.exit(2)
 
