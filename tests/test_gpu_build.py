@@ -14,7 +14,10 @@ token's scale is the max over all its coordinates, so an unstable column can mov
 separated are compared; the quad / r8 scores computed by the oracle from the HIP-built
 and from the oracle-built summaries within 2e-2 * max(|s|, 1) (with a scale shared by all
 columns, pages whose keys span fewer than r directions are left out: there the reference
-formula divides rounding noise by sqrt(1e-10) in any precision); a constant page gives
+formula divides rounding noise by sqrt(1e-10) in any precision; with any grain, pages
+whose r-th and (r+1)-th eigenvalues are within 1e-3 of the largest are left out: their
+top-r subspace is not fixed at fp32 resolution; both exclusions stay under 5 % of the
+page-heads); a constant page gives
 zero V codes; the graph-captured tail rebuild restores corrupted records bit for bit.
 """
 import numpy as np
@@ -40,8 +43,11 @@ def _case(seed):
     K = case.kv_cache
     b0, b1 = int(case.block_table[0, 1]), int(case.block_table[1, 2])
     K[b0, 0] = K[b0, 0, 3]                          # page 1 of request 0: constant keys
-    x = torch.randn(16, 1, 1, device=DEV)           # page 2 of request 1: rank 1 per head
-    K[b1, 0] = (K[b1, 0, :1] + x * torch.randn(1, 8, 128, device=DEV)).to(torch.bfloat16)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(seed + 104729)                  # independent of the global RNG's state
+    x = torch.randn(16, 1, 1, device=DEV, generator=gen)   # page 2 of request 1: rank 1
+    K[b1, 0] = (K[b1, 0, :1] + x * torch.randn(1, 8, 128, device=DEV, generator=gen)
+                ).to(torch.bfloat16)
     return case, b0
 
 
@@ -81,6 +87,15 @@ def _deficient(S2_all, rank):
     is set by noise on both sides."""
     ev = np.sort(S2_all, axis=-1)
     return ev[..., -rank] <= 1e-6 * ev[..., -1]
+
+
+def _ill_posed(S2_all, rank, gap=1e-3):
+    """(N, n_kv) pages whose r-th and (r+1)-th eigenvalues lie within `gap` of the largest:
+    the top-r subspace is not fixed by the data to fp32 resolution (the fp32 Jacobi moves
+    eigenvalues by ~1e-6 of the largest), so any fp32 builder may pick another basis of
+    the near-degenerate pair and the score built from it differs from the float64 one."""
+    ev = np.sort(S2_all, axis=-1)
+    return (ev[..., -rank] - ev[..., -rank - 1]) <= gap * np.maximum(ev[..., -1], 1e-30)
 
 
 def _score_mask(case, blocks, bad, nsh):
@@ -154,7 +169,10 @@ def test_quad_summary_build(rank, v_bits, v_grain):
                            npi(st.reference_V(0))[blocks], vs, sig2, btl, nsh, **kw)
     s_ref = osc.quad_score(q, ref["mu"], ref["mu_scale"], ref["V"], ref["V_scale"],
                            ref["sig2"], btl, nsh, **kw)
-    bad = _deficient(S2_all, rank) if v_grain == "tensor" else np.zeros(S2_all.shape[:2], bool)
+    bad = _ill_posed(S2_all, rank)
+    if v_grain == "tensor":
+        bad |= _deficient(S2_all, rank)
+    assert bad.mean() < 0.05, bad.mean()
     mask = _score_mask(case, blocks, bad, nsh)
     ok = np.abs(s_hip - s_ref) <= 2e-2 * np.maximum(np.abs(s_ref), 1)
     assert np.all(ok | ~mask), float(np.nanmax(np.where(mask, np.abs(s_hip - s_ref), 0)))
@@ -211,7 +229,10 @@ def test_r8_summary_build(rank, vk_bits, c_bits, vk_grain, c_grain):
     s_ref = osc.r8_score(q, ref["mu"], ref["mu_scale"], ref["Vk"], ref["Vk_scale"], ref["c"],
                          ref["c_scale"], btl, sl, nsh, **kw)
     S2_all = np.linalg.eigvalsh(dc @ dc.swapaxes(-1, -2))
-    bad = _deficient(S2_all, rank) if vk_grain == "tensor" else np.zeros(S2_all.shape[:2], bool)
+    bad = _ill_posed(S2_all, rank)
+    if vk_grain == "tensor":
+        bad |= _deficient(S2_all, rank)
+    assert bad.mean() < 0.05, bad.mean()
     mask = _score_mask(case, blocks, bad, nsh)
     ok = np.abs(s_hip - s_ref) <= 2e-2 * np.maximum(np.abs(s_ref), 1)
     assert np.all(ok | ~mask), float(np.nanmax(np.where(mask, np.abs(s_hip - s_ref), 0)))
