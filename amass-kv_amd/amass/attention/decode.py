@@ -89,13 +89,38 @@ def _decode_args(q, k, vsource, block_table, seq_lens, st, out, scale, n_req, *,
         raise ValueError("q / K / out need unit stride on the head dim")
     _, page, n_kv, d = k.shape
     v, svb, svt, svh = vsource.args()
-    G = q.shape[1] // n_kv
+    H = q.shape[1]
+    if H % n_kv:
+        raise ValueError(f"{H} query heads are not a multiple of {n_kv} kv heads")
+    G = H // n_kv
+    # the kernels index the state's partials, page tables and counts with these values
+    if n_kv != st.n_kv or G != st.G:
+        raise ValueError(f"cache / query geometry (n_kv {n_kv}, G {G}) differs from the "
+                         f"state's (n_kv {st.n_kv}, G {st.G})")
+    if n_req > st.max_reqs:
+        raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
+    if q.shape[0] < n_req or out.shape[0] < n_req or tuple(out.shape[1:]) != (H, d) \
+            or block_table.shape[0] < n_req:
+        raise ValueError("q, out and block_table need a row per request (out (T, H, d))")
     if not dense:
         table = st.page_table if table is None else table
         cnt = st.page_cnt if cnt is None else cnt
-    if path != "fused" and getattr(st, "m_part", None) is None:
-        raise ValueError("split-K partials missing: call ensure_stage_b_buffers(st, device) "
-                         "once before decoding (outside any graph capture)")
+        if table.dtype != torch.int32 or cnt.dtype != torch.int32 or \
+                table.shape[0] < n_req or table.shape[1] != n_kv or table.stride(2) != 1 or \
+                cnt.shape[0] < n_req or cnt.shape[1] != n_kv or cnt.stride(1) != 1:
+            raise ValueError("page_table (R, n_kv, MP) / page_cnt (R, n_kv) int32 expected")
+    if path != "fused":
+        m = getattr(st, "m_part", None)
+        if m is None:
+            raise ValueError("split-K partials missing: call ensure_stage_b_buffers(st, "
+                             "device) once before decoding (outside any graph capture)")
+        split = getattr(st, "split", SPLIT)
+        want = (st.max_reqs, n_kv, split, G)
+        if tuple(m.shape) != want or tuple(st.l_part.shape) != want or \
+                tuple(st.acc_part.shape) != want + (d,) or not (
+                    m.is_contiguous() and st.l_part.is_contiguous()
+                    and st.acc_part.is_contiguous()):
+            raise ValueError(f"split-K partials must be contiguous {want}[+(d,)] fp32")
     tf = vsource.tier_fields()
     return DecodeArgs(
         q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),

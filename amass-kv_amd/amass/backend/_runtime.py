@@ -33,17 +33,42 @@ def get_config() -> Optional[AmassConfig]:
     return _config
 
 
+# What the kernels of libamass_hip.so accept (their entry points return a geometry or
+# unsupported status for anything else, so a layer outside these limits must keep the
+# stock attention instead of failing inside forward).
+SCORE_RANKS = {"quad": (2, 4, 8), "clse": (2, 4, 8), "r8": (4, 8)}
+SCORE_GROUPS = {"quad": tuple(range(1, 9)), "clse": (1, 2, 4, 8), "r8": (1, 2, 4, 8)}
+MAX_HEADS_PER_GROUP = 8   # kv heads of one score workgroup: n_kv <= 8 or a multiple of 8
+MAX_SELECT_PAGES = 16384  # pages per request the selection kernel holds in LDS
+
+
 def unsupported_reason(cfg: Optional[AmassConfig], *, head_size: int, block_size: int,
-                       G: int) -> Optional[str]:
-    """Why this build's decode path does not serve a layer (None = it does)."""
+                       G: int, n_kv: Optional[int] = None,
+                       max_pages: Optional[int] = None) -> Optional[str]:
+    """Why this build's decode path does not serve a layer (None = it does): the limits
+    the score, selection and decode kernels check (head size, page size, the GQA group
+    and rank sets per score, the kv-head grouping, the pages one selection holds)."""
     if cfg is None:
         return "no AmassConfig registered"
     if cfg.offload_k:
         return "variant 'mem-kv': K offload is not part of this build"
     if head_size != HEAD_DIM or block_size != PAGE:
         return f"head_size {head_size} / block_size {block_size} (built for 128 / 16)"
-    if not 1 <= G <= 8:
-        return f"GQA group {G} (built for 1..8)"
+    score = cfg.score
+    groups = SCORE_GROUPS.get(score)
+    if groups is None:
+        return f"score {score!r} is not built"
+    if G not in groups:
+        return f"GQA group {G} with score {score!r} (built for {groups})"
+    rank = cfg.r8_rank if score == "r8" else cfg.quad_rank
+    if rank not in SCORE_RANKS[score]:
+        return f"rank {rank} with score {score!r} (built for {SCORE_RANKS[score]})"
+    if n_kv is not None and (n_kv < 1 or (n_kv > MAX_HEADS_PER_GROUP
+                                          and n_kv % MAX_HEADS_PER_GROUP)):
+        return f"{n_kv} kv heads (built for <= 8 or a multiple of 8)"
+    if max_pages is not None and max_pages > MAX_SELECT_PAGES:
+        return (f"{max_pages} pages per sequence (the selection holds at most "
+                f"{MAX_SELECT_PAGES}, i.e. {MAX_SELECT_PAGES * PAGE} tokens)")
     return None
 
 

@@ -71,6 +71,12 @@ def _kv_tensor(mod):
     return kvc if isinstance(kvc, torch.Tensor) and kvc.numel() > 0 else None
 
 
+def _max_pages(vllm_config, block: int):
+    """Pages of the longest sequence the engine admits (None if it does not say)."""
+    mlen = getattr(getattr(vllm_config, "model_config", None), "max_model_len", None)
+    return -(-int(mlen) // block) if isinstance(mlen, int) and mlen > 0 else None
+
+
 def _geometry(vllm_config, kv_cache_spec):
     """(n_kv, G, head_size, block_size) of the layers this builder serves."""
     n_kv = int(kv_cache_spec.num_kv_heads)
@@ -93,8 +99,9 @@ class AmassMetadataBuilderMixin:
         cfg = _runtime.get_config()
         n_kv, G, head, block = _geometry(vllm_config, kv_cache_spec)
         if (cfg is not None and cfg.variant == "fast" and not cfg.force_eager
-                and _runtime.unsupported_reason(cfg, head_size=head, block_size=block,
-                                                G=G) is None):
+                and _runtime.unsupported_reason(
+                    cfg, head_size=head, block_size=block, G=G, n_kv=n_kv,
+                    max_pages=_max_pages(vllm_config, block)) is None):
             return cg.UNIFORM_SINGLE_TOKEN_DECODE
         return cg.NEVER
 
@@ -115,7 +122,9 @@ class AmassMetadataBuilderMixin:
         self._amass_built_once = False
         self._amass_capturing = False
         why = _runtime.unsupported_reason(self._amass_cfg, head_size=head,
-                                          block_size=block, G=self._amass_G)
+                                          block_size=block, G=self._amass_G,
+                                          n_kv=self._amass_n_kv,
+                                          max_pages=_max_pages(vllm_config, block))
         self._amass_enabled = why is None
         if why is not None:
             _notice(f"stock attention kept: {why}")

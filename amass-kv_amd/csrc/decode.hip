@@ -621,6 +621,14 @@ static int decode_common(const amass_decode_args* ain, int force_dense, int v_sr
     if (a.path < 0 || a.path > 2) return AMASS_ERR_GEOMETRY;
     if (a.path != 2 && (a.split < 1 || a.pps_min < 1)) return AMASS_ERR_GEOMETRY;
     if (a.path == 2) a.pps_min = a.pps_min < 1 ? 1 : a.pps_min;
+    // K and V rows are read as 16-byte (8-element) loads, q as 8-byte loads, out written
+    // at least 4 bytes at a time
+    const auto off = [](const void* p, uintptr_t align) { return ((uintptr_t)p & (align - 1)) != 0; };
+    if (off(a.k, 16) || ((a.k_sb | a.k_st | a.k_sh) & 7)) return AMASS_ERR_GEOMETRY;
+    if (a.v && (off(a.v, 16) || ((a.v_sb | a.v_st | a.v_sh) & 7))) return AMASS_ERR_GEOMETRY;
+    if (a.v_src == 1 && (off(a.hot, 16) || off(a.pool, 16))) return AMASS_ERR_GEOMETRY;
+    if (off(a.q, 8) || ((a.q_st | a.q_hs) & 3)) return AMASS_ERR_GEOMETRY;
+    if (off(a.out, 4) || ((a.o_st | a.o_hs) & 1)) return AMASS_ERR_GEOMETRY;
     if (a.n_req == 0) return AMASS_OK;
     if (a.dense) return launch_decode<0, true>(a, a.path, s);
     if (a.v_src == 1) return launch_decode<1, false>(a, a.path, s);

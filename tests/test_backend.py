@@ -83,6 +83,42 @@ def test_unserved_geometry_keeps_stock(vllm):
         vc, vllm.kv_spec(head_size=64)).name == "NEVER"
 
 
+@pytest.mark.parametrize("cfg,n_q,n_kv,max_len", [
+    ({"score": "clse"}, 56, 8, 4096),          # G = 7: the r8/CLSE kernels take 1, 2, 4, 8
+    ({"score": "r8"}, 24, 8, 4096),            # G = 3
+    ({"score": "quad"}, 96, 12, 4096),         # 12 kv heads: <= 8 or a multiple of 8
+    ({"score": "r8", "r8_rank": 6}, 32, 8, 4096),
+    ({"score": "quad", "quad_rank": 6}, 32, 8, 4096),
+    ({}, 32, 8, 16384 * 16 + 1),               # more pages than one selection holds
+])
+def test_kernel_limits_keep_stock(vllm, cfg, n_q, n_kv, max_len):
+    """Layers outside what the kernels accept are refused up front: no graph support,
+    the builder attaches no state, so the impl calls the stock attention."""
+    _, be = _backend(vllm, **cfg)
+    kv = {"l0": torch.zeros(40, 2, 16, n_kv, 128, dtype=torch.bfloat16)}
+    vc = vllm.vllm_config(num_gpu_blocks=40, layers=kv, max_model_len=max_len, n_q=n_q)
+    bld = be.get_builder_cls()
+    assert bld.get_cudagraph_support(vc, vllm.kv_spec(n_kv=n_kv)).name == "NEVER"
+    b = bld(vllm.kv_spec(n_kv=n_kv), list(kv), vc, "cpu")
+    assert not b._amass_enabled
+    md = b.build(0, _cam(torch.tensor([33, 40]), torch.arange(8, dtype=torch.int32).view(2, 4)))
+    assert getattr(md, "amass", None) is None
+    impl = _impl(be, n_q=n_q, n_kv=n_kv)
+    out = torch.zeros(2, n_q * 128)
+    impl.forward(None, torch.zeros(2, n_q, 128), None, None, kv["l0"], md, output=out)
+    assert impl.calls == ["stock"]
+
+
+def test_kernel_limits_accept_the_served_shapes():
+    base = AmassConfig(**FAST)
+    for score, G, rank in (("quad", 7, 8), ("clse", 8, 2), ("r8", 1, 4)):
+        cfg = AmassConfig(**dict(FAST, score=score, quad_rank=rank if score != "r8" else 8,
+                                 r8_rank=rank if score == "r8" else 8))
+        assert _runtime.unsupported_reason(cfg, head_size=128, block_size=16, G=G, n_kv=16,
+                                           max_pages=16384) is None, (score, G, rank)
+    assert _runtime.unsupported_reason(base, head_size=128, block_size=16, G=4) is None
+
+
 def _impl(be, n_q=32, n_kv=8):
     return be.get_impl_cls()(n_q, 128, 0.088, n_kv)
 

@@ -1,6 +1,14 @@
 """Parity at the BASELINE configurations' real shapes (full context lengths and head
-geometry; batch reduced so the CPU oracle finishes in seconds).
+geometry; batch reduced so the CPU oracle finishes in seconds, except config 1).
 
+config 1: the headline shape at its full batch -- B = 32, 16384-token contexts (1024
+          pages), G = 4, quad r'=8 int8, nrm, coverage 0.95, permuted pool; the GPU runs
+          all 32 requests (so every score workgroup walks several tiles), the oracle
+          checks the int32 sums and the scores of four requests over their own blocks,
+          the page tables of all 32 on the GPU's scores, and the decode of four requests;
+          properties at the full batch: graph replay == eager, every unit's kept mass
+          reaches its need, page_cnt >= b + sink + window.  Also the CLSE score with the
+          reference's defaults (r'=2, int4 V and coordinates) at the same shape;
 config 2: r8 score, 6 ragged sequences spanning 2048..65536 tokens, fixed 5 % budget,
           random pool block tables -> r8 int32 sums exact, scores 1e-3, page sets exact,
           decode 2e-2 / 1e-2;
@@ -21,8 +29,9 @@ import oracle.score as osc
 import oracle.select as osel
 import oracle.tier as otier
 from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
-from amass.bench.synth import build_quad_state, build_r8_state, make_case
-from amass.selection import derive_page_params, select_pages_quad
+from amass.bench.synth import build_quad_state, build_r8_state, config_case, make_case
+from amass.selection import derive_page_params, select_pages_clse, select_pages_quad
+from amass.selection.quad_score import clse_score, quad_score_launch
 from amass.tier import Tier, mem_dynamic_decode
 from helpers import announce, npf, npi, rel_close
 
@@ -52,6 +61,161 @@ def _decode_check(case, st, rows, atol=2e-2, rtol=1e-2):
                            tab[r:r + 1], cnt[r:r + 1], scale=case.scale, G=case.G)
         assert np.allclose(got[r:r + 1], want, atol=atol, rtol=rtol), \
             f"req {r}: {float(np.abs(got[r:r + 1] - want).max())}"
+
+
+def _row_blocks(case, r, n):
+    """Oracle inputs restricted to request r's own first n blocks (the oracle then works on
+    a (n, ...) slab and an identity block table)."""
+    blk = npi(case.block_table[r, :n]).astype(np.int64)
+    return torch.from_numpy(blk).to(DEV), np.arange(n, dtype=np.int32)[None]
+
+
+def _graph_replay_equals_eager(step, outs, replays=3):
+    """Capture `step` in one HIP graph; every replay (outputs poisoned before it, eager
+    work and a synchronisation in between) must equal the eager result bit for bit."""
+    step()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for i in range(replays):
+        for o in outs:
+            o.view(torch.uint8).fill_(0xA5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o.view(torch.uint8), e.view(torch.uint8)), f"replay {i}"
+
+
+def _coverage_properties(st, sink=1, window=1, coverage=0.95):
+    """Every unit keeps its sinks and window, at least one selectable page, and selectable
+    pages whose 2^-32 fixed-point masses (score_kind 1: the nrm scores are masses) reach
+    ceil(coverage * total) - sink mass; dropping the lightest kept page falls short."""
+    sc, tab, cnt = npf(st.score), npi(st.page_table), npi(st.page_cnt)
+    nsh = npi(st.n_sel_hi)
+    for r in range(sc.shape[0]):
+        n = int(nsh[r])
+        for kh in range(sc.shape[1]):
+            c = int(cnt[r, kh])
+            assert c >= 1 + sink + window, (r, kh, c)
+            pages = tab[r, kh, :c]
+            assert np.all(np.diff(pages) > 0) and np.all(tab[r, kh, c:] == -1)
+            w = osel.mass_q(sc[r, kh, :n], 0.0, 1).astype(np.int64)
+            need = int(np.ceil(coverage * float(int(w.sum())))) - int(w[:sink].sum())
+            chosen = pages[(pages >= sink) & (pages < n)]
+            kept = int(w[chosen].sum())
+            assert kept >= need, (r, kh, kept, need)
+            if chosen.size > 1 and need > 0:
+                assert kept - int(w[chosen].min()) < need, (r, kh)
+
+
+@pytest.mark.parametrize("boost", ["sigma", "keynorm"])
+def test_config1_b32_16k_coverage(boost):
+    """The headline configuration at its full batch (quad_score.py:35-107, nrm
+    :276-315, the per-(request, kv-head) nucleus of _selection_bridge.py:117-133,
+    decode.py:128-241)."""
+    announce(f"config 1: B=32, 16384 tokens, quad r'=8 int8 nrm, coverage 0.95, boost={boost}")
+    case = config_case(1, seed=1, device=DEV, boost=boost)
+    B, MP, G = 32, case.max_pages, 4
+    assert case.q.shape[0] == B and MP == 1024
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
+    derive_page_params(st, case.seq_lens, B)
+    nsh = npi(st.n_sel_hi)
+    assert np.all(nsh == 1023)
+    # the exact int32 contractions over the multi-tile walk (the comb_out instance walks
+    # the same tiles), then the production step overwrites score_h
+    comb = torch.zeros(B, 8, MP, G, 9, dtype=torch.int32, device=DEV)
+    quad_score_launch(st, 0, case.q, case.block_table, B, case.scale, comb_out=comb)
+    out = torch.zeros(B, 32, 128, dtype=torch.bfloat16, device=DEV)
+    vsrc = ResidentVSource(case.kv_cache)
+
+    def step():
+        select_pages_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                          derive=False)
+        sparse_paged_decode_batched(case.q, case.kv_cache, case.block_table, case.seq_lens,
+                                    st, out, vsrc, scale=case.scale)
+
+    step()
+    torch.cuda.synchronize()
+    mu, mus, _, Vs, sg, _ = st.layer_state(0)
+    V = st.reference_V(0)
+    sh = npf(st.score_h)
+    rows = [0, 9, 22, 31]
+    for r in rows:
+        idx, bt = _row_blocks(case, r, 1023)
+        o = dict(q=npf(case.q[r:r + 1]), mu=npi(mu[idx]), mu_scale=npf(mus[idx]),
+                 V=npi(V[idx]), V_scale=npf(Vs[idx]), sig2=npf(sg[idx]), block_table=bt,
+                 n_sel_hi=np.array([1023]))
+        ref_comb = osc.quad_comb(o["q"], o["mu"], o["V"], bt, o["n_sel_hi"], G=G, v_bits=8,
+                                 max_pages=1023)
+        assert np.array_equal(npi(comb[r:r + 1, :, :1023]).astype(np.int64), ref_comb), r
+        kw = dict(scale=case.scale, page=16, G=G, v_bits=8, max_pages=1023, combine="nrm")
+        ref_f = osc.quad_score(**o, **kw, q_mode="float")
+        ref_l = osc.quad_score(**o, **kw, q_mode="limbs")
+        assert rel_close(sh[r, :, :, :1023], ref_f[0], 1) <= 1e-3, r
+        assert rel_close(sh[r, :, :, :1023], ref_l[0], 1) <= 2e-5, r
+    ref_n = osc.nrm_combine(sh.astype(np.float64), nsh)
+    assert rel_close(npf(st.score)[:, :, :1023], ref_n[:, :, :1023], 1) <= 1e-5
+    # page tables of all 32 requests from the GPU's own scores
+    tab, cnt, _ = osel.select(npf(st.score), npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                              max_pages=MP, mode=1, coverage=0.95, score_kind=1)
+    assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)
+    _coverage_properties(st)
+    frac = float(cnt.sum()) / (B * 8 * MP)
+    announce(f"config 1 ({boost}): selected fraction {frac:.4f}")
+    if boost == "keynorm":
+        assert frac < 0.2
+    _decode_check(case, st, rows)
+    score_eager = st.score[:, :, :1023].clone()
+    _graph_replay_equals_eager(step, [out, st.page_table, st.page_cnt])
+    assert torch.equal(st.score[:, :, :1023], score_eager)
+
+
+@pytest.mark.parametrize("boost", ["sigma", "keynorm"])
+def test_config1_clse_reference_defaults(boost):
+    """The CLSE score with the reference's defaults (cfg:69-82: r'=2, int4 V, int4
+    per-token coordinates, nrm) at the config-1 shape: the CLSE tile walk
+    (quad_score.py:156-393) over 32 x 1023 pages."""
+    announce(f"config 1 shape, CLSE r'=2 int4/int4 nrm coverage 0.95, boost={boost}")
+    case = config_case(1, seed=1, device=DEV, boost=boost)
+    B, MP, G = 32, case.max_pages, 4
+    st = build_quad_state(case, rank=2, v_bits=4, combine="nrm", coverage=0.95,
+                          coords="lse", c_bits=4, c_grain="token")
+    derive_page_params(st, case.seq_lens, B)
+    comb = torch.zeros(B, 8, MP, G, 3, dtype=torch.int32, device=DEV)
+    clse_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
+    select_pages_clse(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                      derive=False)
+    torch.cuda.synchronize()
+    nsh = npi(st.n_sel_hi)
+    mu, mus, _, Vs, _sg, _ = st.layer_state(0)
+    V, c, cs, res = st.reference_V(0), st.quad_c[0], st.c_scale[0], st.quad_resid[0]
+    sh = npf(st.score_h)
+    rows = [0, 13, 31]
+    for r in rows:
+        idx, bt = _row_blocks(case, r, 1023)
+        q = npf(case.q[r:r + 1])
+        ref_comb = osc.quad_comb(q, npi(mu[idx]), npi(V[idx]), bt, np.array([1023]), G=G,
+                                 v_bits=4, max_pages=1023)
+        assert np.array_equal(npi(comb[r:r + 1, :, :1023]).astype(np.int64), ref_comb), r
+        ref = osc.clse_score(q, npi(mu[idx]), npf(mus[idx]), npi(V[idx]), npf(Vs[idx]),
+                             npi(c[idx]), npf(cs[idx]), npf(res[idx]), bt,
+                             npi(case.seq_lens[r:r + 1]), np.array([1023]), scale=case.scale,
+                             page=16, G=G, v_bits=4, c_bits=4, max_pages=1023,
+                             combine="nrm")
+        assert rel_close(sh[r, :, :, :1023], ref[0], 1) <= 1e-3, r
+    tab, cnt, _ = osel.select(npf(st.score), npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                              max_pages=MP, mode=1, coverage=0.95, score_kind=1)
+    assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)
+    _coverage_properties(st)
+    _decode_check(case, st, [0, 31])
 
 
 def test_config2_r8_ragged():

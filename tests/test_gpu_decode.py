@@ -223,3 +223,38 @@ def test_split_merge_repeatable_across_launches_and_graph_replays(dense):
         assert torch.equal(out.view(torch.int16), first.view(torch.int16))
         step()                                   # eager launch between replays
         torch.cuda.synchronize()
+
+
+def test_decode_rejects_inconsistent_geometry():
+    """The host side refuses a query / cache / state mismatch before any launch (the
+    kernels index the state's partials, tables and counts with these values), and the
+    library refuses K or V views that are not 16-byte aligned."""
+    announce("decode geometry checks")
+    from amass._hip import AmassError
+    case = _case(3, 4, seed=5, partial=False)
+    tab, cnt = _selection(case, 0.3, seed=2)
+    kv = case.kv_cache.to(DEV)
+    st = _st(case, tab, cnt)
+    q, bt, sl = case.q.to(DEV), case.block_table.to(DEV), case.seq_lens.to(DEV)
+    out = torch.zeros((3, 32, 128), dtype=torch.bfloat16, device=DEV)
+    run = lambda q_, kv_, out_, st_: sparse_paged_decode_batched(  # noqa: E731
+        q_, kv_, bt, sl, st_, out_, ResidentVSource(kv_), scale=case.scale)
+    run(q, kv, out, st)                                   # consistent: runs
+    torch.cuda.synchronize()
+    st.max_reqs = 2                                       # more requests than the state
+    with pytest.raises(ValueError, match="max_reqs"):
+        run(q, kv, out, st)
+    st.max_reqs = 3
+    st.G = 8                                              # state built for another group
+    with pytest.raises(ValueError, match="geometry"):
+        run(q, kv, out, st)
+    st.G = 4
+    with pytest.raises(ValueError, match="query heads"):
+        run(q[:, :30], kv, out, st)
+    # a cache view one element off its 16-byte alignment
+    flat = torch.empty(kv.numel() + 8, dtype=torch.bfloat16, device=DEV)
+    bad = flat.as_strided(kv.shape, kv.stride(), 1)
+    bad.copy_(kv)
+    with pytest.raises(AmassError):
+        run(q, bad, out, st)
+    torch.cuda.synchronize()
