@@ -160,6 +160,7 @@ ENTRY_POINTS = {
     "amass_topb_select": SelectArgs,
     "amass_coverage_select": SelectArgs,
     "amass_sparse_decode": DecodeArgs,
+    "amass_sparse_decode_noalloc": DecodeArgs,
     "amass_dense_paged_decode": DecodeArgs,
     "amass_tier_decode": DecodeArgs,
     "amass_tier_gather_plan": TierPlanArgs,

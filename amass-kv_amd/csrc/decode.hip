@@ -32,6 +32,8 @@
 // workgroup per unit, merges them (attention/merge.py:21-50); a cross-workgroup ticket
 // in one launch was measured slower, its device-scope fences write back and invalidate
 // the XCD's L2.
+#include <mutex>
+
 #include "common.h"
 
 namespace amass {
@@ -635,12 +637,71 @@ static int decode_common(const amass_decode_args* ain, int force_dense, int v_sr
     return launch_decode<0, false>(a, a.path, s);
 }
 
+// ------------------------------------------------------------------ allocation-free variant
+// The split-K partials live in one file-scope device array (each GPU holds its own copy
+// for the life of the process).  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in symbol): the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current and kept.
+constexpr int64_t DEC_SCRATCH_BYTES = AMASS_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[DEC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int DEC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[DEC_MAX_DEVICES] = {nullptr};
+
+static int scratch_address(float** out) {
+    int dev = 0;
+    int rc = record_hip(hipGetDevice(&dev));
+    if (rc) return rc;
+    if (dev < 0 || dev >= DEC_MAX_DEVICES) return AMASS_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        rc = record_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (rc) return rc;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return AMASS_OK;
+}
+
+// Bytes of partials a launch of `a` uses: m and l (R, n_kv, split, G) each, then acc
+// (R, n_kv, split, G, d) at a 256-byte boundary; 0 when only the fused pass runs.
+static int64_t decode_partial_bytes(const amass_decode_args& a, int64_t& acc_off) {
+    acc_off = 0;
+    if (a.path == 2 || a.split < 3) return 0;
+    const int64_t slots = (int64_t)a.n_req * a.n_kv * a.split * a.G;
+    acc_off = ((2 * slots * (int64_t)sizeof(float)) + 255) & ~(int64_t)255;
+    return acc_off + slots * DEC_D * (int64_t)sizeof(float);
+}
+
+static int decode_noalloc(const amass_decode_args* ain, hipStream_t s) {
+    if (!ain) return AMASS_ERR_NULL;
+    amass_decode_args a = *ain;
+    if (a.n_req < 0 || a.n_kv < 1 || a.G < 1 || a.G > 8 || a.d != DEC_D) return AMASS_ERR_GEOMETRY;
+    if (a.path != 2 && a.split < 1) return AMASS_ERR_GEOMETRY;
+    int64_t acc_off = 0;
+    const int64_t need = decode_partial_bytes(a, acc_off);
+    if (need > DEC_SCRATCH_BYTES) return AMASS_ERR_CAPACITY;
+    float* base = nullptr;
+    const int rc = scratch_address(&base);
+    if (rc) return rc;
+    const int64_t slots = (int64_t)a.n_req * a.n_kv * (a.split > 0 ? a.split : 1) * a.G;
+    a.m_part = base;
+    a.l_part = base + slots;
+    a.acc_part = base + acc_off / (int64_t)sizeof(float);
+    return decode_common(&a, 0, -1, s);
+}
+
 }  // namespace amass
 
 using namespace amass;
 
 extern "C" int amass_sparse_decode(const amass_decode_args* a, void* stream) {
     return decode_common(a, 0, -1, (hipStream_t)stream);
+}
+extern "C" int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream) {
+    return decode_noalloc(a, (hipStream_t)stream);
 }
 extern "C" int amass_dense_paged_decode(const amass_decode_args* a, void* stream) {
     return decode_common(a, 1, -1, (hipStream_t)stream);

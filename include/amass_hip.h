@@ -265,6 +265,20 @@ typedef struct amass_decode_args {
 int amass_sparse_decode(const amass_decode_args* a, void* stream);
 int amass_dense_paged_decode(const amass_decode_args* a, void* stream); /* forces dense=1 */
 
+/* No counterpart in the reference: amass_sparse_decode for callers that cannot allocate
+ * device memory (code under HIP-graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results, except that m_part / l_part /
+ * acc_part are ignored: the split-K partials live in the library's own file-scope device
+ * array of AMASS_DECODE_SCRATCH_BYTES per GPU (held until the process ends).  The
+ * partials take 4 * n_req * n_kv * split * G * (2 + d) bytes (+ <= 256 of alignment),
+ * none with path 2 or split < 3; more than AMASS_DECODE_SCRATCH_BYTES returns
+ * AMASS_ERR_CAPACITY (e.g. n_req 32, n_kv 8, G 4 fits split <= 63).  Nothing is allocated
+ * and nothing needs clearing: every partial the merge reads is written by the same call.
+ * All calls on one GPU share its array, so calls that overlap on one GPU (two streams,
+ * two host threads) race. */
+#define AMASS_DECODE_SCRATCH_BYTES (32 * 1024 * 1024)
+int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
+
 /* ---- mem-v tier ------------------------------------------------------------------ */
 /* Replaces tier/residency.py:385-407 (gather_plan: _miss_diff_kernel +
  * _select_victims_kernel).  Per (request, kv-head) every selected COMPLETE page is a hit
