@@ -19,6 +19,7 @@ Buffers and invariants follow the reference ``tier/residency.py:281-577``:
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .._hip import (CopyRun, InvalidateArgs, TierFetchArgs, TierPlanArgs, call,
@@ -116,48 +117,66 @@ class Residency:
 
     # ---- copy-engine alternative (host planned) ---------------------------------------
     def build_dma_plan(self, layer, pool, n_req):
-        """Coalesced (dst, src, pitches, width, height) runs for the misses whose V is in
-        the pinned pool; returns (runs, has_staged).  Host-side, syncs the miss lists."""
+        """Copy-engine plan for this step's misses (the host-planned alternative to the
+        fetch kernel; reference tier/residency.py:438-493).  A miss whose V is valid in the
+        pinned pool joins a 2-D copy run; a run is a maximal chain of misses that follow
+        each other in one (request, kv head) miss list with victim slot AND block both one
+        higher than the previous one's, i.e. consecutive hot slots filled from consecutive
+        pool blocks (row pitch: one page in the hot buffer, n_kv pages in the pool).
+
+        The chains are found on the device with whole-tensor ops (a miss "extends" its
+        predecessor; heads are fetchable misses that do not; a head's run ends at the next
+        entry that does not extend), and the host receives one compact table of (kv, slot,
+        block, height) rows.  Returns (runs, has_staged): runs is an (n, 6) int64 array of
+        amass_copy_run rows (dst, src, dpitch, spitch, width, height); has_staged tells
+        that some miss's V is only in the staging pool, which the fetch kernel copies."""
         n_kv, S, NB, page, d = self.n_kv, self.S, self.NB, self.page, self.d
-        pbytes = page * d * 2
-        mcnt = self.miss_cnt.cpu()
-        mpage = self.miss_pages.cpu()
-        vict = self.victim_slots.cpu()
-        valid = self.pool_valid[layer].cpu()
+        pbytes = page * d * torch.empty(0, dtype=self.dtype).element_size()
+        if n_req <= 0:
+            return np.zeros((0, 6), np.int64), False
+        dev = self.miss_pages.device
+        blk = self.miss_pages[:n_req].long()
+        slot = self.victim_slots[:n_req].long()
+        live = (torch.arange(blk.shape[-1], device=dev) < self.miss_cnt[:n_req, :, None]) \
+            & (slot >= 0)
+        kvi = torch.arange(n_kv, device=dev).view(1, n_kv, 1).expand_as(blk)
+        in_pool = self.pool_valid[layer][kvi, blk.clamp(0, NB - 1)] != 0
+        fetch = live & in_pool
+        ext = torch.zeros_like(fetch)
+        ext[..., 1:] = (fetch[..., 1:] & fetch[..., :-1]
+                        & (slot[..., 1:] == slot[..., :-1] + 1)
+                        & (blk[..., 1:] == blk[..., :-1] + 1))
+        heads = torch.nonzero((fetch & ~ext).flatten()).flatten()
+        ends = torch.nonzero((~ext).flatten()).flatten()
+        ends = torch.cat([ends, ends.new_tensor([ext.numel()])])
+        height = ends[torch.searchsorted(ends[:-1], heads, right=True)] - heads
+        table = torch.stack([(heads // blk.shape[-1]) % n_kv, slot.flatten()[heads],
+                             blk.flatten()[heads], height], dim=1)
+        flag = (live & ~in_pool).any().long().view(1, 1).expand(1, 4)
+        host = torch.cat([flag, table]).cpu().numpy()          # the one device -> host copy
+        has_staged, (kv, sl, bk, h) = bool(host[0, 0]), host[1:].T
         hot_base = self.hot[layer].data_ptr()
-        pool_host = pool._host_ptr + layer * NB * n_kv * page * d * 2
-        runs, has_staged = [], False
-        for r in range(n_req):
-            for kv in range(n_kv):
-                m, i = int(mcnt[r, kv]), 0
-                while i < m:
-                    slot, blk = int(vict[r, kv, i]), int(mpage[r, kv, i])
-                    if slot < 0:
-                        i += 1
-                        continue
-                    if int(valid[kv, blk]) == 0:
-                        has_staged = True
-                        i += 1
-                        continue
-                    run = 1
-                    while (i + run < m and int(vict[r, kv, i + run]) == slot + run
-                           and int(mpage[r, kv, i + run]) == blk + run
-                           and int(valid[kv, blk + run]) == 1):
-                        run += 1
-                    runs.append((hot_base + (kv * S + slot) * pbytes,
-                                 pool_host + (blk * n_kv + kv) * pbytes,
-                                 pbytes, n_kv * pbytes, pbytes, run))
-                    i += run
+        pool_base = pool._host_ptr + layer * NB * n_kv * pbytes
+        runs = np.empty((host.shape[0] - 1, 6), np.int64)
+        runs[:, 0] = hot_base + (kv * S + sl) * pbytes
+        runs[:, 1] = pool_base + (bk * n_kv + kv) * pbytes
+        runs[:, 2] = pbytes
+        runs[:, 3] = n_kv * pbytes
+        runs[:, 4] = pbytes
+        runs[:, 5] = h
         return runs, has_staged
 
     @staticmethod
     def issue_dma_plan(runs, stream) -> None:
-        if not runs:
+        """Issue an (n, 6) int64 run table (amass_copy_run rows) on `stream`."""
+        if len(runs) == 0:
             return
-        arr = (CopyRun * len(runs))(*[CopyRun(*r) for r in runs])
-        from .._hip import check, load_library
         import ctypes
-        check(load_library().amass_tier_dma(arr, len(runs), ctypes.c_void_p(stream.cuda_stream)),
+        from .._hip import check, load_library
+        runs = np.ascontiguousarray(runs, dtype=np.int64)
+        assert runs.shape[1] * 8 == ctypes.sizeof(CopyRun)
+        check(load_library().amass_tier_dma(runs.ctypes.data_as(ctypes.POINTER(CopyRun)),
+                                            len(runs), ctypes.c_void_p(stream.cuda_stream)),
               "amass_tier_dma")
 
     # ---- invariants ------------------------------------------------------------------
