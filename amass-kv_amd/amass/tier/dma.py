@@ -23,10 +23,10 @@ class CopyEngine:
         self._i = (self._i + 1) % len(self.streams)
         return s
 
-    def issue(self, runs, stream=None) -> torch.cuda.Event:
+    def issue(self, runs, stream=None, timing: bool = False) -> torch.cuda.Event:
         stream = stream or self.next_stream()
         stream.wait_stream(torch.cuda.current_stream(self.device))
         Residency.issue_dma_plan(runs, stream)
-        ev = torch.cuda.Event()
+        ev = torch.cuda.Event(enable_timing=timing)
         ev.record(stream)
         return ev

@@ -10,8 +10,9 @@ speedup over a dense paged decode of all 1024 pages on the same GPU.
 One JSON line is printed.  `value` is the sparse step time in us per layer (lower is
 better); `roofline` is for the kernel with the largest share of the step, using its
 algorithmic bytes per launch over its average duration measured with HIP events on the
-launch stream; `cpu_baseline` times the CPU oracle (the numpy restatement of the
-reference's score / select / attend path) on a bounded sample of the same workload.
+launch stream; `cpu_baseline` times the fp32 PyTorch restatement of the reference's
+score / select / attend path (oracle/torch_path.py) on the host cores
+(torch.set_num_threads = the process's cores), config 0 and config 1, per stage.
 Inputs are synthetic (amass.bench.synth, seeded) and resident in HBM before timing.
 
 Secondary lines (under "configs"; skipped with --quick): config 1 with the key-norm boost,
@@ -77,6 +78,28 @@ def time_graph(g, steps, warmup, reps=1, batches=7):
         b.record()
         torch.cuda.synchronize()
         out.append(a.elapsed_time(b) / (steps * reps))
+    return statistics.median(out)
+
+
+def time_eager(fn, steps, warmup, batches=7):
+    """The eager counterpart of time_graph: median over `batches` of the average ms per
+    call of `steps` back-to-back eager calls between one event pair (the reference's
+    eager mode, bench/timing.py:58-70): host launch overhead included."""
+    import statistics
+
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(batches):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) / steps)
     return statistics.median(out)
 
 
@@ -149,46 +172,106 @@ def attend_bytes(cnt, n_req, n_kv, G, d=128, page=16):
     return pages * (page * d * 2 * 2 + 4 + 4) + 2 * n_req * n_kv * G * d * 2
 
 
-def cpu_baseline(case, st, budget_s=15.0):
-    """Time the CPU oracle chain (quad score fp64 -> nrm -> coverage select -> attend) on
-    whole requests until ~budget_s of work, then scale to the full batch."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    import oracle.decode as odec
-    import oracle.score as osc
-    import oracle.select as osel
 
-    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
-    i = lambda t: t.detach().cpu().numpy()          # noqa: E731
+def cpu_threads():
+    """(threads used, affinity count): torch uses every core of the process's affinity,
+    capped by OMP_NUM_THREADS when the host sets it (the process's share of a shared
+    box)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    n = min(aff, int(omp)) if omp.isdigit() and int(omp) > 0 else aff
+    return n, aff
+
+
+def cpu_path(case, st, *, mode, coverage, budget_s, warmup=3, iters=10):
+    """Time the fp32 torch restatement of the reference path (oracle/torch_path.py:
+    quad score -> nrm -> top-b / coverage select -> attend) on the host cores over the
+    first n requests of `case` (all, unless one pass of all would overrun `budget_s`
+    over warmup + iters passes); per stage the median of `iters` passes after `warmup`
+    (time.perf_counter_ns).  Returns us per layer scaled to the whole batch."""
+    import statistics
+
+    import torch
+
+    import oracle.torch_path as tp
+
     mu, mus, _, Vs, sg, _ = st.layer_state(0)
-    V = st.reference_V(0)
-    host = dict(q=f(case.q), mu=i(mu), mus=f(mus), V=i(V), Vs=f(Vs), sg=f(sg),
-                bt=i(case.block_table), sl=i(case.seq_lens), K=f(case.kv_cache[:, 0]),
-                Vc=f(case.kv_cache[:, 1]), npg=i(st.n_pages), nsh=i(st.n_sel_hi),
-                bfix=i(st.b_fix))
-    B = case.q.shape[0]
-    done, t_total = 0, 0.0
-    with threadpool_limits(limits=1):
-        while done < B and t_total < budget_s:
-            r = slice(done, done + 1)
-            t0 = time.perf_counter()
-            sh = osc.quad_score(host["q"][r], host["mu"], host["mus"], host["V"], host["Vs"],
-                                host["sg"], host["bt"][r], host["nsh"][r], scale=case.scale,
-                                page=16, G=case.G, v_bits=st.v_bits, max_pages=st.max_pages,
-                                combine="nrm")
-            sc = osc.nrm_combine(sh, host["nsh"][r]).astype(np.float32)
-            tab, cnt, _ = osel.select(sc, host["npg"][r], host["nsh"][r], host["bfix"][r],
-                                      sink=1, max_pages=st.max_pages, mode=1, coverage=0.95,
-                                      score_kind=1)
-            odec.attend(host["q"][r], host["K"], host["Vc"], host["bt"][r], host["sl"][r],
-                        tab, cnt, scale=case.scale, G=case.G)
-            t_total += time.perf_counter() - t0
-            done += 1
-    us_full = t_total / done * B * 1e6
-    return {"value": round(us_full, 1), "unit": "us/layer", "cores": 1, "kind": "port",
-            "sample": f"{done} of {B} requests of config 1 (oracle: quad fp64 score, nrm, "
-                      f"coverage select, fp64 attend; numpy, 1 thread), scaled x{B / done:.1f}"}
+    cpu = lambda t: t.detach().cpu()  # noqa: E731
+    h = dict(mu=cpu(mu), mus=cpu(mus), V=cpu(st.reference_V(0)), Vs=cpu(Vs), sg=cpu(sg),
+             bt=cpu(case.block_table), sl=cpu(case.seq_lens), K=cpu(case.kv_cache[:, 0]),
+             Vc=cpu(case.kv_cache[:, 1]), q=cpu(case.q).float())
+    B, MP = case.q.shape[0], case.max_pages
+    npg, nsh, bfix = tp.derive(h["sl"], st.budget, 16, st.window_pages, st.sink_pages)
+
+    def run(n):
+        t = [time.perf_counter_ns()]
+        sh = tp.quad_score(h["q"][:n], h["mu"], h["mus"], h["V"], h["Vs"], h["sg"],
+                           h["bt"][:n], nsh[:n], scale=case.scale, page=16, G=case.G,
+                           v_bits=st.v_bits, max_pages=MP)
+        sc = tp.nrm_combine(sh, nsh[:n])
+        t.append(time.perf_counter_ns())
+        tab, cnt = tp.select(sc, npg[:n], nsh[:n], bfix[:n], sink=st.sink_pages,
+                             max_pages=MP, mode=mode, coverage=coverage, score_kind=1)
+        t.append(time.perf_counter_ns())
+        tp.attend(h["q"][:n], h["K"], h["Vc"], h["bt"][:n], h["sl"][:n], tab, cnt,
+                  scale=case.scale, G=case.G)
+        t.append(time.perf_counter_ns())
+        return [(t[i + 1] - t[i]) / 1e3 for i in range(3)], float(cnt.double().mean())
+
+    n = B
+    first, _ = run(1)                                   # one request: size the sample
+    per_req = sum(first) / 1e6
+    if per_req * B * (warmup + iters) > budget_s:
+        n = max(1, min(B, int(budget_s / (per_req * (warmup + iters)))))
+    for _ in range(warmup):
+        run(n)
+    samples = [run(n) for _ in range(iters)]
+    med = [statistics.median(x[0][i] for x in samples) for i in range(3)]
+    f = B / n
+    return dict(score_us=round(med[0] * f, 1), select_us=round(med[1] * f, 1),
+                attend_us=round(med[2] * f, 1), total_us=round(sum(med) * f, 1),
+                requests_timed=n, requests=B, pages_per_unit=round(samples[-1][1], 1))
+
+
+def cpu_baseline(case1, st1, args):
+    """BASELINE's CPU plan: the fp32 torch path with torch.set_num_threads(cores), config 0
+    (B=1 ctx 4096, fixed 5 %: b = 13) and config 1 (the headline), each split into score /
+    select / attend; `value` is config 1's us per layer."""
+    import torch
+
+    from amass.bench.synth import build_quad_state, config_case
+
+    n, aff = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(n)
+    try:
+        case0 = config_case(0, seed=args.seed, device="cuda")
+        st0 = build_quad_state(case0, rank=8, v_bits=8, combine="nrm", budget=0.05)
+        c0 = cpu_path(case0, st0, mode=0, coverage=1.0, budget_s=5.0)
+        del case0, st0
+        c1 = cpu_path(case1, st1, mode=1, coverage=0.95, budget_s=25.0)
+    finally:
+        torch.set_num_threads(prev)
+    log(f"cpu baseline ({n} threads): config 0 {c0['total_us']} us, config 1 "
+        f"{c1['total_us']} us ({c1['requests_timed']} of {c1['requests']} requests timed)")
+    return {"value": c1["total_us"], "unit": "us/layer", "cores": n, "kind": "port",
+            "sample": (f"config 1: {c1['requests_timed']} of {c1['requests']} requests "
+                       f"timed, scaled x{c1['requests'] / c1['requests_timed']:.2f}; fp32 "
+                       "torch restatement of quad score -> nrm -> coverage select -> "
+                       "attend (oracle/torch_path.py), median of 10 after 3 warmups per "
+                       "stage"),
+            "cpu_model": cpu_model(), "affinity_cores": aff,
+            "torch_threads": n, "config1": c1, "config0": c0}
 
 
 def kernel_entry(us, nbytes, traffic=None):
@@ -258,6 +341,8 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     g_dense = graph_of(dense_step)
     ms_sparse = time_graph(g_sparse, args.steps, args.warmup)
     ms_dense = time_graph(g_dense, args.steps, args.warmup)
+    ms_sparse_eager = time_eager(sparse_step, args.steps, args.warmup)
+    ms_dense_eager = time_eager(dense_step, args.steps, args.warmup)
     reps = 10
     k_steps = max(5, args.steps // 5)
     g_score = graph_of(score_only, reps)
@@ -288,6 +373,8 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
                 dense_us=round(ms_dense * 1e3, 2),
                 dense_gb_s=round(b_dense / (ms_dense * 1e-3) / 1e9, 1),
                 speedup_vs_dense=round(ms_dense / ms_sparse, 3),
+                eager_us=round(ms_sparse_eager * 1e3, 2),
+                dense_eager_us=round(ms_dense_eager * 1e3, 2),
                 selected_fraction=round(frac, 4), attended_fraction=round(att_frac, 4),
                 kernels=kernels)
 
@@ -371,18 +458,21 @@ def run_summary_build(args):
 
 
 def run_config4(args, boost="sigma", steps=64):
-    """mem-v: V in the pinned, device-mapped host pool, a 10 % hot buffer, 64 decode steps
-    with fresh N(0, 1) queries over a fixed boosted page set.  Each step = quad score +
-    coverage select + residency plan + fetch + tiered decode (eager, one event pair around
-    the 64 steps, from a cold hot buffer).  Host bytes = miss pages x 4 KiB (each miss is
-    read over the host link once, into its slot or, when the buffer is exhausted, directly
-    by the decode)."""
+    """mem-v at config 4: V in the pinned, device-mapped host pool, a 10 % hot buffer, 64
+    decode steps over a fixed boosted page set, each from a cold hot buffer.  Two query
+    streams: "fresh" (BASELINE's literal N(0, 1) each step) and "correlated" (the case's
+    queries + 0.3 N(0, 1): the boosted set stays the relevant one, which is the regime a
+    hot buffer is for).  Each step = quad score + coverage select, residency plan, fetch
+    (the fetch kernel, or the copy engine on a side stream after a host-side run plan),
+    tiered decode; each phase is timed with HIP events (plan + host run planning for the
+    copy engine: wall clock, it synchronises).  Host bytes = miss pages x 4 KiB."""
     import torch
 
     from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
     from amass.bench.synth import build_quad_state, config_case
     from amass.selection import derive_page_params, select_pages_quad
-    from amass.tier import Tier, mem_dynamic_decode
+    from amass.tier import Tier
+    from amass.tier.decode_mem import mem_decode
 
     t0 = time.time()
     case = config_case(4, seed=args.seed, device="cuda", boost=boost)
@@ -396,11 +486,10 @@ def run_config4(args, boost="sigma", steps=64):
     log(f"config 4 ({boost}): inputs, summaries, pinned pool {time.time() - t0:.1f}s")
     bt, sl = case.block_table, case.seq_lens
     derive_page_params(st, sl, B)
-    gen = torch.Generator(device="cuda").manual_seed(args.seed + 404)
-    qs = [torch.randn(B, n_kv * G, 128, generator=gen, device="cuda").to(torch.bfloat16)
-          for _ in range(steps)]
     out = torch.zeros(B, n_kv * G, 128, dtype=torch.bfloat16, device="cuda")
     r5 = tier.residency
+    vsrc = ResidentVSource(case.kv_cache)
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
 
     def cold():
         r5.page2slot.fill_(-1)
@@ -409,49 +498,106 @@ def run_config4(args, boost="sigma", steps=64):
         r5.clock.fill_(1)
         r5.overflow.zero_()
 
-    def one(qt):
-        select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
-        mem_dynamic_decode(qt, case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale,
-                           fetch="kernel")
+    def queries(stream):
+        gen = torch.Generator(device="cuda").manual_seed(args.seed + 404)
+        qs = []
+        for _ in range(steps):
+            z = torch.randn(B, n_kv * G, 128, generator=gen, device="cuda")
+            qs.append((z if stream == "fresh" else case.q.float() + 0.3 * z)
+                      .to(torch.bfloat16))
+        return qs
 
-    # pass 1 (statistics, host reads between steps), pass 2 (timed), both from cold
-    cold()
-    sel = miss = 0
-    for qt in qs:
-        one(qt)
-        sel += int(st.page_cnt[:B].sum())
-        miss += int(r5.miss_cnt[:B].sum())
-    cold()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for qt in qs:
-        one(qt)
-    b.record()
-    torch.cuda.synchronize()
-    us_step = a.elapsed_time(b) / steps * 1e3
-    # the same steps with V resident in HBM (graph per step is not needed: eager, same loop)
-    vsrc = ResidentVSource(case.kv_cache)
-    a.record()
-    for qt in qs:
-        select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
-        sparse_paged_decode_batched(qt, case.kv_cache, bt, sl, st, out, vsrc, scale=case.scale)
-    b.record()
-    torch.cuda.synchronize()
-    us_res = a.elapsed_time(b) / steps * 1e3
-    host_bytes = miss * 16 * 128 * 2 / steps
-    wp = write_path_times(tier, case, args)
+    def run(qs, fetch, max_runs=20000):
+        """Per-phase us (mean over the steps run) + hit statistics, from cold."""
+        cold()
+        torch.cuda.synchronize()
+        ph = dict(select=0.0, plan=0.0, fetch=0.0, decode=0.0)
+        sel = miss = runs_tot = 0
+        n_done = 0
+        w0 = time.perf_counter()
+        for qt in qs:
+            e = [ev() for _ in range(4)]
+            e[0].record()
+            select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
+            e[1].record()
+            r5.gather_plan(0, st.page_table, st.page_cnt, bt, sl, B)
+            e[2].record()
+            if fetch == "kernel":
+                r5.gather_fetch(0, tier.staging, tier.pool, B)
+                e[3].record()
+                mem_decode(qt, case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale)
+                e4 = ev()
+                e4.record()
+                torch.cuda.synchronize()
+                ph["plan"] += e[1].elapsed_time(e[2]) * 1e3
+                ph["fetch"] += e[2].elapsed_time(e[3]) * 1e3
+                ph["decode"] += e[3].elapsed_time(e4) * 1e3
+            else:
+                e[2].synchronize()
+                h0 = time.perf_counter()
+                plan, staged = r5.build_dma_plan(0, tier.pool, B)     # synchronises
+                ph["plan"] += (time.perf_counter() - h0) * 1e6 + e[1].elapsed_time(e[2]) * 1e3
+                side = tier.copy_engine.next_stream()
+                side.wait_stream(torch.cuda.current_stream())
+                fs = ev()
+                fs.record(side)
+                done = tier.copy_engine.issue(plan, side, timing=True)
+                if staged:
+                    r5.gather_fetch(0, tier.staging, tier.pool, B)
+                torch.cuda.current_stream().wait_event(done)
+                e[3].record()
+                mem_decode(qt, case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale)
+                e4 = ev()
+                e4.record()
+                torch.cuda.synchronize()
+                ph["fetch"] += fs.elapsed_time(done) * 1e3
+                ph["decode"] += e[3].elapsed_time(e4) * 1e3
+                runs_tot += len(plan)
+            ph["select"] += e[0].elapsed_time(e[1]) * 1e3
+            sel += int(st.page_cnt[:B].sum())
+            miss += int(r5.miss_cnt[:B].sum())
+            n_done += 1
+            if fetch == "dma" and runs_tot / n_done > max_runs and n_done >= 2:
+                break                      # one host API call per run: a bounded sample
+        wall = (time.perf_counter() - w0) * 1e6 / n_done
+        hb = miss * 16 * 128 * 2 / n_done
+        r = {k: round(v / n_done, 1) for k, v in ph.items()}
+        r.update(steps=n_done, hit_rate=round(1.0 - miss / max(sel, 1), 4),
+                 selected_pages_per_step=round(sel / n_done, 1),
+                 miss_pages_per_step=round(miss / n_done, 1),
+                 host_bytes_per_step=int(hb),
+                 host_link_gb_s=round(hb / max(r["fetch"], 1e-3) / 1e3, 2),
+                 us_per_step=round(sum(r[k] for k in ("select", "plan", "fetch", "decode")),
+                                   1),
+                 wall_us_per_step=round(wall, 1))
+        if fetch == "dma":
+            r["copy_runs_per_step"] = round(runs_tot / n_done, 1)
+        return r
+
     res = dict(workload=f"config4: mem-v B={B} ctx 32768 quad r'=8 int8 nrm coverage 0.95, "
-                        f"hot buffer {slots} slots per kv head (10 %), {steps} steps, fresh "
-                        f"N(0,1) queries, boost {boost}",
-               us_per_step=round(us_step, 1), resident_us_per_step=round(us_res, 1),
-               hit_rate=round(1.0 - miss / max(sel, 1), 4),
-               selected_pages_per_step=round(sel / steps, 1),
-               host_bytes_per_step=int(host_bytes),
-               host_link_gb_s=round(host_bytes / (us_step * 1e-6) / 1e9, 2),
-               write_path=wp)
-    log(f"config 4 ({boost}): {us_step:.1f} us/step (resident {us_res:.1f}), "
-        f"hit rate {res['hit_rate']}; write path {wp}")
+                        f"hot buffer {slots} slots per kv head (10 %), {steps} steps from a "
+                        f"cold buffer, boost {boost}; streams: fresh N(0,1) queries "
+                        f"(literal) and correlated (case q + 0.3 N(0,1))")
+    for stream in ("fresh", "correlated"):
+        qs = queries(stream)
+        res[stream] = {f: run(qs, f) for f in ("kernel", "dma")}
+        # the same steps with V resident in HBM
+        a, b = ev(), ev()
+        a.record()
+        for qt in qs:
+            select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
+            sparse_paged_decode_batched(qt, case.kv_cache, bt, sl, st, out, vsrc,
+                                        scale=case.scale)
+        b.record()
+        torch.cuda.synchronize()
+        res[stream]["resident_us_per_step"] = round(a.elapsed_time(b) / steps * 1e3, 1)
+        k = res[stream]["kernel"]
+        log(f"config 4 ({boost}, {stream}): hit {k['hit_rate']}, kernel fetch "
+            f"{k['us_per_step']} us/step (select {k['select']}, plan {k['plan']}, fetch "
+            f"{k['fetch']}, decode {k['decode']}), dma {res[stream]['dma']['us_per_step']}, "
+            f"resident {res[stream]['resident_us_per_step']}")
+        del qs
+    res["write_path"] = write_path_times(tier, case, args)
     return res
 
 
@@ -501,8 +647,9 @@ def main():
     ap.add_argument("--boost", default="sigma", choices=["sigma", "keynorm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
-    ap.add_argument("--configs", default="1k,clse,2,3,4,build",
-                    help="secondary lines: 1k (config 1 with the key-norm boost), clse (the "
+    ap.add_argument("--configs", default="0,1k,clse,2,3,4,build",
+                    help="secondary lines: 0 (config 0 on the GPU), 1k (config 1 with the "
+                         "key-norm boost), clse (the "
                          "CLSE score at the config-1 shape), 2, 3, 4, build (the HIP "
                          "summary builder)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -560,6 +707,7 @@ def main():
                    "graph": "hipGraph replay of score+select+attend"},
         "gb_s": m["gb_s"], "dense_us": m["dense_us"], "dense_gb_s": m["dense_gb_s"],
         "speedup_vs_dense": m["speedup_vs_dense"],
+        "eager_us": m["eager_us"], "dense_eager_us": m["dense_eager_us"],
         "selected_fraction": m["selected_fraction"],
         "attended_fraction": m["attended_fraction"],
         "kernels": kernels,
@@ -589,11 +737,8 @@ def main():
         derive_page_params(st, case.seq_lens, B)
         torch.cuda.synchronize()
     if not args.no_cpu_baseline:
-        from amass.selection import select_pages_quad
-        select_pages_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
-                          derive=False)
         torch.cuda.synchronize()
-        res["cpu_baseline"] = cpu_baseline(case, st)
+        res["cpu_baseline"] = cpu_baseline(case, st, args)
     if not args.quick:
         del case, st
         free_gpu()
@@ -601,7 +746,7 @@ def main():
         for c in [x.strip() for x in args.configs.split(",") if x.strip()]:
             if c == "1k":
                 sec["config1_keynorm"] = run_secondary(1, args, boost="keynorm")
-            elif c in ("2", "3"):
+            elif c in ("0", "2", "3"):
                 sec[f"config{c}"] = run_secondary(int(c), args)
             elif c == "build":
                 sec["summary_build"] = run_summary_build(args)
