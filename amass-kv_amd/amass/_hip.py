@@ -18,7 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
-ABI_VERSION = 6     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
+ABI_VERSION = 7     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):
@@ -38,7 +38,8 @@ def _fields(spec: str):
 class QuadScoreArgs(C.Structure):
     _fields_ = _fields(
         "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 n_sel_hi:p "
-        "score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 comb_out:p "
+        "score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 "
+        "tile_max:p tm_sr:i64 tm_sh:i64 tm_sg:i64 comb_out:p "
         "scale:f32 n_req:i32 n_kv:i32 G:i32 d:i32 page:i32 rank:i32 v_bits:i32 "
         "max_pages:i32 combine:i32")
 
@@ -54,7 +55,8 @@ class ClseScoreArgs(C.Structure):
     _fields_ = _fields(
         "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 seq_lens:p "
         "n_sel_hi:p score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 "
-        "comb_out:p scale:f32 n_req:i32 n_kv:i32 G:i32 d:i32 page:i32 rank:i32 v_bits:i32 "
+        "tile_max:p tm_sr:i64 tm_sh:i64 tm_sg:i64 comb_out:p scale:f32 n_req:i32 n_kv:i32 "
+        "G:i32 d:i32 page:i32 rank:i32 v_bits:i32 "
         "c_bits:i32 max_pages:i32 combine:i32")
 
 
@@ -72,8 +74,9 @@ class NrmArgs(C.Structure):
 
 class SelectArgs(C.Structure):
     _fields_ = _fields(
-        "score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 n_pages:p "
-        "n_sel_hi:p b_fix:p page_table:p pt_sr:i64 pt_sh:i64 page_cnt:p pc_sr:i64 "
+        "score:p sc_sr:i64 sc_sh:i64 score_h:p sh_sr:i64 sh_sh:i64 sh_sg:i64 "
+        "tile_max:p tm_sr:i64 tm_sh:i64 tm_sg:i64 n_pages:p n_sel_hi:p b_fix:p "
+        "page_table:p pt_sr:i64 pt_sh:i64 page_cnt:p pc_sr:i64 "
         "n_sel_out:p coverage:f64 n_req:i32 n_kv:i32 G:i32 max_pages:i32 sink_pages:i32 "
         "mode:i32 tie_mode:i32 score_kind:i32")
 

@@ -5,7 +5,9 @@ Same contract as the reference ``quad_score`` (selection/quad_score.py:110-139) 
 region [0, n_sel_hi); combine="nrm" first writes the per-head scores ``st.score_h`` and
 then the per-head-normalised mass sum_g exp(S_g - max_p S_g) into ``st.score``.
 ``select_pages_quad`` folds that nrm combine into the selection launch instead of a
-separate kernel (one less launch and one less pass over score_h).
+separate kernel (one less launch and one less pass over score_h); the score launch also
+writes per-16-page-tile per-head maxima (``st.score_tmax``), so the selection reads
+score_h once.
 """
 from __future__ import annotations
 
@@ -13,6 +15,17 @@ import torch
 
 from .._hip import ClseScoreArgs, NrmArgs, QuadScoreArgs, call, current_stream, ptr, require_cuda
 from .select import derive_page_params, select_pages
+
+
+def _tile_max(st):
+    """The state's per-tile per-head maxima buffer (nrm states), or None."""
+    return getattr(st, "score_tmax", None) if st.combine == "nrm" else None
+
+
+def _tile_max_fields(tm) -> dict:
+    return dict(tile_max=ptr(tm), tm_sr=tm.stride(0) if tm is not None else 0,
+                tm_sh=tm.stride(1) if tm is not None else 0,
+                tm_sg=tm.stride(2) if tm is not None else 0)
 
 
 def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadScoreArgs:
@@ -29,7 +42,7 @@ def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadSc
     if getattr(st, "coords", "none") != "none":
         raise ValueError("a CLSE state (coords='lse') is scored by clse_score")
     nrm = st.combine == "nrm"
-    sh = st.score_h
+    sh, tm = st.score_h, _tile_max(st)
     return QuadScoreArgs(
         q=ptr(q), q_st=q.stride(0), q_hs=q.stride(1),
         rec=ptr(rec), rec_sb=rec.stride(0),
@@ -39,6 +52,7 @@ def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadSc
         score_h=ptr(sh) if nrm else None,
         sh_sr=sh.stride(0) if nrm else 0, sh_sh=sh.stride(1) if nrm else 0,
         sh_sg=sh.stride(2) if nrm else 0,
+        **_tile_max_fields(tm),
         comb_out=ptr(comb_out), scale=float(scale),
         n_req=n_req, n_kv=st.n_kv, G=st.G, d=st.d, page=st.page, rank=st.r,
         v_bits=st.v_bits, max_pages=st.max_pages, combine=1 if nrm else 0)
@@ -77,7 +91,9 @@ def select_pages_quad(st, layer: int, q, block_table, seq_lens, n_req: int, scal
     if derive:
         derive_page_params(st, seq_lens, n_req)
     quad_score_launch(st, layer, q, block_table, n_req, scale)
-    select_pages(st, n_req, score_h=st.score_h if st.combine == "nrm" else None)
+    nrm = st.combine == "nrm"
+    select_pages(st, n_req, score_h=st.score_h if nrm else None,
+                 tile_max=_tile_max(st) if nrm else None)
 
 
 def clse_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
@@ -109,6 +125,7 @@ def clse_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: floa
         score_h=ptr(sh) if nrm else None,
         sh_sr=sh.stride(0) if nrm else 0, sh_sh=sh.stride(1) if nrm else 0,
         sh_sg=sh.stride(2) if nrm else 0,
+        **_tile_max_fields(_tile_max(st)),
         comb_out=ptr(comb_out), scale=float(scale), n_req=n_req, n_kv=st.n_kv, G=st.G,
         d=st.d, page=st.page, rank=st.r, v_bits=st.v_bits, c_bits=st.c_bits,
         max_pages=st.max_pages, combine=1 if nrm else 0)
@@ -122,4 +139,6 @@ def select_pages_clse(st, layer: int, q, block_table, seq_lens, n_req: int, scal
     if derive:
         derive_page_params(st, seq_lens, n_req)
     clse_score(st, layer, q, block_table, seq_lens, n_req, scale)
-    select_pages(st, n_req, score_h=st.score_h if st.combine == "nrm" else None)
+    nrm = st.combine == "nrm"
+    select_pages(st, n_req, score_h=st.score_h if nrm else None,
+                 tile_max=_tile_max(st) if nrm else None)

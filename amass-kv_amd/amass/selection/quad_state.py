@@ -34,7 +34,8 @@ with V_scale at half 0, c_scale at halves 8..23 (``c_grain="page"``: one scale p
 quad_resid at half 25; ``quad_sig2`` is None there.
 
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
-(R, n_kv, G, MP) and hmax (R, n_kv, G).
+(R, n_kv, G, MP) and score_tmax (R, n_kv, G, ceil(MP / 16)), the per-16-page-tile
+per-head maxima the score launch writes beside score_h for the fused nrm combine.
 """
 from __future__ import annotations
 
@@ -175,9 +176,10 @@ class QuadState:
         self.n_sel = torch.zeros(R, n_kv, device=device, dtype=i32)
         if combine == "nrm":
             self.score_h = torch.empty(R, n_kv, G, MP, device=device, dtype=f32)
-            self.hmax = torch.zeros(R, n_kv, G, device=device, dtype=f32)
+            self.score_tmax = torch.empty(R, n_kv, G, (MP + 15) // 16, device=device,
+                                          dtype=f32)
         else:
-            self.score_h = self.hmax = None
+            self.score_h = self.score_tmax = None
         self.n_pages = torch.zeros(R, device=device, dtype=i32)
         self.n_sel_hi = torch.zeros(R, device=device, dtype=i32)
         self.b_fix = torch.ones(R, device=device, dtype=i32)

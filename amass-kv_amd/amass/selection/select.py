@@ -44,10 +44,12 @@ def score_kind(st) -> int:
     return 1 if getattr(st, "combine", "max") == "nrm" and hasattr(st, "quad_V") else 0
 
 
-def _select(st, n_req: int, *, mode: str = "auto", score_h=None, coverage=None,
-            tie_mode=None) -> None:
+def _select(st, n_req: int, *, mode: str = "auto", score_h=None, tile_max=None,
+            coverage=None, tie_mode=None) -> None:
     if n_req > st.max_reqs:
         raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
+    if tile_max is not None and score_h is None:
+        raise ValueError("tile_max comes with score_h (the fused nrm combine)")
     if mode == "auto":
         coverage = getattr(st, "coverage", None)
     elif mode == "topb":
@@ -63,6 +65,9 @@ def _select(st, n_req: int, *, mode: str = "auto", score_h=None, coverage=None,
         sh_sr=score_h.stride(0) if score_h is not None else 0,
         sh_sh=score_h.stride(1) if score_h is not None else 0,
         sh_sg=score_h.stride(2) if score_h is not None else 0,
+        tile_max=ptr(tile_max), tm_sr=tile_max.stride(0) if tile_max is not None else 0,
+        tm_sh=tile_max.stride(1) if tile_max is not None else 0,
+        tm_sg=tile_max.stride(2) if tile_max is not None else 0,
         n_pages=ptr(st.n_pages), n_sel_hi=ptr(st.n_sel_hi), b_fix=ptr(st.b_fix),
         page_table=ptr(tab), pt_sr=tab.stride(0), pt_sh=tab.stride(1),
         page_cnt=ptr(st.page_cnt), pc_sr=st.page_cnt.stride(0),
@@ -86,11 +91,13 @@ def coverage_select(st, n_req: int, coverage: float, *, tie_mode=None) -> None:
     _select(st, n_req, mode="coverage", coverage=coverage, tie_mode=tie_mode)
 
 
-def select_pages(st, n_req: int, *, score_h=None) -> None:
+def select_pages(st, n_req: int, *, score_h=None, tile_max=None) -> None:
     """Top-b or coverage selection per the state's configuration (``st.coverage``);
     with ``score_h`` the nrm GQA combine runs fused in the same launch (and writes
-    st.score)."""
-    _select(st, n_req, mode="auto", score_h=score_h)
+    st.score).  ``tile_max``: the per-tile per-head maxima the score launch that wrote
+    ``score_h`` produced (st.score_tmax); without it the combine takes the maxima with
+    its own pass over score_h."""
+    _select(st, n_req, mode="auto", score_h=score_h, tile_max=tile_max)
 
 
 def select_pages_r8(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,

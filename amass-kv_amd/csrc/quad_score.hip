@@ -53,6 +53,7 @@ struct QuadParams {
     const int32_t* nsh;
     float* score; int64_t sc_sr, sc_sh;
     float* score_h; int64_t sh_sr, sh_sh, sh_sg;
+    float* tmax; int64_t tm_sr, tm_sh, tm_sg;      // optional per-tile per-head maxima (nrm)
     int32_t* comb_out;
     float scale;
     int n_req, n_kv, G, page, max_pages;
@@ -235,6 +236,20 @@ __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (
             if (valid && g0 < p.G) p.score_h[row + off] = S[0];
             if (valid && g1 < p.G) p.score_h[row + off + (int)p.sh_sg] = S[1];
         }
+        if (p.tmax) {
+            // the tile's maximum of S_g0 / S_g1: the 16 lanes of row kg hold its 16 pages
+            float m0 = valid ? S[0] : -INFINITY, m1 = valid ? S[1] : -INFINITY;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                m0 = fmaxf(m0, __shfl_xor(m0, o, WAVE));
+                m1 = fmaxf(m1, __shfl_xor(m1, o, WAVE));
+            }
+            if (n == 0) {
+                const int64_t t = (int64_t)req * p.tm_sr + (int64_t)h * p.tm_sh + tile;
+                if (g0 < p.G) p.tmax[t + g0 * p.tm_sg] = m0;
+                if (g1 < p.G) p.tmax[t + g1 * p.tm_sg] = m1;
+            }
+        }
     } else {
         float m = g0 < p.G ? (g1 < p.G ? fmaxf(S[0], S[1]) : S[0]) : -INFINITY;
         if (p.G > 2) m = fmaxf(m, __shfl_xor(m, 16, WAVE));
@@ -379,6 +394,8 @@ extern "C" int amass_quad_score(const amass_quad_score_args* a, void* stream) {
     p.nsh = a->n_sel_hi;
     p.score = a->score; p.sc_sr = a->sc_sr; p.sc_sh = a->sc_sh;
     p.score_h = a->score_h; p.sh_sr = a->sh_sr; p.sh_sh = a->sh_sh; p.sh_sg = a->sh_sg;
+    p.tmax = a->combine == 1 ? a->tile_max : nullptr;
+    p.tm_sr = a->tm_sr; p.tm_sh = a->tm_sh; p.tm_sg = a->tm_sg;
     p.comb_out = a->comb_out;
     p.scale = a->scale;
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.G = a->G; p.page = a->page;

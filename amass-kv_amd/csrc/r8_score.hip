@@ -27,6 +27,7 @@ extern "C" int amass_r8_score(const amass_r8_score_args* a, void* stream) {
     p.comb_out = a->comb_out;
     p.scale = a->scale;
     p.score_h = nullptr; p.sh_sr = p.sh_sh = p.sh_sg = 0;
+    p.tmax = nullptr; p.tm_sr = p.tm_sh = p.tm_sg = 0;
     p.iso_coef = 0.f;
     p.combine = 0;
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.page = a->page; p.max_pages = a->max_pages;

@@ -50,6 +50,7 @@ struct R8Params {
     const int32_t* nsh;
     float* score; int64_t sc_sr, sc_sh;
     float* score_h; int64_t sh_sr, sh_sh, sh_sg;   // CLSE per-head output (combine 1)
+    float* tmax; int64_t tm_sr, tm_sh, tm_sg;      // optional per-tile per-head maxima (nrm)
     int32_t* comb_out;
     float scale;
     float iso_coef;                               // CLSE: s^2 / (2 P (d - r))
@@ -331,6 +332,21 @@ __device__ __forceinline__ void r8_tile_tail(const R8Params& p,
             const int64_t row = (int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh + page;
             p.score_h[row + (int64_t)(2 * pair) * p.sh_sg] = S[0];
             if (G >= 2) p.score_h[row + (int64_t)(2 * pair + 1) * p.sh_sg] = S[1];
+        }
+        if (p.tmax) {
+            // the tile's maximum per head: the 16 lanes of row kg hold its 16 pages
+            float m0 = valid ? S[0] : -INFINITY, m1 = valid ? S[1] : -INFINITY;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                m0 = fmaxf(m0, __shfl_xor(m0, o, WAVE));
+                m1 = fmaxf(m1, __shfl_xor(m1, o, WAVE));
+            }
+            if (part == 0 && (threadIdx.x & 15) == 0) {
+                const int64_t t = (int64_t)req * p.tm_sr + (int64_t)h * p.tm_sh +
+                                  page / SC_TILE;
+                p.tmax[t + (int64_t)(2 * pair) * p.tm_sg] = m0;
+                if (G >= 2) p.tmax[t + (int64_t)(2 * pair + 1) * p.tm_sg] = m1;
+            }
         }
         return;
     }

@@ -1,13 +1,12 @@
 // Stage-A selection for gfx950: derive params, nrm combine, top-b / coverage nucleus.
 //
-// One workgroup (512 threads, 8 waves) per (request, kv-head).  The unit's scores are
-// staged once in LDS (fp32, up to MAXP pages), optionally produced there by the fused nrm
-// combine.  The b-th largest score is found by a 4-pass MSD radix select over
-// order-preserving uint32 keys (256-bin LDS histograms; in coverage mode each bin also
+// One workgroup (512 threads, 8 waves) per (request, kv-head), the unit's pages held in
+// registers.  The b-th largest score is found by an MSD digit search over order-preserving
+// uint32 keys (2048-bin LDS histograms of 11 key bits; in coverage mode each bin also
 // accumulates the 2^-32 fixed-point page mass with 64-bit LDS atomics, so the cut is
-// found by mass instead of by count).  Bin scans are wave-parallel prefix sums.  The
-// final keep test and the ascending compaction are two chunked block scans in page order
-// (the second also ranks ties at tau by page index).
+// found by mass instead of by count), usually one histogram followed by an exact ranking
+// of the chosen bin's keys by one wave.  The keep test and the ascending compaction rank
+// ties at tau by page index.
 //
 // Semantics follow selection/select.py:60-101 (_topb_select_kernel): keep =
 // (selectable & chosen) | p < sink | p >= n_sel_hi | (n_sel_hi - sink <= 1), compaction
@@ -19,7 +18,7 @@ namespace amass {
 
 constexpr int SEL_THREADS = 512;
 constexpr int SEL_WAVES = SEL_THREADS / WAVE;
-constexpr int SEL_MAXP = 16384;   // 64 KB of fp32 scores in LDS
+constexpr int SEL_MAXP = 16384;   // pages per request: 32 per thread of the selection
 
 // ------------------------------------------------------------------ derive params
 __global__ void derive_kernel(const int32_t* __restrict__ sl, int32_t* __restrict__ npg,
@@ -59,6 +58,10 @@ __device__ __forceinline__ int lanes_below(unsigned long long m) {
 }
 
 // ------------------------------------------------------------------ nrm combine
+// The nrm combine's exp (every combine site uses this one, so the standalone, fused and
+// pre-pass combines agree bit for bit): the hardware exp2 of x log2(e), ~1e-7 relative.
+__device__ __forceinline__ float nrm_exp(float x) { return __expf(x); }
+
 // Per-head maxima m[0..G) of the block: wave reductions, one LDS exchange, one barrier.
 __device__ __forceinline__ void head_max(float* m, int G, float (*red)[SEL_WAVES]) {
     const int w = threadIdx.x >> 6;
@@ -161,7 +164,7 @@ __device__ void nrm_run(const float* __restrict__ sh, int64_t sg, int G, int n, 
                 for (int g = 0; g < 8; ++g)
                     if (g < G)
 #pragma unroll
-                        for (int i = 0; i < V; ++i) acc[i] += expf(v[k][g][i] - m[g]);
+                        for (int i = 0; i < V; ++i) acc[i] += nrm_exp(v[k][g][i] - m[g]);
                 st_run<V>(gs, p, n, acc);
 #pragma unroll
                 for (int i = 0; i < V; ++i)
@@ -245,158 +248,336 @@ __global__ __launch_bounds__(SEL_THREADS) void nrm_kernel(const amass_nrm_args a
 }
 
 // ------------------------------------------------------------------ selection
-// A radix pass whose chosen bin holds <= SEL_CAND keys ends the radix search: those keys
-// are gathered and ranked against each other exactly (all pairs), which replaces the
-// remaining passes.
-constexpr int SEL_CAND = 256;
+// One workgroup of XS_THREADS per (request, kv-head); thread t holds pages
+// c * V * XS_THREADS + V t + i (chunk c < NC, i < V, V * NC = PPT pages per thread) in
+// registers from the first load to the page-table write, so every phase reads registers
+// and LDS carries only the histogram and small exchanges.  Phases:
+//   stage    plain scores, or the fused nrm combine over score_h with the per-head maxima
+//            taken from the score launch's per-tile maxima; the loads cover the row's
+//            MP pages and are issued before n_sel_hi arrives (the rows are MP wide);
+//   search   tau = the b-th largest key (count) or the key where the mass from the top
+//            reaches `need` (coverage): 2048-bin histograms of the key relative to the
+//            unit's smallest selectable key, 11 bits at a time from its highest set bit,
+//            each followed by a block scan; a chosen bin of <= 64 keys is ranked by one
+//            wave, exactly;
+//   compact  per-(chunk, wave) keep / tie counts, one exchange, then every thread
+//            writes its kept pages at their ranks (ascending page ids).
+// Large nrm units (MP G beyond the fused staging's registers) get a pre-pass over many
+// workgroups (nrm_pass_kernel) that writes the combined scores; the selection then reads
+// those.  Without per-tile maxima the standalone two-pass nrm_kernel does that.
+constexpr int XS_THREADS = 512;
+constexpr int XS_WAVES = XS_THREADS / WAVE;
+constexpr int XS_BITS = 11;                   // key bits per histogram digit
+constexpr int XS_BINS = 1 << XS_BITS;         // four bins per thread in the scan
+constexpr int XS_BPT = XS_BINS / XS_THREADS;
+constexpr int XS_CAND = WAVE;                 // a bin this small is ranked by one wave
+constexpr int XS_TILE = 16;                   // pages per per-tile maximum of score_h
+constexpr int XS_FUSED = 64;                  // PPT * G floats of the fused nrm staging
+constexpr int XS_MAXNC = 8;                   // chunks per thread at PPT = 32
+constexpr int NP_THREADS = 256;               // nrm pre-pass workgroup
+constexpr int NP_PAGES = 4 * NP_THREADS;      // pages per pre-pass workgroup
 
-struct __align__(16) SelShared {
-    unsigned int hcnt[2][256];           // double-buffered radix histograms
-    unsigned long long hmass[2][256];
-    unsigned int ckey[SEL_CAND];         // candidates: rel keys and masses
-    unsigned long long cmass[SEL_CAND];
+struct __align__(16) XSel {
+    unsigned long long hmass[XS_BINS];        // histogram: 2^-32 fixed-point masses
+    unsigned int hcnt[XS_BINS];               //            and counts
+    unsigned long long cmass[XS_CAND];        // candidates: masses and relative keys
+    unsigned int ckey[XS_CAND];
+    unsigned long long wm[XS_WAVES];          // bin scan: per-wave totals
+    unsigned int wc[XS_WAVES];
+    unsigned long long ured[2][XS_WAVES];     // total / sink mass
+    float hred[8][XS_WAVES];                  // per-head maxima
+    float fred[XS_WAVES];                     // score max
+    unsigned int kred[2][XS_WAVES];           // selectable key min / max
+    int ccnt[XS_MAXNC][XS_WAVES][2];          // compaction: sure-keep / tie counts
     int ncand;
-    unsigned int f_prefix;               // candidate finish result
-    int f_cab, f_ceq;
-    unsigned long long f_mab;
-    float hred[8][SEL_WAVES];            // nrm per-head maxima
-    float fred[SEL_WAVES];               // score max
-    unsigned int kred[2][SEL_WAVES];     // selectable key min / max
-    unsigned long long ured[2][SEL_WAVES];  // total / sink mass
-    int wred[2][SEL_WAVES];              // per-wave sure-keep / tie counts
-    unsigned int prefix, bin;            // radix state (written by the scanning lane)
-    int cnt_above;
+    unsigned int prefix, bin, bin_cnt;        // digit search: rel >> shift of the chosen bin
+    int cnt_above;                            // keys / mass strictly above the chosen bin
     unsigned long long mass_above;
+    unsigned int f_key;                       // candidate finish: tau's relative key,
+    int f_cab, f_ceq;                         // the keys above it, its tie count,
+    unsigned long long f_mab;                 // the mass above it
 };
 
-// Wave 0 scans the 256 bins of histogram `buf` from high to low and finds the bin holding
-// the target.  Count mode: first bin where cnt_above + cumulative count >= target; mass
-// mode likewise on mass.  The scanning lane appends the bin to the prefix (at `shift`) and
-// adds the bins strictly above to the running totals.
-__device__ void scan_bins(SelShared& s, int buf, bool by_mass, unsigned long long target,
-                          int shift) {
-    const int lane = threadIdx.x & 63;
-    // lane L owns bins 255-4L .. 252-4L (descending)
-    unsigned long long v[4];
-    unsigned int c[4];
+// V consecutive floats of src from page p: one vector load when the run is whole and
+// `vec` (16-byte aligned base, stride a multiple of 4 floats), else guarded scalar loads.
+template <int V>
+__device__ __forceinline__ void ld_pages(const float* __restrict__ src, int p, int n, bool vec,
+                                         float fill, float* o) {
+    if (vec && p + V <= n) {
+        if constexpr (V == 4) {
+            const float4 x = *reinterpret_cast<const float4*>(src + p);
+            o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+        } else if constexpr (V == 2) {
+            const float2 x = *reinterpret_cast<const float2*>(src + p);
+            o[0] = x.x; o[1] = x.y;
+        } else {
+            o[0] = src[p];
+        }
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int bin = 255 - 4 * lane - i;
-        c[i] = s.hcnt[buf][bin];
-        v[i] = by_mass ? s.hmass[buf][bin] : (unsigned long long)c[i];
+        for (int i = 0; i < V; ++i) o[i] = p + i < n ? src[p + i] : fill;
     }
-    unsigned long long own = v[0] + v[1] + v[2] + v[3];
-    unsigned int ownc = c[0] + c[1] + c[2] + c[3];
+}
+template <int V>
+__device__ __forceinline__ void st_pages(float* __restrict__ dst, int p, int n, bool vec,
+                                         const float* v) {
+    if (vec && p + V <= n) {
+        if constexpr (V == 4) {
+            *reinterpret_cast<float4*>(dst + p) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if constexpr (V == 2) {
+            *reinterpret_cast<float2*>(dst + p) = make_float2(v[0], v[1]);
+        } else {
+            dst[p] = v[0];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+            if (p + i < n) dst[p + i] = v[i];
+    }
+}
+
+// the nrm pages of a unit: min(n_sel_hi, n_pages, max_pages), >= 0
+__device__ __forceinline__ int scored_pages(const amass_select_args& a, int r) {
+    const int np = min(a.n_pages[r], a.max_pages);
+    const int ns = min(a.n_sel_hi[r], np);
+    return ns > 0 ? ns : 0;
+}
+
+// Per-head maxima over the block: wave reductions, one LDS exchange, one barrier.
+template <int WAVES>
+__device__ __forceinline__ void block_head_max(float* m, int G, float (*red)[WAVES]) {
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+        if (g < G) {
+            const float x = wave_maxf(m[g]);
+            if ((threadIdx.x & 63) == 0) red[g][w] = x;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+        if (g < G) {
+            float x = red[g][0];
+#pragma unroll
+            for (int i = 1; i < WAVES; ++i) x = fmaxf(x, red[g][i]);
+            m[g] = x;
+        }
+}
+
+// The nrm combine of NP_PAGES pages of one unit (workgroup (chunk, kv-head, request)):
+// score[p] = sum_{g ascending} exp(score_h[g][p] - hmax_g), hmax_g = the maximum of the
+// unit's per-tile maxima (the same maxima and sums as the fused staging).  The score_h
+// loads are issued before the maxima are read and reduced.
+__global__ __launch_bounds__(NP_THREADS) void nrm_pass_kernel(const amass_select_args a) {
+    constexpr int TPT = (SEL_MAXP / XS_TILE) / NP_THREADS;   // tile maxima per thread
+    __shared__ float red[8][NP_THREADS / WAVE];
+    const int chunk = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int tid = threadIdx.x, G = a.G, MP = a.max_pages;
+    const int p0 = chunk * NP_PAGES;
+    const float* sh = a.score_h + (int64_t)r * a.sh_sr + (int64_t)kh * a.sh_sh;
+    const float* tm = a.tile_max + (int64_t)r * a.tm_sr + (int64_t)kh * a.tm_sh;
+    float* gs = a.score + (int64_t)r * a.sc_sr + (int64_t)kh * a.sc_sh;
+    const bool vec = ((((uintptr_t)sh) | ((uintptr_t)gs)) & 15) == 0 && (a.sh_sg & 3) == 0;
+    // loads first: the row's pages and tile maxima are in bounds (rows are MP wide)
+    float v[8][4];                              // [head][page]: pages p0 + 4 tid + {0..3}
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+        if (g < G) ld_pages<4>(sh + g * a.sh_sg, p0 + 4 * tid, MP, vec, -INFINITY, v[g]);
+    const int ntm = (MP + XS_TILE - 1) / XS_TILE;
+    float tv[8][TPT];
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) {
+            const int t = tid + k * NP_THREADS;
+            tv[g][k] = (g < G && t < ntm) ? tm[g * a.tm_sg + t] : -INFINITY;
+        }
+    const int n = scored_pages(a, r);
+    if (p0 >= n) return;                        // uniform over the workgroup
+    const int nt = (n + XS_TILE - 1) / XS_TILE;
+    float m[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        m[g] = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < TPT; ++k)
+            if (tid + k * NP_THREADS < nt) m[g] = fmaxf(m[g], tv[g][k]);
+    }
+    block_head_max<NP_THREADS / WAVE>(m, G, red);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+        if (g < G)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += nrm_exp(v[g][i] - m[g]);
+    st_pages<4>(gs, p0 + 4 * tid, n, vec, acc);
+}
+
+// Block scan of the histogram from the highest bin down: the bin where the cumulative
+// weight (mass in coverage mode, else count) from the top, after what earlier digits put
+// above, reaches `target`.  Thread t owns bins XS_BINS-1-XS_BPT t .. down.  The thread
+// holding it appends the bin to the prefix (digit bits [shift, top)) and adds the bins
+// above it to the running total.  Two barriers.
+__device__ void xs_scan(XSel& s, bool by_mass, unsigned long long target, int shift, int top) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int b0 = XS_BINS - 1 - XS_BPT * tid;
+    unsigned long long m[XS_BPT];
+    unsigned long long own = 0;
+#pragma unroll
+    for (int i = 0; i < XS_BPT; ++i) {
+        m[i] = by_mass ? s.hmass[b0 - i] : (unsigned long long)s.hcnt[b0 - i];
+        own += m[i];
+    }
     unsigned long long incl = own;
-    unsigned int inclc = ownc;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
+    for (int o = 1; o < WAVE; o <<= 1) {
         const unsigned long long y = __shfl_up(incl, o, WAVE);
-        const unsigned int yc = __shfl_up(inclc, o, WAVE);
-        if (lane >= o) { incl += y; inclc += yc; }
+        if (lane >= o) incl += y;
     }
-    const unsigned long long excl = incl - own;
-    const unsigned int exclc = inclc - ownc;
-    const unsigned long long base = by_mass ? s.mass_above : (unsigned long long)s.cnt_above;
-    // first lane whose inclusive sum reaches the target
-    const bool hit = base + incl >= target;
-    const unsigned long long bal = __ballot(hit);
-    const int L = bal ? (__ffsll((long long)bal) - 1) : 63;
-    if (lane == L) {
-        unsigned long long cum = base + excl;
-        unsigned long long mab = s.mass_above + (by_mass ? excl : 0ull);
-        unsigned int cab = (unsigned int)s.cnt_above + exclc;
-        int pick = 3;
-        for (int i = 0; i < 4; ++i) {
-            if (cum + v[i] >= target || i == 3) { pick = i; break; }
-            cum += v[i];
-            cab += c[i];
-            mab += by_mass ? v[i] : 0ull;
-        }
-        // mass of bins above in count mode is not tracked (not needed)
-        const unsigned int bin = (unsigned int)(255 - 4 * L - pick);
-        s.bin = bin;
-        s.prefix |= bin << shift;
-        s.cnt_above = (int)cab;
-        s.mass_above = mab;
-    }
-}
-
-// sc[p4..p4+4) from LDS in one 128-bit read (p4 % 4 == 0; the LDS array is padded to a
-// multiple of 4 floats)
-__device__ __forceinline__ void ld4(const float* sc, int p4, float* v) {
-    const float4 x = *reinterpret_cast<const float4*>(sc + p4);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-}
-
-struct SelTrack {
-    int lo, hi;
-    float pmax;
-    unsigned int kmin, kmax;
-    __device__ void operator()(int p, float v) {
-        pmax = fmaxf(pmax, v);
-        if (p >= lo && p < hi) {
-            const unsigned int k = f2u(v);
-            kmin = min(kmin, k);
-            kmax = max(kmax, k);
+    if (lane == WAVE - 1) s.wm[wv] = incl;
+    const unsigned long long above0 = by_mass ? s.mass_above : (unsigned long long)s.cnt_above;
+    __syncthreads();
+    unsigned long long base = 0;
+#pragma unroll
+    for (int i = 0; i < XS_WAVES; ++i)
+        if (i < wv) base += s.wm[i];
+    unsigned long long wabove = above0 + base + incl - own;      // weight above bin b0
+    if (wabove < target && target <= wabove + own) {
+#pragma unroll
+        for (int i = 0; i < XS_BPT; ++i) {
+            if (wabove + m[i] >= target) {
+                const unsigned int bin = (unsigned int)(b0 - i);
+                s.bin = bin;
+                s.bin_cnt = by_mass ? 0u : (unsigned int)m[i];
+                if (by_mass) s.mass_above = wabove;
+                else s.cnt_above = (int)wabove;
+                s.prefix = (s.prefix << (top - shift)) | bin;
+                break;
+            }
+            wabove += m[i];
         }
     }
-};
+    __syncthreads();
+}
 
-__global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_args a) {
-    extern __shared__ __align__(16) float sc[];   // scores of this unit, [round4(max_pages)]
-    __shared__ SelShared s;
+template <int PPT, bool NRM>
+__global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_args a) {
+    constexpr int V = PPT < 4 ? PPT : 4;        // pages per run
+    constexpr int NC = PPT / V;                 // runs (chunks) per thread
+    constexpr int CSTEP = V * XS_THREADS;       // pages per chunk
+    __shared__ XSel s;
     const int kh = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int MP = a.max_pages;
+    float* gscore = a.score + (int64_t)r * a.sc_sr + (int64_t)kh * a.sc_sh;
+    auto page_of = [&](int c, int i) { return c * CSTEP + V * tid + i; };
+
+    // ---- stage: loads first (the row's MP pages), then the unit's geometry ---------------
+    float v[PPT];
+    float hv[NRM ? 8 : 1][NRM ? PPT : 1];
+    float m[8];
+    if constexpr (NRM) {
+        const float* sh = a.score_h + (int64_t)r * a.sh_sr + (int64_t)kh * a.sh_sh;
+        const bool vec = ((((uintptr_t)sh) | ((uintptr_t)gscore)) & 15) == 0 &&
+                         (a.sh_sg & 3) == 0;
+#pragma unroll
+        for (int g = 0; g < 8; ++g)
+            if (g < a.G) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    ld_pages<V>(sh + g * a.sh_sg, page_of(c, 0), MP, vec, -INFINITY,
+                                &hv[g][c * V]);
+            }
+    } else {
+        const bool vec = (((uintptr_t)gscore) & 15) == 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) ld_pages<V>(gscore, page_of(c, 0), MP, vec, 0.f, &v[c * V]);
+    }
+    // fused: tile t's maxima (tiles < ceil(MP / 16) <= XS_THREADS, in bounds), masked below
+    if constexpr (NRM) {
+        const float* tm = a.tile_max + (int64_t)r * a.tm_sr + (int64_t)kh * a.tm_sh;
+        const int ntm = (MP + XS_TILE - 1) / XS_TILE;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) m[g] = (g < a.G && tid < ntm) ? tm[g * a.tm_sg + tid] : -INFINITY;
+    }
     const int np = min(a.n_pages[r], MP);       // a row never exceeds its table width
     const int nsh = min(a.n_sel_hi[r], np);
     const int bfix = a.mode == 0 ? a.b_fix[r] : 0;
     const int sink = a.sink_pages;
-    int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kh * a.pt_sh;
-    float* gscore = a.score + (int64_t)r * a.sc_sr + (int64_t)kh * a.sc_sh;
     const int nsc = nsh > 0 ? nsh : 0;          // scored pages [0, nsc)
-
     const int S = nsh - sink;
     const bool keep_all = S <= 1;
-    const int lo = sink, hi = nsh;        // selectable [lo, hi) when !keep_all
+    const int lo = sink, hi = nsh;              // selectable [lo, hi) when !keep_all
+    int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kh * a.pt_sh;
 
-    for (int i = tid; i < 2 * 256; i += SEL_THREADS) {
-        (&s.hcnt[0][0])[i] = 0;
-        (&s.hmass[0][0])[i] = 0;
+    for (int i = tid; i < XS_BINS; i += XS_THREADS) {
+        s.hcnt[i] = 0;
+        s.hmass[i] = 0;
     }
-    if (tid == 0) { s.prefix = 0; s.cnt_above = 0; s.mass_above = 0; s.ncand = 0; }
+    if (tid == 0) {
+        s.prefix = 0;
+        s.bin = 0;
+        s.bin_cnt = 0;
+        s.cnt_above = 0;
+        s.mass_above = 0;
+        s.ncand = 0;
+    }
+    if constexpr (NRM) {
+        if (tid >= (nsc + XS_TILE - 1) / XS_TILE) {
+#pragma unroll
+            for (int g = 0; g < 8; ++g) m[g] = -INFINITY;
+        }
+        block_head_max<XS_WAVES>(m, a.G, s.hred);
+        const bool vec = (((uintptr_t)gscore) & 15) == 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                float acc = 0.f;
+#pragma unroll
+                for (int g = 0; g < 8; ++g)
+                    if (g < a.G) acc += nrm_exp(hv[g][c * V + i] - m[g]);
+                v[c * V + i] = acc;
+            }
+            st_pages<V>(gscore, page_of(c, 0), nsc, vec, &v[c * V]);
+        }
+    }
 
-    // ---- stage scores in LDS; track the score max and the selectable key range ---------
-    SelTrack tr{lo, hi, -INFINITY, 0xFFFFFFFFu, 0u};
-    if (a.score_h != nullptr) {
-        const float* sh = a.score_h + (int64_t)r * a.sh_sr + (int64_t)kh * a.sh_sh;
-        nrm_stage(sh, a.sh_sg, a.G, nsc, sc, gscore, s.hred, tr);
-    } else if ((((uintptr_t)gscore) & 15) == 0) {
-        copy_run<4, 2>(gscore, nsc, sc, tr);
-    } else {
-        copy_run<1, 4>(gscore, nsc, sc, tr);
-    }
+    // ---- score max and the selectable key range -------------------------------------------
     {
-        const float m = wave_maxf(tr.pmax);
-        const unsigned int k0 = wave_minu(tr.kmin), k1 = wave_maxu(tr.kmax);
-        if (lane == 0) { s.fred[wv] = m; s.kred[0][wv] = k0; s.kred[1][wv] = k1; }
+        float pmax = -INFINITY;
+        unsigned int kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+        for (int k = 0; k < PPT; ++k) {
+            const int p = page_of(k / V, k % V);
+            if (p < nsc) {
+                pmax = fmaxf(pmax, v[k]);
+                if (p >= lo && p < hi) {
+                    const unsigned int key = f2u(v[k]);
+                    kmin = min(kmin, key);
+                    kmax = max(kmax, key);
+                }
+            }
+        }
+        pmax = wave_maxf(pmax);
+        kmin = wave_minu(kmin);
+        kmax = wave_maxu(kmax);
+        if (lane == 0) { s.fred[wv] = pmax; s.kred[0][wv] = kmin; s.kred[1][wv] = kmax; }
     }
     __syncthreads();
     float bmax = s.fred[0];
     unsigned int kmin = s.kred[0][0], kmax = s.kred[1][0];
 #pragma unroll
-    for (int i = 1; i < SEL_WAVES; ++i) {
+    for (int i = 1; i < XS_WAVES; ++i) {
         bmax = fmaxf(bmax, s.fred[i]);
         kmin = min(kmin, s.kred[0][i]);
         kmax = max(kmax, s.kred[1][i]);
     }
 
-    // Radix digits are taken of rel = key - kmin (order-preserving on [lo, hi)), from its
-    // highest set bit down, so the first pass already spreads the unit over the bins.
+    // digits are taken of rel = key - kmin (order-preserving on [lo, hi)) from its
+    // highest set bit down, so the first histogram already spreads the unit over the bins
     const unsigned int range = kmax - kmin;
     const int nb = range ? 32 - __clz(range) : 1;
-    const int passes = (nb + 7) >> 3;
 
     bool coverage = a.mode == 1;
     int b = 0;
@@ -405,49 +586,39 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_
     unsigned int tau = 0;
     int take = 0;
 
+    if (!coverage) b = bfix < 1 ? 1 : (bfix > S ? S : bfix);
     if (!keep_all) {
-        // ---- pass-0 histogram (and, in coverage mode, the total / sink mass) ------------
-        const int sh0 = nb > 8 ? nb - 8 : 0;
-        if (coverage) {
+        const int shift = nb > XS_BITS ? nb - XS_BITS : 0;
+        // ---- first digit's histogram (and, in coverage mode, the total / sink mass) ----
+        // (top-b builds the count histogram; coverage its mass histogram and totals)
+        {
             unsigned long long tot = 0, snk = 0;
-            for (int p4 = 4 * tid; p4 < nsc; p4 += 4 * SEL_THREADS) {
-                float v[4];
-                ld4(sc, p4, v);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int p = p4 + j;
-                    if (p < nsc) {
-                        const unsigned long long w = mass_q(v[j], smax, a.score_kind);
+            for (int k = 0; k < PPT; ++k) {
+                const int p = page_of(k / V, k % V);
+                if (p < nsc) {
+                    const bool sel = p >= lo && p < hi;
+                    if (coverage) {
+                        const unsigned long long w = mass_q(v[k], smax, a.score_kind);
                         tot += w;
                         if (p < sink) snk += w;
-                        if (p >= lo && p < hi) {
-                            const unsigned int bin = ((f2u(v[j]) - kmin) >> sh0) & 255u;
-                            atomicAdd(&s.hcnt[0][bin], 1u);
-                            atomicAdd(&s.hmass[0][bin], w);
-                        }
+                        if (sel) atomicAdd(&s.hmass[(f2u(v[k]) - kmin) >> shift], w);
+                    } else if (sel && b != 1) {
+                        atomicAdd(&s.hcnt[(f2u(v[k]) - kmin) >> shift], 1u);
                     }
                 }
             }
-            tot = wave_sum_u64(tot);
-            snk = wave_sum_u64(snk);
-            if (lane == 0) { s.ured[0][wv] = tot; s.ured[1][wv] = snk; }
-        } else {
-            for (int p4 = (lo & ~3) + 4 * tid; p4 < hi; p4 += 4 * SEL_THREADS) {
-                float v[4];
-                ld4(sc, p4, v);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int p = p4 + j;
-                    if (p >= lo && p < hi)
-                        atomicAdd(&s.hcnt[0][((f2u(v[j]) - kmin) >> sh0) & 255u], 1u);
-                }
+            if (coverage) {
+                tot = wave_sum_u64(tot);
+                snk = wave_sum_u64(snk);
+                if (lane == 0) { s.ured[0][wv] = tot; s.ured[1][wv] = snk; }
             }
         }
         __syncthreads();
         if (coverage) {
             unsigned long long tot = 0, snk = 0;
 #pragma unroll
-            for (int i = 0; i < SEL_WAVES; ++i) { tot += s.ured[0][i]; snk += s.ured[1][i]; }
+            for (int i = 0; i < XS_WAVES; ++i) { tot += s.ured[0][i]; snk += s.ured[1][i]; }
             const double nd = ceil(a.coverage * (double)tot);
             const long long needs = (long long)nd - (long long)snk;
             if (needs <= 0) {          // sinks already cover: one selectable page
@@ -456,71 +627,31 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_
             } else {
                 need = (unsigned long long)needs;
             }
-        } else {
-            b = bfix < 1 ? 1 : (bfix > S ? S : bfix);
         }
+    }
+    if (!keep_all && !coverage && b == 1) {
+        // one page: tau = the largest selectable key, its lowest-index tie (or, for the
+        // threshold rule, all of them) -- no histogram needed
+        tau = kmax;
+        take = a.tie_mode == 1 ? 0x7FFFFFFF : 1;
+    } else if (!keep_all) {
+        int top = nb;
+        int shift = top > XS_BITS ? top - XS_BITS : 0;
 
-        // ---- radix select of tau: scan, then the next digit's histogram ----------------
-        int fshift = -1;                // >= 0: finish by candidates below this bit
-        for (int pass = 0; pass < passes; ++pass) {
-            const int top = nb - 8 * pass;             // digit = rel bits [shift, top)
-            const int shift = top > 8 ? top - 8 : 0;
-            const int buf = pass & 1;
-            if (pass > 0) {
+        // ---- digit search --------------------------------------------------------------
+        // After each scan the chosen bin's keys are gathered (the first XS_CAND kept, all
+        // counted); a bin of more keys takes the next 11 bits.  Top-b knows the bin's count
+        // from its histogram and skips the gather of a large bin.
+        for (;;) {
+            xs_scan(s, coverage, coverage ? need : (unsigned long long)b, shift, top);
+            const bool gather = shift == 0 || coverage || s.bin_cnt <= XS_CAND;
+            if (gather) {
                 const unsigned int pre = s.prefix;
-                const unsigned int pm = 0xFFFFFFFFu << top;   // top < 32 after pass 0
-                for (int p4 = (lo & ~3) + 4 * tid; p4 < hi; p4 += 4 * SEL_THREADS) {
-                    float v[4];
-                    ld4(sc, p4, v);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int p = p4 + j;
-                        const unsigned int rel = f2u(v[j]) - kmin;
-                        if (p >= lo && p < hi && (rel & pm) == pre) {
-                            const unsigned int bin = (rel >> shift) & 255u;
-                            atomicAdd(&s.hcnt[buf][bin], 1u);
-                            if (coverage)
-                                atomicAdd(&s.hmass[buf][bin], mass_q(v[j], smax, a.score_kind));
-                        }
-                    }
-                }
-                __syncthreads();
-            }
-            if (tid < WAVE) {
-                scan_bins(s, buf, coverage, coverage ? need : (unsigned long long)b, shift);
-            } else if (pass + 1 < passes && pass > 0) {
-                for (int i = tid - WAVE; i < 256; i += SEL_THREADS - WAVE) {
-                    s.hcnt[buf ^ 1][i] = 0;
-                    s.hmass[buf ^ 1][i] = 0;
-                }
-            }
-            __syncthreads();
-            if (pass + 1 < passes && (int)s.hcnt[buf][s.bin] <= SEL_CAND) {
-                fshift = shift;
-                break;
-            }
-        }
-        unsigned int tau_rel;
-        int count_eq, cab;
-        unsigned long long mab;
-        if (fshift >= 0) {
-            // ---- candidate finish: the keys of the chosen bin, ranked all-pairs ----------
-            const unsigned int pre = s.prefix;
-            const unsigned int pm = 0xFFFFFFFFu << fshift;
-            if (tid == 0) {            // defaults (replaced by the winner below)
-                s.f_prefix = pre;
-                s.f_cab = s.cnt_above;
-                s.f_mab = s.mass_above;
-                s.f_ceq = 0;
-            }
-            for (int p4 = (lo & ~3) + 4 * tid; p4 < hi; p4 += 4 * SEL_THREADS) {
-                float v[4];
-                ld4(sc, p4, v);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int p = p4 + j;
-                    const unsigned int rel = f2u(v[j]) - kmin;
-                    const bool in = p >= lo && p < hi && (rel & pm) == pre;
+                for (int k = 0; k < PPT; ++k) {
+                    const int p = page_of(k / V, k % V);
+                    const unsigned int rel = f2u(v[k]) - kmin;
+                    const bool in = p >= lo && p < hi && (rel >> shift) == pre;
                     const unsigned long long bal = __ballot(in);
                     if (bal) {
                         int base = 0;
@@ -528,36 +659,57 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_
                         base = __shfl(base, 0, WAVE);
                         if (in) {
                             const int idx = base + lanes_below(bal);
-                            s.ckey[idx] = rel;
-                            s.cmass[idx] = coverage ? mass_q(v[j], smax, a.score_kind) : 0ull;
+                            if (idx < XS_CAND) {
+                                s.ckey[idx] = rel;
+                                s.cmass[idx] = coverage ? mass_q(v[k], smax, a.score_kind) : 0ull;
+                            }
                         }
                     }
                 }
+                __syncthreads();
+                if (shift == 0 || s.ncand <= XS_CAND) break;
+            }
+            // the next 11 bits of the keys inside the chosen bin
+            for (int i = tid; i < XS_BINS; i += XS_THREADS) {
+                s.hcnt[i] = 0;
+                s.hmass[i] = 0;
             }
             __syncthreads();
-            const int c = s.ncand;
-            if (tid < c) {
-                const unsigned int kt = s.ckey[tid];
+            if (tid == 0) s.ncand = 0;          // every thread read it before the barrier
+            top = shift;
+            shift = top > XS_BITS ? top - XS_BITS : 0;
+            const unsigned int pre = s.prefix;
+#pragma unroll
+            for (int k = 0; k < PPT; ++k) {
+                const int p = page_of(k / V, k % V);
+                const unsigned int rel = f2u(v[k]) - kmin;
+                if (p >= lo && p < hi && (rel >> top) == pre) {
+                    const unsigned int bin = (rel >> shift) & (XS_BINS - 1);
+                    if (coverage) atomicAdd(&s.hmass[bin], mass_q(v[k], smax, a.score_kind));
+                    else atomicAdd(&s.hcnt[bin], 1u);
+                }
+            }
+            __syncthreads();
+        }
+        unsigned int tau_rel;
+        int count_eq, cab;                      // cab: keys above tau (top-b only)
+        unsigned long long mab;
+        if (shift > 0) {
+            // ---- the <= 64 candidates ranked exactly by wave 0 (register broadcasts) ------
+            if (wv == 0) {
+                const int c = min(s.ncand, XS_CAND);
+                const unsigned int kt = lane < c ? s.ckey[lane] : 0u;
+                const unsigned long long mt = lane < c ? s.cmass[lane] : 0ull;
+                const uint32_t mlo = (uint32_t)mt, mhi = (uint32_t)(mt >> 32);
                 unsigned int ab = 0, eq = 0;
                 unsigned long long am = 0, em = 0;
-                int j = 0;
-                for (; j + 4 <= c; j += 4) {
-                    const uint4 k4 = *reinterpret_cast<const uint4*>(&s.ckey[j]);
-                    const ulonglong2 m0 = *reinterpret_cast<const ulonglong2*>(&s.cmass[j]);
-                    const ulonglong2 m1 = *reinterpret_cast<const ulonglong2*>(&s.cmass[j + 2]);
-                    const unsigned int kk[4] = {k4.x, k4.y, k4.z, k4.w};
-                    const unsigned long long mm[4] = {m0.x, m0.y, m1.x, m1.y};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        ab += kk[i] > kt;
-                        eq += kk[i] == kt;
-                        am += kk[i] > kt ? mm[i] : 0ull;
-                        em += kk[i] == kt ? mm[i] : 0ull;
-                    }
-                }
-                for (; j < c; ++j) {
-                    const unsigned int kj = s.ckey[j];
-                    const unsigned long long mj = s.cmass[j];
+                for (int j = 0; j < c; ++j) {
+                    // readlane returns int: widen through uint32_t (no sign extension)
+                    const unsigned int kj = (uint32_t)__builtin_amdgcn_readlane((int)kt, j);
+                    const unsigned long long mj =
+                        ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)mhi, j)
+                         << 32) |
+                        (unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)mlo, j);
                     ab += kj > kt;
                     eq += kj == kt;
                     am += kj > kt ? mj : 0ull;
@@ -569,21 +721,27 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_
                     coverage ? s.mass_above + am : (unsigned long long)(s.cnt_above + (int)ab);
                 const unsigned long long own = coverage ? em : (unsigned long long)eq;
                 const unsigned long long target = coverage ? need : (unsigned long long)b;
-                if (above < target && target <= above + own) {   // all ties of kt agree
-                    s.f_prefix = kt;
-                    s.f_cab = s.cnt_above + (int)ab;
-                    s.f_mab = s.mass_above + am;
-                    s.f_ceq = (int)eq;
+                const bool win = lane < c && above < target && target <= above + own;
+                const unsigned long long wb = __ballot(win);
+                const int src = wb ? __ffsll((long long)wb) - 1 : 0;   // ties of kt agree
+                const unsigned int fk = __shfl(kt, src, WAVE);
+                const int feq = __shfl((int)eq, src, WAVE), fab = __shfl((int)ab, src, WAVE);
+                const unsigned long long fam = __shfl(am, src, WAVE);
+                if (lane == 0) {
+                    s.f_key = wb ? fk : s.prefix << shift;
+                    s.f_cab = s.cnt_above + (wb ? fab : 0);
+                    s.f_mab = s.mass_above + (wb ? fam : 0ull);
+                    s.f_ceq = wb ? feq : 0;
                 }
             }
             __syncthreads();
-            tau_rel = s.f_prefix;
+            tau_rel = s.f_key;
             count_eq = s.f_ceq;
             cab = s.f_cab;
             mab = s.f_mab;
         } else {
-            tau_rel = s.prefix;
-            count_eq = (int)s.hcnt[(passes - 1) & 1][s.bin];
+            tau_rel = s.prefix;                 // every bit resolved: one tie class
+            count_eq = s.ncand;
             cab = s.cnt_above;
             mab = s.mass_above;
         }
@@ -595,7 +753,6 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_
             if (t < 1) t = 1;
             if (t > count_eq) t = count_eq;
             take = (int)t;
-            b = cab + take;
         } else {
             take = b - cab;
         }
@@ -606,91 +763,100 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(const amass_select_
     // A page is a sure keep (outside the selectable region, key > tau, or for the
     // threshold rule score >= tau) or a tie (key == tau, index rule); ties are kept in page
     // order while their rank is < take, so pages kept before p = sure(<p) + min(ties(<p),
-    // take).  Wave w owns a run of 256-page blocks; lane l takes pages 4l..4l+3 of a block,
-    // and ballots per slot j give each lane the counts of the lanes below it.
-    const int n = np > 0 ? np : 0;
-    const int per = (((n + SEL_WAVES - 1) / SEL_WAVES) + 255) & ~255;
-    const int w0 = wv * per, w1 = min(n, w0 + per);
+    // take).  Page order is (chunk, thread, slot): per-(chunk, wave) counts, one
+    // exchange, then ballot prefixes inside the wave.
     const float ftau = u2f(tau);
-    auto classify = [&](int p4, bool* sure, bool* tie) {
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p4 < w1) ld4(sc, p4, v);           // w1 <= n <= max_pages: inside the array
+    uint32_t sure_m = 0, tie_m = 0;              // bit k: page slot k
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = p4 + j;
-            sure[j] = false;
-            tie[j] = false;
-            if (p >= w1) continue;
+    for (int k = 0; k < PPT; ++k) {
+        const int p = page_of(k / V, k % V);
+        bool su = false, ti = false;
+        if (p < np) {
             if (keep_all || p < lo || p >= hi) {
-                sure[j] = true;
+                su = true;
             } else if (a.tie_mode == 1) {
-                sure[j] = v[j] >= ftau;
+                su = v[k] >= ftau;
             } else {
-                const unsigned int k = f2u(v[j]);
-                sure[j] = k > tau;
-                tie[j] = k == tau;
+                const unsigned int key = f2u(v[k]);
+                su = key > tau;
+                ti = key == tau;
             }
         }
-    };
-    int sure_c = 0, tie_c = 0;
-    for (int b0 = w0; b0 < w1; b0 += 4 * WAVE) {
-        bool sure[4], tie[4];
-        classify(b0 + 4 * lane, sure, tie);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sure_c += __popcll(__ballot(sure[j]));
-            tie_c += __popcll(__ballot(tie[j]));
-        }
+        sure_m |= (uint32_t)su << k;
+        tie_m |= (uint32_t)ti << k;
     }
-    if (lane == 0) { s.wred[0][wv] = sure_c; s.wred[1][wv] = tie_c; }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int sc = 0, tc = 0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            sc += __popcll(__ballot((sure_m >> (c * V + i)) & 1u));
+            tc += __popcll(__ballot((tie_m >> (c * V + i)) & 1u));
+        }
+        if (lane == 0) { s.ccnt[c][wv][0] = sc; s.ccnt[c][wv][1] = tc; }
+    }
     __syncthreads();
-    int sure_base = 0, tie_base = 0, sure_tot = 0, tie_tot = 0;
+    int sure_tot = 0, tie_tot = 0;
 #pragma unroll
-    for (int i = 0; i < SEL_WAVES; ++i) {
-        const int x = s.wred[0][i], t = s.wred[1][i];
-        if (i < wv) { sure_base += x; tie_base += t; }
-        sure_tot += x;
-        tie_tot += t;
-    }
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int w = 0; w < XS_WAVES; ++w) {
+            sure_tot += s.ccnt[c][w][0];
+            tie_tot += s.ccnt[c][w][1];
+        }
     const int cnt = sure_tot + min(tie_tot, take);
-    int kp = sure_base + min(tie_base, take);
-    int rt = tie_base;
-    for (int b0 = w0; b0 < w1; b0 += 4 * WAVE) {
-        bool sure[4], tie[4], keep[4];
-        const int p4 = b0 + 4 * lane;
-        classify(p4, sure, tie);
-        int rk = rt, t_all = 0;                  // tie rank of this lane's next tie
+    int sure_base = 0, tie_base = 0;            // pages of (chunk, wave)s before this one
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const unsigned long long bt = __ballot(tie[j]);
-            rk += lanes_below(bt);
-            t_all += __popcll(bt);
+    for (int c = 0; c < NC; ++c) {
+        int sb = sure_base, tb = tie_base;
+#pragma unroll
+        for (int w = 0; w < XS_WAVES; ++w)
+            if (w < wv) {
+                sb += s.ccnt[c][w][0];
+                tb += s.ccnt[c][w][1];
+            }
+        int rk = tb;                             // tie rank of this lane's first tie
+#pragma unroll
+        for (int i = 0; i < V; ++i) rk += lanes_below(__ballot((tie_m >> (c * V + i)) & 1u));
+        bool keep[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) {            // lane-local ties in slot order
+            const bool ti = (tie_m >> (c * V + i)) & 1u;
+            keep[i] = ((sure_m >> (c * V + i)) & 1u) || (ti && rk < take);
+            rk += ti;
         }
+        int pos = sb + min(tb, take);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {            // lane-local ties in slot order
-            keep[j] = sure[j] || (tie[j] && rk < take);
-            rk += tie[j];
+        for (int i = 0; i < V; ++i) pos += lanes_below(__ballot(keep[i]));
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+            if (keep[i]) tab[pos++] = page_of(c, i);
+#pragma unroll
+        for (int w = 0; w < XS_WAVES; ++w) {
+            sure_base += s.ccnt[c][w][0];
+            tie_base += s.ccnt[c][w][1];
         }
-        int pos = kp, k_all = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const unsigned long long bk = __ballot(keep[j]);
-            pos += lanes_below(bk);
-            k_all += __popcll(bk);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (keep[j]) tab[pos++] = p4 + j;
-        rt += t_all;
-        kp += k_all;
     }
-    for (int p = cnt + tid; p < MP; p += SEL_THREADS) tab[p] = -1;
+    for (int p = cnt + tid; p < MP; p += XS_THREADS) tab[p] = -1;
     if (tid == 0) {
         a.page_cnt[(int64_t)r * a.pc_sr + kh] = cnt;
+        // selectable pages kept: every page outside [lo, hi) of the row is kept
         if (a.n_sel_out)
-            a.n_sel_out[(int64_t)r * a.n_kv + kh] =
-                keep_all ? (S > 0 ? S : 0) : (a.tie_mode == 1 ? cnt - (n - S) : b);
+            a.n_sel_out[(int64_t)r * a.n_kv + kh] = keep_all ? (S > 0 ? S : 0) : cnt - (np - S);
     }
+}
+
+template <int PPT>
+static void launch_select_ppt(const amass_select_args& k, bool fused, hipStream_t st) {
+    if constexpr (PPT <= 8) {
+        if (fused) {
+            hipLaunchKernelGGL((select_kernel<PPT, true>), dim3(k.n_kv, k.n_req),
+                               dim3(XS_THREADS), 0, st, k);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((select_kernel<PPT, false>), dim3(k.n_kv, k.n_req), dim3(XS_THREADS),
+                       0, st, k);
 }
 
 }  // namespace amass
@@ -728,6 +894,7 @@ static int select_common(const amass_select_args* a, int mode, void* stream) {
     if (mode == 0 && !a->b_fix) return AMASS_ERR_NULL;
     if (a->n_kv < 1 || a->max_pages < 1 || a->sink_pages < 0) return AMASS_ERR_GEOMETRY;
     if (a->score_h && (a->G < 1 || a->G > 8)) return AMASS_ERR_GEOMETRY;
+    if (a->tile_max && !a->score_h) return AMASS_ERR_GEOMETRY;
     if (a->max_pages > SEL_MAXP) return AMASS_ERR_CAPACITY;
     if (a->tie_mode != 0 && a->tie_mode != 1) return AMASS_ERR_GEOMETRY;
     if (a->score_kind != 0 && a->score_kind != 1) return AMASS_ERR_GEOMETRY;
@@ -735,9 +902,39 @@ static int select_common(const amass_select_args* a, int mode, void* stream) {
     if (a->n_req == 0) return AMASS_OK;
     amass_select_args k = *a;
     k.mode = mode;
-    const size_t lds = (size_t)((a->max_pages + 3) & ~3) * sizeof(float);
-    hipLaunchKernelGGL(select_kernel, dim3(a->n_kv, a->n_req), dim3(SEL_THREADS), lds,
-                       (hipStream_t)stream, k);
+    hipStream_t st = (hipStream_t)stream;
+    int ppt = 1;
+    while (ppt * XS_THREADS < k.max_pages) ppt *= 2;           // <= 32 (SEL_MAXP)
+    bool fused = false;
+    if (k.score_h) {
+        fused = k.tile_max && ppt <= 8 && ppt * k.G <= XS_FUSED;
+        if (!fused) {
+            // the combined scores first (many workgroups with the per-tile maxima, else
+            // the standalone two-pass combine), then the selection over st.score
+            if (k.tile_max) {
+                const int chunks = (k.max_pages + NP_PAGES - 1) / NP_PAGES;
+                hipLaunchKernelGGL(nrm_pass_kernel, dim3(chunks, k.n_kv, k.n_req),
+                                   dim3(NP_THREADS), 0, st, k);
+            } else {
+                amass_nrm_args na;
+                na.score_h = k.score_h; na.sh_sr = k.sh_sr; na.sh_sh = k.sh_sh; na.sh_sg = k.sh_sg;
+                na.score = k.score; na.sc_sr = k.sc_sr; na.sc_sh = k.sc_sh;
+                na.n_sel_hi = k.n_sel_hi;
+                na.n_req = k.n_req; na.n_kv = k.n_kv; na.G = k.G; na.max_pages = k.max_pages;
+                hipLaunchKernelGGL(nrm_kernel, dim3(k.n_kv, k.n_req), dim3(SEL_THREADS), 0, st, na);
+            }
+            const int rc = check_launch();
+            if (rc) return rc;
+        }
+    }
+    switch (ppt) {
+        case 1: launch_select_ppt<1>(k, fused, st); break;
+        case 2: launch_select_ppt<2>(k, fused, st); break;
+        case 4: launch_select_ppt<4>(k, fused, st); break;
+        case 8: launch_select_ppt<8>(k, fused, st); break;
+        case 16: launch_select_ppt<16>(k, fused, st); break;
+        default: launch_select_ppt<32>(k, fused, st); break;
+    }
     return check_launch();
 }
 

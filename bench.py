@@ -347,7 +347,8 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     k_steps = max(5, args.steps // 5)
     g_score = graph_of(score_only, reps)
     us_score = time_graph(g_score, k_steps, 2, reps) * 1e3
-    g_sel = graph_of(lambda: select_pages(st, B, score_h=st.score_h if nrm else None), reps)
+    g_sel = graph_of(lambda: select_pages(st, B, score_h=st.score_h if nrm else None,
+                                          tile_max=st.score_tmax if nrm else None), reps)
     us_sel = time_graph(g_sel, k_steps, 2, reps) * 1e3
     g_att = graph_of(lambda: sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc,
                                                           scale=case.scale), reps)

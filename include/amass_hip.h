@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 6
+#define AMASS_ABI_VERSION 7
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -55,7 +55,10 @@ extern "C" {
  *   head h at n_kv*VM+64h:  fp16 V_scale[0..r') at half 0, sig2[0..r') at half 8,
  *                           mu_scale at half 16, the rest zero
  * rec points at block 0 of the layer, rec_sb is the block stride in bytes (at least
- * n_kv * AMASS_QUAD_REC_BYTES, a multiple of 16).  n_kv <= 8 or a multiple of 8. */
+ * n_kv * AMASS_QUAD_REC_BYTES, a multiple of 16).  n_kv <= 8 or a multiple of 8.
+ * tile_max (combine 1, optional): tile_max[r,kh,g,t] = max of S_g over the scored pages
+ * of tile t (pages 16t .. 16t+15), t < ceil(n_sel_hi / 16), (R,n_kv,G,ceil(MP/16)) fp32;
+ * the per-head maxima the nrm combine needs, so the selection reads score_h once. */
 #define AMASS_QUAD_REC_BYTES(rank, v_bits) ((rank) * ((v_bits) == 8 ? 128 : 64) + 192)
 typedef struct amass_quad_score_args {
     const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
@@ -64,6 +67,7 @@ typedef struct amass_quad_score_args {
     const int32_t* n_sel_hi;                         /* (R,) int32                      */
     float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32 (combine 0)    */
     float*         score_h;  int64_t sh_sr, sh_sh, sh_sg; /* (R,n_kv,G,MP) (combine 1)  */
+    float*         tile_max; int64_t tm_sr, tm_sh, tm_sg; /* optional (combine 1), see above */
     int32_t*       comb_out; /* optional (R,n_kv,MP,G,r'+1) exact int32 sums; NULL = off */
     float          scale;    /* s = 1/sqrt(d) */
     int32_t n_req, n_kv, G, d, page, rank, v_bits, max_pages, combine;
@@ -155,6 +159,7 @@ typedef struct amass_clse_score_args {
     const int32_t* n_sel_hi;                         /* (R,) int32                      */
     float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32, combine 0     */
     float*         score_h;  int64_t sh_sr, sh_sh, sh_sg; /* (R,n_kv,G,MP), combine 1  */
+    float*         tile_max; int64_t tm_sr, tm_sh, tm_sg; /* optional, as for quad      */
     int32_t*       comb_out; /* optional (R,n_kv,MP,G,r+1) exact int32 sums; NULL = off */
     float          scale;
     int32_t n_req, n_kv, G, d, page, rank, v_bits, c_bits, max_pages, combine;
@@ -200,10 +205,13 @@ int amass_nrm_combine(const amass_nrm_args* a, void* stream);
  *                      sink mass; b = fewest top pages whose mass reaches need (>= 1).
  *   tie_mode 0: exactly b pages, ties at the b-th score broken to the lower page index.
  *   tie_mode 1: keep every page with score >= the b-th score (reference threshold rule).
- * If score_h != NULL the nrm combine runs first and writes its result into score. */
+ * If score_h != NULL the nrm combine runs first and writes its result into score; its
+ * per-head maxima come from tile_max when given (the per-tile maxima the score launch
+ * that wrote score_h produced), else from a pass over score_h. */
 typedef struct amass_select_args {
     float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) in (or out if nrm)  */
     const float*   score_h;  int64_t sh_sr, sh_sh, sh_sg; /* optional nrm input          */
+    const float*   tile_max; int64_t tm_sr, tm_sh, tm_sg; /* optional with score_h       */
     const int32_t* n_pages;
     const int32_t* n_sel_hi;
     const int32_t* b_fix;

@@ -179,3 +179,50 @@ def test_config0_known_answer():
     derive_page_params(st, torch.tensor([4096], dtype=torch.int32, device=DEV), 1)
     torch.cuda.synchronize()
     assert int(st.n_pages[0]) == 256 and int(st.n_sel_hi[0]) == 255 and int(st.b_fix[0]) == 13
+
+
+@pytest.mark.parametrize("G,coords", [(4, "none"), (8, "none"), (4, "lse")])
+def test_tile_maxima_equal_the_max_pass(G, coords):
+    """The score launch's per-16-page-tile per-head maxima (st.score_tmax) are the exact
+    maxima of score_h over each tile's scored pages (ragged lengths: partial last tiles),
+    and the selection that takes its per-head maxima from them writes the same scores
+    and page tables, bit for bit, as the one that takes them with a pass over score_h."""
+    announce(f"tile maxima G={G} coords={coords}")
+    from amass.bench.synth import build_quad_state, make_case
+    from amass.selection.quad_score import clse_score, quad_score_launch
+    R = 5
+    case = make_case(B=R, ctx=(900, 9000), n_kv=8, G=G, heavy=0.05, table="perm",
+                     seed=90 + G, device=DEV)
+    st = build_quad_state(case, rank=2, v_bits=8, combine="nrm", coverage=0.95,
+                          coords=coords, c_bits=4)
+    derive_page_params(st, case.seq_lens, R)
+    st.score_tmax.fill_(float("nan"))
+    if coords == "lse":
+        clse_score(st, 0, case.q, case.block_table, case.seq_lens, R, case.scale)
+    else:
+        quad_score_launch(st, 0, case.q, case.block_table, R, case.scale)
+    torch.cuda.synchronize()
+    nsh = npi(st.n_sel_hi)
+    sh, tm = npf(st.score_h), npf(st.score_tmax)
+    for r in range(R):
+        n = int(nsh[r])
+        nt = (n + 15) // 16
+        pad = np.full((8, G, nt * 16), -np.inf, np.float32)
+        pad[..., :n] = sh[r, :, :, :n]
+        want = pad.reshape(8, G, nt, 16).max(axis=-1)
+        assert np.array_equal(tm[r, :, :, :nt], want), r
+    outs = []
+    for tmax in (st.score_tmax, None):
+        st.score.fill_(0)
+        st.page_table.fill_(-7)
+        select_pages(st, R, score_h=st.score_h, tile_max=tmax)
+        torch.cuda.synchronize()
+        outs.append((npf(st.score), npi(st.page_table), npi(st.page_cnt)))
+    for r in range(R):
+        n = int(nsh[r])
+        assert np.array_equal(outs[0][0][r, :, :n].view(np.uint32),
+                              outs[1][0][r, :, :n].view(np.uint32))
+    assert np.array_equal(outs[0][1], outs[1][1]) and np.array_equal(outs[0][2], outs[1][2])
+    tab, cnt, _ = osel.select(outs[0][0], npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                              max_pages=st.max_pages, mode=1, coverage=0.95, score_kind=1)
+    assert np.array_equal(outs[0][1], tab) and np.array_equal(outs[0][2], cnt)
