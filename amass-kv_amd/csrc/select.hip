@@ -1,6 +1,6 @@
 // Stage-A selection for gfx950: derive params, nrm combine, top-b / coverage nucleus.
 //
-// One workgroup (512 threads, 8 waves) per (request, kv-head), the unit's pages held in
+// One workgroup (512 or 1024 threads) per (request, kv-head), the unit's pages held in
 // registers.  The b-th largest score is found by an MSD digit search over order-preserving
 // uint32 keys (2048-bin LDS histograms of 11 key bits; in coverage mode each bin also
 // accumulates the 2^-32 fixed-point page mass with 64-bit LDS atomics, so the cut is
@@ -248,8 +248,8 @@ __global__ __launch_bounds__(SEL_THREADS) void nrm_kernel(const amass_nrm_args a
 }
 
 // ------------------------------------------------------------------ selection
-// One workgroup of XS_THREADS per (request, kv-head); thread t holds pages
-// c * V * XS_THREADS + V t + i (chunk c < NC, i < V, V * NC = PPT pages per thread) in
+// One workgroup of NT threads per (request, kv-head) (512; 1024 for units of 4097 to 8192
+// pages); thread t holds pages c * V * NT + V t + i (chunk c < NC, i < V, V * NC = PPT) in
 // registers from the first load to the page-table write, so every phase reads registers
 // and LDS carries only the histogram and small exchanges.  Phases:
 //   stage    plain scores, or the fused nrm combine over score_h with the per-head maxima
@@ -265,11 +265,11 @@ __global__ __launch_bounds__(SEL_THREADS) void nrm_kernel(const amass_nrm_args a
 // Large nrm units (MP G beyond the fused staging's registers) get a pre-pass over many
 // workgroups (nrm_pass_kernel) that writes the combined scores; the selection then reads
 // those.  Without per-tile maxima the standalone two-pass nrm_kernel does that.
-constexpr int XS_THREADS = 512;
-constexpr int XS_WAVES = XS_THREADS / WAVE;
+constexpr int XS_THREADS = 512;              // units up to 4096 pages (and above 8192)
+constexpr int XS_THREADS_L = 1024;            // units of 4097 .. 8192 pages
+constexpr int XS_WAVES = XS_THREADS_L / WAVE; // exchange arrays sized for the larger block
 constexpr int XS_BITS = 11;                   // key bits per histogram digit
 constexpr int XS_BINS = 1 << XS_BITS;         // four bins per thread in the scan
-constexpr int XS_BPT = XS_BINS / XS_THREADS;
 constexpr int XS_CAND = WAVE;                 // a bin this small is ranked by one wave
 constexpr int XS_TILE = 16;                   // pages per per-tile maximum of score_h
 constexpr int XS_FUSED = 64;                  // PPT * G floats of the fused nrm staging
@@ -344,8 +344,8 @@ __device__ __forceinline__ int scored_pages(const amass_select_args& a, int r) {
 }
 
 // Per-head maxima over the block: wave reductions, one LDS exchange, one barrier.
-template <int WAVES>
-__device__ __forceinline__ void block_head_max(float* m, int G, float (*red)[WAVES]) {
+template <int WAVES, int CAP>
+__device__ __forceinline__ void block_head_max(float* m, int G, float (*red)[CAP]) {
     const int w = threadIdx.x >> 6;
 #pragma unroll
     for (int g = 0; g < 8; ++g)
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(NP_THREADS) void nrm_pass_kernel(const amass_select
         for (int k = 0; k < TPT; ++k)
             if (tid + k * NP_THREADS < nt) m[g] = fmaxf(m[g], tv[g][k]);
     }
-    block_head_max<NP_THREADS / WAVE>(m, G, red);
+    block_head_max<NP_THREADS / WAVE, NP_THREADS / WAVE>(m, G, red);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < 8; ++g)
@@ -418,7 +418,10 @@ __global__ __launch_bounds__(NP_THREADS) void nrm_pass_kernel(const amass_select
 // above, reaches `target`.  Thread t owns bins XS_BINS-1-XS_BPT t .. down.  The thread
 // holding it appends the bin to the prefix (digit bits [shift, top)) and adds the bins
 // above it to the running total.  Two barriers.
+template <int NT>
 __device__ void xs_scan(XSel& s, bool by_mass, unsigned long long target, int shift, int top) {
+    constexpr int XS_BPT = XS_BINS / NT;
+    constexpr int NW = NT / WAVE;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int b0 = XS_BINS - 1 - XS_BPT * tid;
     unsigned long long m[XS_BPT];
@@ -439,7 +442,7 @@ __device__ void xs_scan(XSel& s, bool by_mass, unsigned long long target, int sh
     __syncthreads();
     unsigned long long base = 0;
 #pragma unroll
-    for (int i = 0; i < XS_WAVES; ++i)
+    for (int i = 0; i < NW; ++i)
         if (i < wv) base += s.wm[i];
     unsigned long long wabove = above0 + base + incl - own;      // weight above bin b0
     if (wabove < target && target <= wabove + own) {
@@ -460,11 +463,12 @@ __device__ void xs_scan(XSel& s, bool by_mass, unsigned long long target, int sh
     __syncthreads();
 }
 
-template <int PPT, bool NRM>
-__global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_args a) {
+template <int NT, int PPT, bool NRM>
+__global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
+    constexpr int NW = NT / WAVE;
     constexpr int V = PPT < 4 ? PPT : 4;        // pages per run
     constexpr int NC = PPT / V;                 // runs (chunks) per thread
-    constexpr int CSTEP = V * XS_THREADS;       // pages per chunk
+    constexpr int CSTEP = V * NT;               // pages per chunk
     __shared__ XSel s;
     const int kh = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -493,7 +497,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
 #pragma unroll
         for (int c = 0; c < NC; ++c) ld_pages<V>(gscore, page_of(c, 0), MP, vec, 0.f, &v[c * V]);
     }
-    // fused: tile t's maxima (tiles < ceil(MP / 16) <= XS_THREADS, in bounds), masked below
+    // fused: tile t's maxima (tiles < ceil(MP / 16) <= NT, in bounds), masked below
     if constexpr (NRM) {
         const float* tm = a.tile_max + (int64_t)r * a.tm_sr + (int64_t)kh * a.tm_sh;
         const int ntm = (MP + XS_TILE - 1) / XS_TILE;
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
     const int lo = sink, hi = nsh;              // selectable [lo, hi) when !keep_all
     int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kh * a.pt_sh;
 
-    for (int i = tid; i < XS_BINS; i += XS_THREADS) {
+    for (int i = tid; i < XS_BINS; i += NT) {
         s.hcnt[i] = 0;
         s.hmass[i] = 0;
     }
@@ -527,7 +531,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
 #pragma unroll
             for (int g = 0; g < 8; ++g) m[g] = -INFINITY;
         }
-        block_head_max<XS_WAVES>(m, a.G, s.hred);
+        block_head_max<NW, XS_WAVES>(m, a.G, s.hred);
         const bool vec = (((uintptr_t)gscore) & 15) == 0;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -568,7 +572,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
     float bmax = s.fred[0];
     unsigned int kmin = s.kred[0][0], kmax = s.kred[1][0];
 #pragma unroll
-    for (int i = 1; i < XS_WAVES; ++i) {
+    for (int i = 1; i < NW; ++i) {
         bmax = fmaxf(bmax, s.fred[i]);
         kmin = min(kmin, s.kred[0][i]);
         kmax = max(kmax, s.kred[1][i]);
@@ -618,7 +622,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
         if (coverage) {
             unsigned long long tot = 0, snk = 0;
 #pragma unroll
-            for (int i = 0; i < XS_WAVES; ++i) { tot += s.ured[0][i]; snk += s.ured[1][i]; }
+            for (int i = 0; i < NW; ++i) { tot += s.ured[0][i]; snk += s.ured[1][i]; }
             const double nd = ceil(a.coverage * (double)tot);
             const long long needs = (long long)nd - (long long)snk;
             if (needs <= 0) {          // sinks already cover: one selectable page
@@ -643,7 +647,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
         // counted); a bin of more keys takes the next 11 bits.  Top-b knows the bin's count
         // from its histogram and skips the gather of a large bin.
         for (;;) {
-            xs_scan(s, coverage, coverage ? need : (unsigned long long)b, shift, top);
+            xs_scan<NT>(s, coverage, coverage ? need : (unsigned long long)b, shift, top);
             const bool gather = shift == 0 || coverage || s.bin_cnt <= XS_CAND;
             if (gather) {
                 const unsigned int pre = s.prefix;
@@ -670,7 +674,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
                 if (shift == 0 || s.ncand <= XS_CAND) break;
             }
             // the next 11 bits of the keys inside the chosen bin
-            for (int i = tid; i < XS_BINS; i += XS_THREADS) {
+            for (int i = tid; i < XS_BINS; i += NT) {
                 s.hcnt[i] = 0;
                 s.hmass[i] = 0;
             }
@@ -800,7 +804,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int w = 0; w < XS_WAVES; ++w) {
+        for (int w = 0; w < NW; ++w) {
             sure_tot += s.ccnt[c][w][0];
             tie_tot += s.ccnt[c][w][1];
         }
@@ -810,7 +814,7 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
     for (int c = 0; c < NC; ++c) {
         int sb = sure_base, tb = tie_base;
 #pragma unroll
-        for (int w = 0; w < XS_WAVES; ++w)
+        for (int w = 0; w < NW; ++w)
             if (w < wv) {
                 sb += s.ccnt[c][w][0];
                 tb += s.ccnt[c][w][1];
@@ -832,12 +836,12 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
         for (int i = 0; i < V; ++i)
             if (keep[i]) tab[pos++] = page_of(c, i);
 #pragma unroll
-        for (int w = 0; w < XS_WAVES; ++w) {
+        for (int w = 0; w < NW; ++w) {
             sure_base += s.ccnt[c][w][0];
             tie_base += s.ccnt[c][w][1];
         }
     }
-    for (int p = cnt + tid; p < MP; p += XS_THREADS) tab[p] = -1;
+    for (int p = cnt + tid; p < MP; p += NT) tab[p] = -1;
     if (tid == 0) {
         a.page_cnt[(int64_t)r * a.pc_sr + kh] = cnt;
         // selectable pages kept: every page outside [lo, hi) of the row is kept
@@ -846,17 +850,17 @@ __global__ __launch_bounds__(XS_THREADS) void select_kernel(const amass_select_a
     }
 }
 
-template <int PPT>
-static void launch_select_ppt(const amass_select_args& k, bool fused, hipStream_t st) {
-    if constexpr (PPT <= 8) {
+template <int NT, int PPT>
+static void launch_select(const amass_select_args& k, bool fused, hipStream_t st) {
+    if constexpr (NT == XS_THREADS && PPT <= 8) {
         if (fused) {
-            hipLaunchKernelGGL((select_kernel<PPT, true>), dim3(k.n_kv, k.n_req),
-                               dim3(XS_THREADS), 0, st, k);
+            hipLaunchKernelGGL((select_kernel<NT, PPT, true>), dim3(k.n_kv, k.n_req), dim3(NT),
+                               0, st, k);
             return;
         }
     }
-    hipLaunchKernelGGL((select_kernel<PPT, false>), dim3(k.n_kv, k.n_req), dim3(XS_THREADS),
-                       0, st, k);
+    hipLaunchKernelGGL((select_kernel<NT, PPT, false>), dim3(k.n_kv, k.n_req), dim3(NT), 0,
+                       st, k);
 }
 
 }  // namespace amass
@@ -927,13 +931,15 @@ static int select_common(const amass_select_args* a, int mode, void* stream) {
             if (rc) return rc;
         }
     }
+    // 512 threads up to 4096 pages (1..8 per thread) and beyond 8192 (32), 1024 threads
+    // for 4097 .. 8192 pages (8 per thread)
     switch (ppt) {
-        case 1: launch_select_ppt<1>(k, fused, st); break;
-        case 2: launch_select_ppt<2>(k, fused, st); break;
-        case 4: launch_select_ppt<4>(k, fused, st); break;
-        case 8: launch_select_ppt<8>(k, fused, st); break;
-        case 16: launch_select_ppt<16>(k, fused, st); break;
-        default: launch_select_ppt<32>(k, fused, st); break;
+        case 1: launch_select<XS_THREADS, 1>(k, fused, st); break;
+        case 2: launch_select<XS_THREADS, 2>(k, fused, st); break;
+        case 4: launch_select<XS_THREADS, 4>(k, fused, st); break;
+        case 8: launch_select<XS_THREADS, 8>(k, fused, st); break;
+        case 16: launch_select<XS_THREADS_L, 8>(k, fused, st); break;
+        default: launch_select<XS_THREADS, 32>(k, fused, st); break;
     }
     return check_launch();
 }
