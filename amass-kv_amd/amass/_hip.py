@@ -18,7 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
-ABI_VERSION = 7     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
+ABI_VERSION = 8     # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):
@@ -48,7 +48,7 @@ class R8ScoreArgs(C.Structure):
     _fields_ = _fields(
         "q:p q_st:i64 q_hs:i64 rec:p rec_sb:i64 block_table:p bt_st:i64 seq_lens:p "
         "n_sel_hi:p score:p sc_sr:i64 sc_sh:i64 comb_out:p scale:f32 n_req:i32 n_kv:i32 "
-        "G:i32 d:i32 page:i32 rank:i32 vk_bits:i32 c_bits:i32 max_pages:i32")
+        "G:i32 d:i32 page:i32 rank:i32 vk_bits:i32 c_bits:i32 max_pages:i32 c_fp32:i32")
 
 
 class ClseScoreArgs(C.Structure):

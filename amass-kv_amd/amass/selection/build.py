@@ -68,6 +68,9 @@ def _quant_c(c, grain: str = "page", bits: int = 8):
     if grain == "page":
         code, s = _quant(c, dim=-1, bits=bits)
         sc = s.squeeze(-1).to(torch.float16)
+    elif grain == "page_f32":                # one fp32 scale per page (not rounded)
+        code, s = _quant(c, dim=(-2, -1), bits=bits)
+        sc = s[..., 0, 0].float()
     else:
         code, s = _quant(c, dim=(-2, -1), bits=bits)
         sc = s.squeeze(-1).expand(*c.shape[:-2], c.shape[-2]).contiguous().to(torch.float16)
@@ -129,7 +132,10 @@ def r8_write(st, Kp_flat: torch.Tensor, layer: int, blocks: torch.Tensor) -> Non
     st.r8_Vk[layer, blocks] = v_to_device(vk_code, st.vk_bits, tiled=True)
     st.Vk_scale[layer, blocks] = vk_s
     st.r8_c[layer, blocks] = c_code
-    st.c_scale[layer, blocks] = c_s
+    if st.c_grain == "page_f32":
+        st.c_scale_f32[layer, blocks] = c_s
+    else:
+        st.c_scale[layer, blocks] = c_s
     st.r8_tag[layer, blocks] = Kp_flat[:, st.page - 1, :, :st.tagw].to(st.r8_tag.dtype)
 
 
@@ -168,15 +174,17 @@ def summary_build_hip(st, layer, K, blocks: torch.Tensor) -> None:
     clse = not r8 and getattr(st, "coords", "none") == "lse"
     v_bits = st.vk_bits if r8 else st.v_bits
     v_grain = (st.vk_grain if r8 else st.v_grain) == "tensor"
-    # one c scale per (block, head): r8 c_grain "tensor", CLSE c_grain "page"
+    # c scales: per token (0), one fp16 per (block, head) (1: r8 "tensor", CLSE "page"),
+    # one fp32 per (block, head) (2: r8 "page_f32")
     c_head = (r8 and st.c_grain == "tensor") or (clse and st.c_grain == "page")
+    c_grain = 2 if (r8 and st.c_grain == "page_f32") else int(c_head)
     a = BuildArgs(
         k=ptr(K0), k_sb=K0.stride(0), k_st=K0.stride(1), k_sh=K0.stride(2), k_layers=ptr(kl),
         blocks=ptr(blocks), rec=ptr(rec), rec_sb=rec.stride(0), rec_lsb=rec_all.stride(0),
         tag=ptr(tag), tag_sb=tag.stride(0), tag_sh=tag.stride(1), tag_lsb=tag_all.stride(0),
         n=int(blocks.numel()), n_layers=nl, n_kv=st.n_kv, d=st.d, page=st.page,
         kind=1 if r8 else (2 if clse else 0), rank=st.r, v_bits=v_bits,
-        c_bits=st.c_bits if (r8 or clse) else 8, v_grain=int(v_grain), c_grain=int(c_head),
+        c_bits=st.c_bits if (r8 or clse) else 8, v_grain=int(v_grain), c_grain=c_grain,
         tagw=st.tagw)
     call("amass_summary_build", a, current_stream(K0.device))
 

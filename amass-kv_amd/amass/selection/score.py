@@ -38,5 +38,6 @@ def r8_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
         score=ptr(st.score), sc_sr=st.score.stride(0), sc_sh=st.score.stride(1),
         comb_out=ptr(comb_out), scale=float(scale),
         n_req=n_req, n_kv=st.n_kv, G=st.G, d=st.d, page=st.page, rank=st.r,
-        vk_bits=st.vk_bits, c_bits=st.c_bits, max_pages=st.max_pages)
+        vk_bits=st.vk_bits, c_bits=st.c_bits, max_pages=st.max_pages,
+        c_fp32=1 if getattr(st, "c_grain", "page") == "page_f32" else 0)
     call("amass_r8_score", a, current_stream(q.device))

@@ -18,7 +18,9 @@ per kv head:
                low nibble = even column, as in the reference)
     then n_kv scale blocks of 64 bytes (fp16 halves), head h at n_kv * VM + 64 h:
       Vk_scale (L, NB, n_kv, r)       half 0..r-1
-      c_scale  (L, NB, n_kv, page)    half 8..23
+      c_scale  (L, NB, n_kv, page)    half 8..23 (c_grain "page" / "tensor")
+      c_scale_f32 (L, NB, n_kv)       fp32 at bytes 16..19 (c_grain "page_f32": one fp32 c
+               scale per page, BASELINE's per-page fp32 scale; halves 10..23 zero)
       mu_scale (L, NB, n_kv)          half 24; the other halves are zero
   r8_tag   (L, NB, n_kv, TAGW)  bf16  NaN-init content tag (separate)
 
@@ -48,7 +50,7 @@ class R8State:
         if window_pages < 1:
             raise ValueError("window_pages must be >= 1 (the partial tail lives in the "
                              "always-attended window)")
-        if vk_grain not in ("col", "tensor") or c_grain not in ("page", "tensor"):
+        if vk_grain not in ("col", "tensor") or c_grain not in ("page", "tensor", "page_f32"):
             raise ValueError(f"bad grain vk={vk_grain!r} c={c_grain!r}")
         if vk_bits not in (4, 8) or c_bits not in (4, 8) or mu_bits != 8:
             raise ValueError("Vk/c codes are int4 or int8; mu stays int8")
@@ -80,6 +82,7 @@ class R8State:
         self.r8_c = recs[..., vb + D:].unflatten(-1, (page, rc))
         self.Vk_scale = meta[..., 0:r]
         self.c_scale = meta[..., 8:8 + page]
+        self.c_scale_f32 = meta.view(f32)[..., 4]
         self.mu_scale = meta[..., 24]
         self.r8_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=device, dtype=bf16)
         self.score = torch.empty(R, n_kv, MP, device=device, dtype=f32)
@@ -95,11 +98,20 @@ class R8State:
         return self.r8_rec[0].numel() + 2 * self.r8_tag[0].numel()
 
     def layer_state(self, layer: int):
-        """(mu, mu_scale, Vk, Vk_scale, c, c_scale, tag) views of ``layer`` (Vk tiled;
-        :meth:`reference_Vk` gives the reference layout)."""
+        """(mu, mu_scale, Vk, Vk_scale, c, c_scale, tag) of ``layer`` (views; Vk tiled,
+        :meth:`reference_Vk` gives the reference layout).  c_scale is per token: for
+        c_grain "page_f32" the page's fp32 scale broadcast over its tokens (a copy)."""
         return (self.r8_mu[layer], self.mu_scale[layer], self.r8_Vk[layer],
-                self.Vk_scale[layer], self.r8_c[layer], self.c_scale[layer],
+                self.Vk_scale[layer], self.r8_c[layer], self.token_c_scale(layer),
                 self.r8_tag[layer])
+
+    def token_c_scale(self, layer: int) -> torch.Tensor:
+        """The c scale of every token (L=layer: (NB, n_kv, page)): the stored fp16 slots,
+        or the fp32 per-page scale repeated over the page."""
+        if self.c_grain == "page_f32":
+            cs = self.c_scale_f32[layer]
+            return cs[..., None].expand(*cs.shape, self.page)
+        return self.c_scale[layer]
 
     def load_reference(self, layer: int, mu, mu_scale, Vk, Vk_scale, c, c_scale) -> None:
         """Write one layer's summaries given in the reference layout
@@ -112,7 +124,10 @@ class R8State:
                                             tiled=True))
         self.Vk_scale[layer].copy_(torch.as_tensor(Vk_scale).to(dev))
         self.r8_c[layer].copy_(torch.as_tensor(c).to(dev))
-        self.c_scale[layer].copy_(torch.as_tensor(c_scale).to(dev))
+        if self.c_grain == "page_f32":      # c_scale (NB, n_kv) fp32 per page
+            self.c_scale_f32[layer].copy_(torch.as_tensor(c_scale).to(dev))
+        else:
+            self.c_scale[layer].copy_(torch.as_tensor(c_scale).to(dev))
 
     def reference_Vk(self, layer: int) -> torch.Tensor:
         """r8_Vk of ``layer`` in the reference layout (NB, n_kv, d, r[/2])."""

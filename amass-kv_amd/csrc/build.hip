@@ -299,7 +299,7 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
             cv[k] = k < r ? L.v[w][t][L.idx[w][k]] * sqrtf(L.s2[w][k]) : 0.f;
             m = fmaxf(m, fabsf(cv[k]));
         }
-        if (a.c_grain == 1) {                           // one scale per (block, head)
+        if (a.c_grain >= 1) {                           // one scale per (block, head)
             m = fmaxf(m, __shfl_xor(m, 1, WAVE));
             m = fmaxf(m, __shfl_xor(m, 2, WAVE));
             m = fmaxf(m, __shfl_xor(m, 4, WAVE));
@@ -322,6 +322,7 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
 
     // ---- the 64-byte fp16 scale block ----------------------------------------------------
     const float cs_in = __shfl(csc_t, (lane - 8) & 63, WAVE);   // c_scale of token lane - 8
+    const uint32_t cs_bits = __float_as_uint(__shfl(csc_t, 0, WAVE));  // c_grain 2: fp32
     if (lane < 32) {
         float v = 0.f;
         bool set = false;
@@ -329,7 +330,7 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         for (int k = 0; k < 8; ++k)
             if (lane == k && k < r) { v = vsc[k]; set = true; }
         if constexpr (R8) {
-            if (lane >= 8 && lane < 24) { v = cs_in; set = true; }
+            if (lane >= 8 && lane < 24 && a.c_grain != 2) { v = cs_in; set = true; }
             else if (lane == 24) { v = msc; set = true; }
             else if (CLSE && lane == 25) {
                 float top = 0.f;
@@ -341,7 +342,12 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
             if (lane >= 8 && lane < 8 + r) { v = L.s2[w][lane - 8]; set = true; }
             else if (lane == 16) { v = msc; set = true; }
         }
-        meta[lane] = set ? f2h_bits(v) : (uint16_t)0;
+        uint16_t h = set ? f2h_bits(v) : (uint16_t)0;
+        if constexpr (R8) {
+            if (a.c_grain == 2 && (lane == 8 || lane == 9))   // the page's fp32 c scale
+                h = (uint16_t)(lane == 8 ? (cs_bits & 0xFFFFu) : (cs_bits >> 16));
+        }
+        meta[lane] = h;
     }
 }
 
@@ -357,6 +363,7 @@ extern "C" int amass_summary_build(const amass_build_args* a, void* stream) {
     if (a->rank < 1 || a->rank > 8) return AMASS_ERR_UNSUPPORTED;
     if (a->v_bits != 8 && a->v_bits != 4) return AMASS_ERR_GEOMETRY;
     if (a->kind >= 1 && a->c_bits != 8 && a->c_bits != 4) return AMASS_ERR_GEOMETRY;
+    if (a->c_grain < 0 || a->c_grain > (a->kind == 1 ? 2 : 1)) return AMASS_ERR_GEOMETRY;
     if ((a->v_bits == 4 || (a->kind >= 1 && a->c_bits == 4)) && (a->rank & 1))
         return AMASS_ERR_GEOMETRY;
     if (a->tag && (a->tagw < 0 || a->tagw > 64)) return AMASS_ERR_GEOMETRY;

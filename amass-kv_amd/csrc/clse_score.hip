@@ -31,6 +31,7 @@ extern "C" int amass_clse_score(const amass_clse_score_args* a, void* stream) {
     p.score_h = a->score_h; p.sh_sr = a->sh_sr; p.sh_sh = a->sh_sh; p.sh_sg = a->sh_sg;
     p.tmax = a->combine == 1 ? a->tile_max : nullptr;
     p.tm_sr = a->tm_sr; p.tm_sh = a->tm_sh; p.tm_sg = a->tm_sg;
+    p.c_fp32 = 0;
     p.comb_out = a->comb_out;
     p.scale = a->scale;
     const int dr = a->d - a->rank > 1 ? a->d - a->rank : 1;

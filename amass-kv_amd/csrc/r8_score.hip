@@ -28,6 +28,8 @@ extern "C" int amass_r8_score(const amass_r8_score_args* a, void* stream) {
     p.scale = a->scale;
     p.score_h = nullptr; p.sh_sr = p.sh_sh = p.sh_sg = 0;
     p.tmax = nullptr; p.tm_sr = p.tm_sh = p.tm_sg = 0;
+    if (a->c_fp32 != 0 && a->c_fp32 != 1) return AMASS_ERR_GEOMETRY;
+    p.c_fp32 = a->c_fp32;
     p.iso_coef = 0.f;
     p.combine = 0;
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.page = a->page; p.max_pages = a->max_pages;

@@ -51,6 +51,7 @@ struct R8Params {
     float* score; int64_t sc_sr, sc_sh;
     float* score_h; int64_t sh_sr, sh_sh, sh_sg;   // CLSE per-head output (combine 1)
     float* tmax; int64_t tm_sr, tm_sh, tm_sg;      // optional per-tile per-head maxima (nrm)
+    int c_fp32;                                   // r8: one fp32 c scale per page
     int32_t* comb_out;
     float scale;
     float iso_coef;                               // CLSE: s^2 / (2 P (d - r))
@@ -137,7 +138,8 @@ struct R8Scales {
 };
 
 template <int RP, int TPL>
-__device__ __forceinline__ R8Scales<RP, TPL> r8_gather_scales(i32x4_t meta, int n, int part) {
+__device__ __forceinline__ R8Scales<RP, TPL> r8_gather_scales(i32x4_t meta, int n, int part,
+                                                              bool c_fp32) {
     R8Scales<RP, TPL> s;
     constexpr int NW = RP / 2;            // dwords holding r halves
 #pragma unroll
@@ -145,6 +147,12 @@ __device__ __forceinline__ R8Scales<RP, TPL> r8_gather_scales(i32x4_t meta, int 
     const uint32_t w24 = (uint32_t)__shfl(meta[0], n + 48, WAVE);   // halves 24, 25
     s.mus = fp16_to_f32((uint16_t)(w24 & 0xFFFFu));
     s.resid = fp16_to_f32((uint16_t)(w24 >> 16));
+    if (c_fp32) {                         // one fp32 for the page: bytes 16..19 (group 1)
+        const float c = __uint_as_float((uint32_t)__shfl(meta[0], n + 16, WAVE));
+#pragma unroll
+        for (int t = 0; t < TPL; ++t) s.cs[t] = c;
+        return s;
+    }
     if constexpr (TPL == 16) {
         uint32_t w[8];
 #pragma unroll
@@ -445,7 +453,7 @@ void r8_score_kernel(const R8Params p) {
     for (int i = 0; i + 1 < cnt; ++i) {
         const int page = page_of(tile);
         const bool valid = page < nsh;
-        const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part);
+        const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part, p.c_fp32 != 0);
         r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid,
                                        pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
@@ -465,7 +473,7 @@ void r8_score_kernel(const R8Params p) {
     }
     const int page = page_of(tile);
     const bool valid = page < nsh;
-    const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part);
+    const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part, p.c_fp32 != 0);
     r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid, pair,
                                    part, n);
     r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, row, req, h, page, valid, pair,

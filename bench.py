@@ -16,14 +16,15 @@ score / select / attend path (oracle/torch_path.py) on the host cores
 Inputs are synthetic (amass.bench.synth, seeded) and resident in HBM before timing.
 
 Secondary lines (under "configs"; skipped with --quick): config 1 with the key-norm boost,
-config 2 (r8, 64 ragged sequences, 5 % budget), config 3 (G = 8, 131072 tokens, coverage
+config 2 (r8, 64 ragged sequences, 5 % budget; fp16 per-token c scales and, as "2f", the
+per-page fp32 c scale), config 3 (G = 8, 131072 tokens, coverage
 0.95, split-K path) and config 4 (mem-v, 64 steps from a cold hot buffer, both boosts),
 each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s; the CLSE
 score (the reference's default score) at the config-1 shape; and the HIP page-summary
 builder (bulk build and steady-state tail rebuild at config 1).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--quick]
-                  [--configs 1k,clse,2,3,4,build]
+                  [--configs 0,1k,clse,2,2f,3,4,build]
 """
 from __future__ import annotations
 
@@ -135,12 +136,14 @@ def quad_score_bytes(st, n_req, G):
 
 def r8_score_bytes(st, n_req, G):
     """Algorithmic HBM bytes of one r8-score launch: per scored (page, kv-head) Vk
-    d*r*vb/8 + mu d + c page*r*cb/8 + Vk_scale 2r + mu_scale 2 + c_scale 2*page (1330 B
-    at r=8 int8), plus the block table, q and one score float per record."""
+    d*r*vb/8 + mu d + c page*r*cb/8 + Vk_scale 2r + mu_scale 2 + c_scale (2*page fp16
+    per-token scales, or one fp32 for c_grain "page_f32"; 1330 / 1318 B at r=8 int8), plus
+    the block table, q and one score float per record."""
     nsh = st.n_sel_hi[:n_req].clamp_min(0).long()
     units = int(nsh.sum()) * st.n_kv
+    cs = 4 if st.c_grain == "page_f32" else 2 * st.page
     rec = (st.d * st.r * st.vk_bits // 8 + st.d + st.page * st.r * st.c_bits // 8
-           + 2 * st.r + 2 + 2 * st.page)
+           + 2 * st.r + 2 + cs)
     return units * (rec + 4) + int(nsh.sum()) * 4 + n_req * st.n_kv * G * st.d * 2
 
 
@@ -380,15 +383,17 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
                 kernels=kernels)
 
 
-def run_secondary(idx, args, boost="sigma"):
-    """A BASELINE configuration other than the headline, measured like config 1."""
+def run_secondary(idx, args, boost="sigma", c_grain="page"):
+    """A BASELINE configuration other than the headline, measured like config 1
+    (config 2 with c_grain "page_f32": one fp32 c scale per page and head)."""
     from amass.bench.synth import CONFIGS, build_quad_state, build_r8_state, config_case
 
     cfg = CONFIGS[idx]
     t0 = time.time()
     case = config_case(idx, seed=args.seed, device="cuda", boost=boost)
     if cfg["score"] == "r8":
-        st = build_r8_state(case, rank=8, vk_bits=8, c_bits=8, budget=cfg["budget"])
+        st = build_r8_state(case, rank=8, vk_bits=8, c_bits=8, budget=cfg["budget"],
+                            c_grain=c_grain)
     else:
         st = build_quad_state(case, rank=8, v_bits=8, combine="nrm",
                               coverage=cfg["coverage"], budget=cfg["budget"] or 0.1)
@@ -399,7 +404,8 @@ def run_secondary(idx, args, boost="sigma"):
     res["workload"] = (f"config{idx}: B={case.q.shape[0]} ctx "
                        + (f"{int(lens.min())}..{int(lens.max())} (sum {int(lens.sum())})"
                           if isinstance(cfg["ctx"], tuple) else f"{cfg['ctx']}")
-                       + f" G={case.G} {cfg['score']} r=8 int8, {sel}, boost {boost}")
+                       + f" G={case.G} {cfg['score']} r=8 int8, {sel}, boost {boost}"
+                       + (f", c scale {c_grain}" if cfg["score"] == "r8" else ""))
     log(f"config {idx}: sparse {res['us']} us, dense {res['dense_us']} us")
     return res
 
@@ -648,7 +654,7 @@ def main():
     ap.add_argument("--boost", default="sigma", choices=["sigma", "keynorm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
-    ap.add_argument("--configs", default="0,1k,clse,2,3,4,build",
+    ap.add_argument("--configs", default="0,1k,clse,2,2f,3,4,build",
                     help="secondary lines: 0 (config 0 on the GPU), 1k (config 1 with the "
                          "key-norm boost), clse (the "
                          "CLSE score at the config-1 shape), 2, 3, 4, build (the HIP "
@@ -749,6 +755,8 @@ def main():
                 sec["config1_keynorm"] = run_secondary(1, args, boost="keynorm")
             elif c in ("0", "2", "3"):
                 sec[f"config{c}"] = run_secondary(int(c), args)
+            elif c == "2f":
+                sec["config2_page_f32"] = run_secondary(2, args, c_grain="page_f32")
             elif c == "build":
                 sec["summary_build"] = run_summary_build(args)
             elif c == "clse":

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 7
+#define AMASS_ABI_VERSION 8
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -92,7 +92,10 @@ int amass_quad_score(const amass_quad_score_args* a, void* stream);
  *   at n_kv*VM + 64*h:      fp16 halves: Vk_scale[0..r), c_scale[0..16) at half 8,
  *                           mu_scale at half 24
  * VM = r*CB + 128 + 16*r*c_bits/8.  rec_sb (bytes between blocks) >= n_kv * REC_BYTES, a
- * multiple of 16.  rank 4 or 8; G 1, 2, 4 or 8; n_kv <= 8 or a multiple of 8. */
+ * multiple of 16.  rank 4 or 8; G 1, 2, 4 or 8; n_kv <= 8 or a multiple of 8.
+ * c_fp32 = 1 (no counterpart in the reference, whose c scales are fp16 per token): the
+ * page's 16 tokens share one fp32 c scale, stored at bytes 16..19 of the scale block
+ * (halves 8..9; halves 10..23 zero) -- the per-page fp32 scale layout. */
 #define AMASS_R8_REC_BYTES(rank, vk_bits, c_bits) \
     ((rank) * ((vk_bits) == 8 ? 128 : 64) + 128 + 2 * (rank) * (c_bits) + 64)
 typedef struct amass_r8_score_args {
@@ -104,7 +107,7 @@ typedef struct amass_r8_score_args {
     float*         score;    int64_t sc_sr, sc_sh;   /* (R,n_kv,MP) fp32                */
     int32_t*       comb_out; /* optional (R,n_kv,MP,G,r+1) exact int32 sums; NULL = off */
     float          scale;
-    int32_t n_req, n_kv, G, d, page, rank, vk_bits, c_bits, max_pages;
+    int32_t n_req, n_kv, G, d, page, rank, vk_bits, c_bits, max_pages, c_fp32;
 } amass_r8_score_args;
 int amass_r8_score(const amass_r8_score_args* a, void* stream);
 
@@ -118,7 +121,8 @@ int amass_r8_score(const amass_r8_score_args* a, void* stream);
  * eigenpairs (S2r = max(eig, 1e-10), ascending), Vk = dc^T U8 / sqrt(S2r) and, for r8,
  * c = U8 sqrt(S2r); symmetric quantisation s = max(amax / lvl, 1e-8), code =
  * clamp(rint(x / s), +-lvl), scale stored as fp16(s) (mu per head; Vk per column for
- * v_grain 0 or per head for 1; c per token for c_grain 0 or per head for 1).  Writes the
+ * v_grain 0 or per head for 1; c per token for c_grain 0 or per head for 1; r8 only:
+ * c_grain 2 = per head with the scale stored as fp32, the c_fp32 layout of the r8 score).  Writes the
  * block's packed record (kind 0: quad, AMASS_QUAD_REC_BYTES layout with sig2 = fp16(S2r);
  * kind 1: r8, AMASS_R8_REC_BYTES layout; kind 2: CLSE, the r8 layout plus the residual
  * scatter energy resid = max(trace(Gm) - sum S2r, 0) as fp16 at half 25, c_grain 0 per

@@ -54,7 +54,10 @@ def quad_summary(K, rank: int, v_bits: int = 8, v_grain: str = "col"):
 
 def r8_summary(K, rank: int, vk_bits: int = 8, c_bits: int = 8, vk_grain: str = "col",
                c_grain: str = "page"):
-    """-> dict(mu, mu_scale, Vk, Vk_scale, c (N, n_kv, page, r[/2]), c_scale (N, n_kv, page))."""
+    """-> dict(mu, mu_scale, Vk, Vk_scale, c (N, n_kv, page, r[/2]), c_scale (N, n_kv, page)).
+    c_grain "page": a scale per token; "tensor" and "page_f32": one scale per (block,
+    head) over the page's coordinates (repeated per token here; stored fp16 by the
+    reference's "tensor" layout, fp32 by the per-page fp32 layout)."""
     mu, _dc, S2r, U8, Vk = page_factors(K, rank)
     mu_code, mu_s = quant(mu.astype(np.float32), axis=-1, bits=8)
     V, Vs = _vk_codes(Vk, vk_bits, vk_grain)

@@ -194,7 +194,7 @@ def test_quad_summary_build(rank, v_bits, v_grain):
 
 @pytest.mark.parametrize("rank,vk_bits,c_bits,vk_grain,c_grain",
                          [(8, 8, 8, "col", "page"), (8, 4, 4, "col", "page"),
-                          (4, 8, 4, "tensor", "tensor")])
+                          (4, 8, 4, "tensor", "tensor"), (8, 8, 8, "col", "page_f32")])
 def test_r8_summary_build(rank, vk_bits, c_bits, vk_grain, c_grain):
     announce(f"HIP builder r8 r={rank} vk={vk_bits} c={c_bits} {vk_grain}/{c_grain}")
     from amass.selection.build import r8_build_refresh
@@ -218,9 +218,11 @@ def test_r8_summary_build(rank, vk_bits, c_bits, vk_grain, c_grain):
     sgn = _col_check(oq.codes(ref["Vk"], vk_bits), Vk, sep)
     c = oq.codes(npi(st.r8_c[0])[blocks], c_bits).astype(np.float64) * sgn  # same column signs
     cref = oq.codes(ref["c"], c_bits).astype(np.float64)
-    cs = npf(st.c_scale[0])[blocks]
-    if c_grain == "tensor":
+    cs = npf(st.token_c_scale(0))[blocks]
+    if c_grain != "page":
         assert np.all(cs == cs[..., :1])
+    if c_grain == "page_f32":         # stored fp32, not rounded to fp16
+        assert not np.all(cs == cs.astype(np.float16).astype(np.float32))
     # a token's scale is the max over its r coordinates: rows whose scale agrees, columns
     # that are separated
     same = np.abs(cs - ref["c_scale"]) <= 2e-3 * ref["c_scale"]

@@ -213,3 +213,39 @@ def test_r8_head_layouts(n_kv, G):
         n = int(nsh[r])
         assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
         assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3
+
+
+@pytest.mark.parametrize("vk_bits,c_bits,G", [(8, 8, 4), (8, 4, 8), (4, 8, 2)])
+def test_r8_page_f32_scale(vk_bits, c_bits, G):
+    """The per-page fp32 c scale (c_grain "page_f32", BASELINE config 2's "per-page fp32
+    scale"): int32 contractions exact (they do not depend on the scale format), scores
+    within 1e-3 of the fp64 oracle fed the same fp32 scales."""
+    announce(f"r8 page_f32 vk={vk_bits} c={c_bits} G={G}")
+    case = make_case(B=3, ctx=(300, 1400), n_kv=8, G=G, seed=71 + G + c_bits)
+    st = build_r8_state(case, rank=8, vk_bits=vk_bits, c_bits=c_bits, c_grain="page_f32")
+    to_device(st, DEV)
+    case_to(case, DEV)
+    B, MP = 3, st.max_pages
+    derive_page_params(st, case.seq_lens, B)
+    comb = torch.zeros(B, 8, MP, G, 9, dtype=torch.int32, device=DEV)
+    r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
+    torch.cuda.synchronize()
+    sc_comb = npf(st.score).copy()
+    r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale)
+    torch.cuda.synchronize()
+    mu, mus, _, Vks, c, cs, _ = st.layer_state(0)
+    assert bool((npf(st.c_scale_f32[0]) > 0).any())
+    Vk = st.reference_Vk(0)
+    nsh = npi(st.n_sel_hi)
+    ref_comb = osc.r8_comb(npf(case.q), npi(mu), npi(Vk), npi(case.block_table), nsh, G=G,
+                           vk_bits=vk_bits, max_pages=MP)
+    ref = osc.r8_score(npf(case.q), npi(mu), npf(mus), npi(Vk), npf(Vks), npi(c), npf(cs),
+                       npi(case.block_table), npi(case.seq_lens), nsh, scale=case.scale,
+                       page=16, G=G, vk_bits=vk_bits, c_bits=c_bits, max_pages=MP)
+    got = npi(comb).astype(np.int64)
+    sc = npf(st.score)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
+        assert rel_close(sc[r, :, :n], sc_comb[r, :, :n], 1) <= 1e-6
+        assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3

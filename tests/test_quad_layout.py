@@ -121,3 +121,30 @@ def test_r8_record_positions(vk_bits, c_bits, r):
     meta = raw[b, n_kv * vm + 64 * h: n_kv * vm + 64 * (h + 1)].view(np.float16)
     assert np.array_equal(meta[:r], vks[b, h]) and np.array_equal(meta[8:24], cs[b, h])
     assert meta[24] == mus[b, h] and not meta[25:].any()
+
+
+def test_r8_page_f32_scale_position():
+    """c_grain "page_f32" (the per-page fp32 c scale): one fp32 per (block, head) at bytes
+    16..19 of the head's scale block, halves 10..23 zero; token_c_scale repeats it."""
+    from amass.selection import R8State
+    n_kv, NB, r = 2, 3, 8
+    st = R8State("cpu", num_layers=1, num_blocks=NB, n_kv=n_kv, G=4, head_dim=128, page=16,
+                 max_reqs=1, max_pages=4, rank=r, c_grain="page_f32")
+    rng = np.random.default_rng(5)
+    Vk = rng.integers(-127, 128, (NB, n_kv, 128, r)).astype(np.int8)
+    c = rng.integers(-127, 128, (NB, n_kv, 16, r)).astype(np.int8)
+    mu = rng.integers(-127, 128, (NB, n_kv, 128)).astype(np.int8)
+    mus = rng.random((NB, n_kv)).astype(np.float16)
+    vks = rng.random((NB, n_kv, r)).astype(np.float16)
+    cs = (rng.random((NB, n_kv)) * 1e-3 + 1e-7).astype(np.float32)   # not fp16-exact
+    st.load_reference(0, mu, mus, Vk, vks, c, cs)
+    vm = r * 128 + 128 + 16 * r
+    raw = st.r8_rec[0].numpy().view(np.uint8)
+    for b in range(NB):
+        for h in range(n_kv):
+            blk = raw[b, n_kv * vm + 64 * h: n_kv * vm + 64 * (h + 1)]
+            assert blk[16:20].view(np.float32)[0] == cs[b, h]
+            assert not blk[20:48].any()
+            assert blk[48:50].view(np.float16)[0] == mus[b, h]
+    tcs = st.token_c_scale(0).numpy()
+    assert tcs.shape == (NB, n_kv, 16) and np.array_equal(tcs, np.repeat(cs[..., None], 16, -1))
