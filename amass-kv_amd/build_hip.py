@@ -1,6 +1,7 @@
 """Build libamass_hip.so (every HIP source under csrc/) for gfx950, in tree.
 
     python amass-kv_amd/build_hip.py            # -> amass-kv_amd/amass/_lib/libamass_hip.so
+                                                #    and libamass_calib.so (calib/)
 
 Each .hip file compiles to an object in amass-kv_amd/_build/ (in parallel), then one
 hipcc link produces the shared library.  Packed fp32 VALU ops are disabled for all device
@@ -72,5 +73,26 @@ def build(verbose: bool = True) -> str:
     return LIB
 
 
+CALIB_SRC = os.path.join(HERE, "calib", "gather_calib.hip")
+CALIB_LIB = os.path.join(OUT_DIR, "libamass_calib.so")
+
+
+def build_calib(verbose: bool = True) -> str:
+    """Build libamass_calib.so: the HBM-counter calibration kernel bench.py profiles
+    beside the hot path (measurement only; not part of libamass_hip.so's ABI)."""
+    t0 = time.time()
+    os.makedirs(OUT_DIR, exist_ok=True)
+    tmp = CALIB_LIB + ".tmp"
+    cmd = [_hipcc(), *CFLAGS, "-shared", CALIB_SRC, "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {CALIB_SRC}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, CALIB_LIB)
+    if verbose:
+        print(f"[amass build] calibration kernel -> {CALIB_LIB} ({time.time() - t0:.1f}s)")
+    return CALIB_LIB
+
+
 if __name__ == "__main__":
     build()
+    build_calib()

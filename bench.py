@@ -23,8 +23,16 @@ each with its dense paged decode and per-kernel GB/s and fraction of 8 TB/s; the
 score (the reference's default score) at the config-1 shape; and the HIP page-summary
 builder (bulk build and steady-state tail rebuild at config 1).
 
+Each kernel entry carries `traffic` (HBM bytes per launch from rocprofv3 FETCH_SIZE /
+WRITE_SIZE) and `mfma` (MFMA-busy percentage and operations per launch from rocprofv3,
+with the rate those operations reach at the live duration) where the workload's
+profiles/counters_<workload>.txt holds them.  Two calibration
+kernels of known size run first (torch.neg, and a gather with the decode's access
+pattern): the counter runs scale FETCH_SIZE / WRITE_SIZE by them, and the gather's live
+GB/s is reported as the streaming ceiling of that access pattern.
+
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--quick]
-                  [--configs 0,1k,clse,2,2f,3,4,build]
+                  [--configs 0,1k,clse,2,2f,3,4,build] [--only WORKLOAD]
 """
 from __future__ import annotations
 
@@ -104,23 +112,108 @@ def time_eager(fn, steps, warmup, batches=7):
     return statistics.median(out)
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config1.txt")
+PROFILES = os.path.join(ROOT, "profiles")
+PEAK_MFMA = {"bf16": 2.5e15, "i8": 5.0e15}   # MI355X dense MFMA, flop/s and op/s
 
 
-def profiled_traffic():
-    """HBM bytes per launch measured by rocprofv3 (FETCH_SIZE / WRITE_SIZE, calibrated
-    against a kernel of known size) for the config-1 kernels: the `traffic <kernel>
-    <bytes>` lines of profiles/hbm_traffic_config1.txt, or {} when it is absent."""
+def _profile_lines(path, tag):
     out = {}
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) == 3 and parts[0] == "traffic":
-                    out[parts[1]] = int(parts[2])
+                if len(parts) >= 3 and parts[0] == tag:
+                    out[parts[1]] = parts[2:]
     except OSError:
         pass
     return out
+
+
+def profiled_traffic(name="config1"):
+    """HBM bytes per launch measured by rocprofv3 (FETCH_SIZE / WRITE_SIZE, scaled by the
+    same counters on two calibration kernels of known size) for workload `name`: the
+    `traffic <kernel> <bytes>` lines of profiles/counters_<name>.txt ({} if absent)."""
+    return {k: int(v[0]) for k, v in
+            _profile_lines(os.path.join(PROFILES, f"counters_{name}.txt"), "traffic").items()}
+
+
+def profiled_mfma(name="config1"):
+    """MFMA counters per launch for workload `name` (profiles/counters_<name>.txt `mfma
+    <kernel> <util%> <bf16_ops> <i8_ops> <insts>` lines): {kernel: (util%, bf16, i8)}."""
+    return {k: (float(v[0]), float(v[1]), float(v[2])) for k, v in
+            _profile_lines(os.path.join(PROFILES, f"counters_{name}.txt"), "mfma").items()}
+
+
+def mfma_entry(us, prof):
+    """The kernel's MFMA use: rocprofv3's MFMA-busy percentage and MFMA operation count
+    per launch (same workload, profiled), the rate those operations reach at the live
+    duration `us`, and that rate over MI355X's dense peak for the operand type."""
+    if prof is None:
+        return None
+    util, bf, i8 = prof
+    if bf == 0 and i8 == 0:
+        return {"busy_pct": round(util, 2), "ops_per_launch": 0}     # no MFMA in the kernel
+    kind, ops = ("i8", i8) if i8 > bf else ("bf16", bf)
+    rate = ops / (us * 1e-6)
+    return {"busy_pct": round(util, 2), "type": kind, "ops_per_launch": ops,
+            "achieved_tops": round(rate / 1e12, 2), "peak_tops": PEAK_MFMA[kind] / 1e12,
+            "frac": round(rate / PEAK_MFMA[kind], 5)}
+
+
+def run_calibration(dev, reps=3):
+    """Two kernels whose HBM bytes are known exactly, profiled beside the hot path to
+    scale rocprofv3's FETCH_SIZE / WRITE_SIZE: torch.neg over 256 MiB fp32 (reads and
+    writes 256 MiB), and libamass_calib's gather, which reads every (block, kv head) K and
+    V slice of a 2 GiB paged pool (32768 blocks, 8 kv heads, page 16, d 128) once in a
+    random block order with the decode kernel's 16-byte non-temporal lane pattern.
+    Returns both kernels' live GB/s (the gather's is the streaming rate that access
+    pattern reaches on this GPU)."""
+    import ctypes as C
+
+    import torch
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        torch.neg(src, out=dst)
+    b.record()
+    torch.cuda.synchronize()
+    neg_gbs = 2 * (256 << 20) * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    lib = C.CDLL(os.path.join(ROOT, "amass-kv_amd", "amass", "_lib", "libamass_calib.so"))
+    fn = lib.amass_calib_gather
+    fn.argtypes = [C.c_void_p, C.c_void_p] + [C.c_int64] * 6 + [C.c_void_p, C.c_int32,
+                                                                 C.c_int32, C.c_void_p,
+                                                                 C.c_void_p]
+    fn.restype = C.c_int
+    NB, n_kv = 32768, 8
+    pool = torch.empty(NB, 2, 16, n_kv, 128, dtype=torch.bfloat16, device=dev).normal_()
+    k, v = pool[:, 0], pool[:, 1]
+    blocks = torch.randperm(NB, device=dev).to(torch.int32)
+    out = torch.empty(((NB + 15) // 16) * n_kv, dtype=torch.int32, device=dev)
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def launch():
+        rc = fn(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+                v.stride(0), v.stride(1), v.stride(2), blocks.data_ptr(), NB, n_kv,
+                out.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"amass_calib_gather returned {rc}")
+    launch()
+    a.record()
+    for _ in range(reps):
+        launch()
+    b.record()
+    torch.cuda.synchronize()
+    nbytes = NB * n_kv * 2 * 16 * 128 * 2 + 4 * NB
+    gather_gbs = nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del pool, k, v, blocks, out
+    torch.cuda.empty_cache()
+    log(f"calibration: neg {neg_gbs:.0f} GB/s, decode-pattern gather {gather_gbs:.0f} GB/s")
+    return {"neg_gbs": round(neg_gbs, 1), "gather_gbs": round(gather_gbs, 1),
+            "gather_bytes": nbytes}
 
 
 def quad_score_bytes(st, n_req, G):
@@ -277,9 +370,13 @@ def cpu_baseline(case1, st1, args):
             "torch_threads": n, "config1": c1, "config0": c0}
 
 
-def kernel_entry(us, nbytes, traffic=None):
-    return dict(us=round(us, 2), bytes=nbytes, gbs=round(nbytes / us / 1e3, 1),
-                frac=round(nbytes / (us * 1e-6) / PEAK_HBM, 4), traffic=traffic)
+def kernel_entry(us, nbytes, traffic=None, mfma=None):
+    e = dict(us=round(us, 2), bytes=nbytes, gbs=round(nbytes / us / 1e3, 1),
+             frac=round(nbytes / (us * 1e-6) / PEAK_HBM, 4), traffic=traffic)
+    m = mfma_entry(us, mfma)
+    if m is not None:
+        e["mfma"] = m
+    return e
 
 
 def free_gpu():
@@ -291,7 +388,7 @@ def free_gpu():
     torch.cuda.empty_cache()
 
 
-def measure_step(case, st, args, *, score="quad", traffic=None):
+def measure_step(case, st, args, *, score="quad", name="config1"):
     """Time one layer's sparse decode step (score + select + attend, one HIP graph) and
     the dense paged decode of the same batch, then each kernel alone (10 launches per
     graph); returns the per-config result dict."""
@@ -305,7 +402,7 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     from amass.selection.score import r8_score
     from amass.selection.select import select_pages
 
-    traffic = traffic or {}
+    traffic, mf = profiled_traffic(name), profiled_mfma(name)
     B, G, n_kv = case.q.shape[0], case.G, case.n_kv
     q, kv, bt, sl = case.q, case.kv_cache, case.block_table, case.seq_lens
     derive_page_params(st, sl, B)
@@ -368,10 +465,11 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
     b_att = attend_bytes(cnt, B, n_kv, G)
     b_dense = attend_bytes(st.n_pages[:B][:, None].expand(B, n_kv), B, n_kv, G)
     sname = f"{score}_score"
-    kernels = {sname: kernel_entry(us_score, b_score, traffic.get(sname)),
+    kernels = {sname: kernel_entry(us_score, b_score, traffic.get(sname), mf.get(sname)),
                ("select_nrm_coverage" if nrm else "select"):
-                   kernel_entry(us_sel, b_sel, traffic.get("select_nrm_coverage")),
-               "sparse_decode": kernel_entry(us_att, b_att, traffic.get("sparse_decode"))}
+                   kernel_entry(us_sel, b_sel, traffic.get("select"), mf.get("select")),
+               "sparse_decode": kernel_entry(us_att, b_att, traffic.get("sparse_decode"),
+                                             mf.get("sparse_decode"))}
     return dict(us=round(ms_sparse * 1e3, 2),
                 gb_s=round((b_score + b_sel + b_att) / (ms_sparse * 1e-3) / 1e9, 1),
                 dense_us=round(ms_dense * 1e3, 2),
@@ -379,13 +477,15 @@ def measure_step(case, st, args, *, score="quad", traffic=None):
                 speedup_vs_dense=round(ms_dense / ms_sparse, 3),
                 eager_us=round(ms_sparse_eager * 1e3, 2),
                 dense_eager_us=round(ms_dense_eager * 1e3, 2),
+                dense_bytes=b_dense, dense_traffic=traffic.get("dense_decode"),
                 selected_fraction=round(frac, 4), attended_fraction=round(att_frac, 4),
                 kernels=kernels)
 
 
-def run_secondary(idx, args, boost="sigma", c_grain="page"):
+def run_secondary(idx, args, boost="sigma", c_grain="page", name=None):
     """A BASELINE configuration other than the headline, measured like config 1
-    (config 2 with c_grain "page_f32": one fp32 c scale per page and head)."""
+    (config 2 with c_grain "page_f32": one fp32 c scale per page and head).  `name` keys
+    the profiled counter files of the workload (profiles/*_<name>.txt)."""
     from amass.bench.synth import CONFIGS, build_quad_state, build_r8_state, config_case
 
     cfg = CONFIGS[idx]
@@ -398,7 +498,7 @@ def run_secondary(idx, args, boost="sigma", c_grain="page"):
         st = build_quad_state(case, rank=8, v_bits=8, combine="nrm",
                               coverage=cfg["coverage"], budget=cfg["budget"] or 0.1)
     log(f"config {idx} ({boost}): inputs + summaries {time.time() - t0:.1f}s")
-    res = measure_step(case, st, args, score=cfg["score"])
+    res = measure_step(case, st, args, score=cfg["score"], name=name or f"config{idx}")
     lens = case.seq_lens.long()
     sel = (f"top-b {cfg['budget']:.0%}" if cfg["budget"] else f"coverage {cfg['coverage']}")
     res["workload"] = (f"config{idx}: B={case.q.shape[0]} ctx "
@@ -418,7 +518,8 @@ def run_clse(args, boost="sigma"):
     case = config_case(1, seed=args.seed, device="cuda", boost=boost)
     st = build_quad_state(case, rank=2, v_bits=4, combine="nrm", coverage=0.95,
                           coords="lse", c_bits=4, c_grain="token")
-    res = measure_step(case, st, args, score="clse")
+    res = measure_step(case, st, args, score="clse",
+                       name="config1_clse" + ("_keynorm" if boost == "keynorm" else ""))
     res["workload"] = (f"config1 shape: B=32 ctx 16384 G=4, CLSE r'=2 int4 V + int4 per-token "
                        f"coords, nrm, coverage 0.95, boost {boost}")
     log(f"clse ({boost}): sparse {res['us']} us, dense {res['dense_us']} us")
@@ -645,6 +746,30 @@ def write_path_times(tier, case, args):
                 requests=B, staging_ok=ok)
 
 
+def run_headline_only(args):
+    """Config 1's measured step alone (no fixed-budget line, no CPU baseline)."""
+    from amass.bench.synth import build_quad_state, config_case
+    case = config_case(1, seed=args.seed, device="cuda", boost=args.boost)
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
+    return measure_step(case, st, args, score="quad", name="config1")
+
+
+# secondary lines: --configs token -> (result key, runner); the key also names the
+# workload's profiled counter files
+SECONDARY = {
+    "0": ("config0", lambda a: run_secondary(0, a)),
+    "1k": ("config1_keynorm", lambda a: run_secondary(1, a, boost="keynorm",
+                                                      name="config1_keynorm")),
+    "2": ("config2", lambda a: run_secondary(2, a)),
+    "2f": ("config2_page_f32", lambda a: run_secondary(2, a, c_grain="page_f32",
+                                                       name="config2_page_f32")),
+    "3": ("config3", lambda a: run_secondary(3, a)),
+}
+ONLY = {"1": run_headline_only, "clse": lambda a: run_clse(a),
+        "clsek": lambda a: run_clse(a, "keynorm"),
+        **{k: v[1] for k, v in SECONDARY.items()}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -656,11 +781,12 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (for profiling)")
     ap.add_argument("--configs", default="0,1k,clse,2,2f,3,4,build",
                     help="secondary lines: 0 (config 0 on the GPU), 1k (config 1 with the "
-                         "key-norm boost), clse (the "
-                         "CLSE score at the config-1 shape), 2, 3, 4, build (the HIP "
-                         "summary builder)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a plain 256 MiB read + 256 MiB write kernel (HBM counter calibration)")
+                         "key-norm boost), clse (the CLSE score at the config-1 shape), 2, "
+                         "2f (config 2 with the per-page fp32 c scale), 3, 4, build (the "
+                         "HIP summary builder)")
+    ap.add_argument("--only", choices=sorted(ONLY),
+                    help="measure one workload alone and print {\"only\": result} (for "
+                         "counter runs under rocprofv3): " + ", ".join(sorted(ONLY)))
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path has no "
@@ -675,32 +801,30 @@ def main():
     from amass.selection import derive_page_params
 
     dev = "cuda"
-    if args.copy_calibration:
-        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).normal_()
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)     # one elementwise kernel: reads 256 MiB, writes 256 MiB
-        torch.cuda.synchronize()
-        log("copy calibration: 3 x 256 MiB device copies done")
-        del src, dst
+    calib = run_calibration(dev)
+    if args.only:
+        print(json.dumps({"only": ONLY[args.only](args), "calibration": calib}), flush=True)
+        return
     t0 = time.time()
     case = config_case(1, seed=args.seed, device=dev, boost=args.boost)
     log(f"inputs generated ({time.time() - t0:.1f}s)")
     st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
     log(f"quad summaries built ({time.time() - t0:.1f}s)")
     B = case.q.shape[0]
-    traffic = profiled_traffic()
-    m = measure_step(case, st, args, score="quad", traffic=traffic)
+    m = measure_step(case, st, args, score="quad", name="config1")
     log(f"sparse {m['us']} us, dense {m['dense_us']} us")
     kernels = m["kernels"]
     dom = max(kernels, key=lambda k: kernels[k]["us"])
     dk = kernels[dom]
     roof = {"bound": "hbm", "kernel": dom, "achieved": dk["gbs"],
             "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": dk["frac"],
-            "traffic": traffic.get(dom),
-            "traffic_source": "profiles/hbm_traffic_config1.txt: rocprofv3 FETCH_SIZE x2.000 "
-                              "+ WRITE_SIZE x1.000 (scales from a 256 MiB neg kernel)"
-            if dom in traffic else None}
+            "traffic": dk["traffic"],
+            "traffic_source": "profiles/counters_config1.txt: rocprofv3 FETCH_SIZE and "
+                              "WRITE_SIZE per launch, scaled by the same counters on a "
+                              "256 MiB neg kernel (checked on a decode-pattern gather)"
+            if dk["traffic"] is not None else None,
+            "pattern_ceiling_gbs": calib["gather_gbs"],
+            "mfma": dk.get("mfma")}
     res = {
         "metric": "sparse decode attn us/layer + HBM GB/s at B=32 ctx16k; speedup vs dense paged",
         "value": m["us"], "unit": "us/layer", "n_gpus": 1,
@@ -719,6 +843,7 @@ def main():
         "attended_fraction": m["attended_fraction"],
         "kernels": kernels,
         "roofline": roof,
+        "calibration": calib,
     }
     if not args.quick:
         # secondary: fixed 5% budget at the same shape (same summaries, top-b selection)
@@ -751,12 +876,9 @@ def main():
         free_gpu()
         sec = {}
         for c in [x.strip() for x in args.configs.split(",") if x.strip()]:
-            if c == "1k":
-                sec["config1_keynorm"] = run_secondary(1, args, boost="keynorm")
-            elif c in ("0", "2", "3"):
-                sec[f"config{c}"] = run_secondary(int(c), args)
-            elif c == "2f":
-                sec["config2_page_f32"] = run_secondary(2, args, c_grain="page_f32")
+            if c in SECONDARY:
+                key, fn = SECONDARY[c]
+                sec[key] = fn(args)
             elif c == "build":
                 sec["summary_build"] = run_summary_build(args)
             elif c == "clse":
