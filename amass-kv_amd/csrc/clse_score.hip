@@ -36,6 +36,8 @@ extern "C" int amass_clse_score(const amass_clse_score_args* a, void* stream) {
     p.scale = a->scale;
     const int dr = a->d - a->rank > 1 ? a->d - a->rank : 1;
     p.iso_coef = a->scale * a->scale / (2.0f * (float)a->page * (float)dr);
+    p.scale_l2 = p.scale * 1.44269504088896341f;
+    p.iso_k = p.iso_coef / (p.scale_l2 * p.scale_l2);
     p.combine = a->combine;
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.page = a->page; p.max_pages = a->max_pages;
     p.hw = a->n_kv < R8_MAXW ? a->n_kv : R8_MAXW;

@@ -31,6 +31,8 @@ extern "C" int amass_r8_score(const amass_r8_score_args* a, void* stream) {
     if (a->c_fp32 != 0 && a->c_fp32 != 1) return AMASS_ERR_GEOMETRY;
     p.c_fp32 = a->c_fp32;
     p.iso_coef = 0.f;
+    p.scale_l2 = p.scale * 1.44269504088896341f;
+    p.iso_k = p.iso_coef / (p.scale_l2 * p.scale_l2);
     p.combine = 0;
     p.n_req = a->n_req; p.n_kv = a->n_kv; p.page = a->page; p.max_pages = a->max_pages;
     p.hw = a->n_kv < R8_MAXW ? a->n_kv : R8_MAXW;

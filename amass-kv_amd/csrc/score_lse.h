@@ -55,6 +55,8 @@ struct R8Params {
     int32_t* comb_out;
     float scale;
     float iso_coef;                               // CLSE: s^2 / (2 P (d - r))
+    float scale_l2;                               // scale * log2(e) (base-2 token logits)
+    float iso_k;                                  // iso_coef / scale_l2^2
     int combine;                                  // CLSE: 0 group max, 1 per head
     int n_req, n_kv, page, max_pages;
     int hw;         // kv heads (waves) per workgroup
@@ -185,7 +187,8 @@ __device__ __forceinline__ R8Scales<RP, TPL> r8_gather_scales(i32x4_t meta, int 
     return s;
 }
 
-// q~ of the lane's two heads (e = 0: g0, e = 1: g1) and their mu terms.
+// q~ of the lane's two heads (e = 0: g0, e = 1: g1) times scale * log2(e), and their mu
+// terms.
 template <int RP>
 struct R8Acc {
     float qt[2][RP];
@@ -261,53 +264,77 @@ __device__ __forceinline__ void r8_tile_mid(const R8Params& p, const i32x4_t (&q
 #pragma unroll
     for (int k = 0; k < RP; ++k) {
         const float vsc = half_at(sc.vs, k);
-        acc.qt[0][k] = (float)x[k].x * qs0 * vsc;
-        acc.qt[1][k] = (float)x[k].y * qs1 * vsc;
+        acc.qt[0][k] = (float)x[k].x * (qs0 * p.scale_l2) * vsc;
+        acc.qt[1][k] = (float)x[k].y * (qs1 * p.scale_l2) * vsc;
         if (co0) co0[k] = x[k].x;
         if (co1) co1[k] = x[k].y;
     }
 }
 
-// signed code k of token row t of the lane's c words
+// Code k of token row t of the lane's c words as a float.  int8: the signed byte.
+// int4: from `cu`, the words with every nibble's sign bit flipped and split into low
+// (cu[2i]) and high (cu[2i + 1]) nibbles, one per byte -- the nibble's value + 8, taken
+// with one byte conversion; the caller subtracts 8 sum_k q~_k once per head.
 template <int RP, int CBITS>
-__device__ __forceinline__ float c_code(const uint32_t* cw, int t, int k) {
+__device__ __forceinline__ float c_code(const uint32_t* cw, const uint32_t* cu, int t, int k) {
     constexpr int CROW = RP * CBITS / 8;
     if constexpr (CBITS == 8) {
         const int byte = t * CROW + k;
         return (float)(((int)(cw[byte >> 2] << (24 - 8 * (byte & 3)))) >> 24);
     } else {
         const int nib = t * 2 * CROW + k;       // low nibble = even column
-        return (float)(((int)(cw[nib >> 3] << (28 - 4 * (nib & 7)))) >> 28);
+        const uint32_t w = cu[2 * (nib >> 3) + (nib & 1)];
+        return (float)((w >> (8 * ((nib & 7) >> 1))) & 0xFFu);
     }
 }
 
-template <int RP, int CBITS, int G, bool CLSE>
-__device__ __forceinline__ void r8_tile_tail(const R8Params& p,
-                                             const R8GroupC<R8Split<G>::TPL * RP * CBITS / 8>& b,
-                                             const R8Scales<RP, R8Split<G>::TPL>& sc,
-                                             const R8Acc<RP>& acc, int req, int h, int page,
-                                             bool valid, int pair, int part, int kg, int sl,
-                                             float qsq0, float qsq1) {
+// Token logits and their logsumexp over the lane's TPL tokens, in base 2: acc.qt holds
+// q~ * scale * log2(e) (so a logit is c_scale * c . qt), the logsumexp is
+// ln 2 (m + log2 sum 2^(l - m)) on the hardware's exp2 / log2; tokens >= seq_len are
+// masked.  (An unmasked variant for the tiles that end below seq_len measured slower: the
+// compiler's schedule for it needs more registers and the launch loses a wave per SIMD.)
+template <int RP, int CBITS, int G>
+__device__ __forceinline__ void r8_lse(const R8GroupC<R8Split<G>::TPL * RP * CBITS / 8>& b,
+                                       const R8Scales<RP, R8Split<G>::TPL>& sc,
+                                       const R8Acc<RP>& acc, int tok0, int sl, float (&lse)[2]) {
     constexpr int TPL = R8Split<G>::TPL;
     constexpr int GP = R8Split<G>::GP;
-    // token logits of the lane's TPL tokens for both heads
-    const int tok0 = page * p.page + part * TPL;
+    constexpr int NCW = TPL * RP * CBITS / 32 > 0 ? TPL * RP * CBITS / 32 : 1;
+    uint32_t cu[CBITS == 4 ? 2 * NCW : 1];
+    float a0i = 0.f, a1i = 0.f;
+    if constexpr (CBITS == 4) {
+#pragma unroll
+        for (int i = 0; i < NCW; ++i) {
+            const uint32_t x = b.c[i] ^ 0x88888888u;
+            cu[2 * i] = x & 0x0F0F0F0Fu;
+            cu[2 * i + 1] = (x >> 4) & 0x0F0F0F0Fu;
+        }
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < RP; ++k) {
+            s0 += acc.qt[0][k];
+            s1 += acc.qt[1][k];
+        }
+        a0i = -8.f * s0;
+        a1i = -8.f * s1;
+    }
     float lg[2][TPL];
 #pragma unroll
     for (int t = 0; t < TPL; ++t) {
-        float a0 = 0.f, a1 = 0.f;
+        float a0 = a0i, a1 = a1i;
 #pragma unroll
         for (int k = 0; k < RP; ++k) {
-            const float cf = c_code<RP, CBITS>(b.c, t, k);
+            const float cf = c_code<RP, CBITS>(b.c, cu, t, k);
             a0 += cf * acc.qt[0][k];
             a1 += cf * acc.qt[1][k];
         }
-        const float f = p.scale * sc.cs[t];
-        const bool live = tok0 + t < sl;
-        lg[0][t] = live ? a0 * f : -INFINITY;
-        lg[1][t] = live ? a1 * f : -INFINITY;
+        lg[0][t] = a0 * sc.cs[t];
+        lg[1][t] = a1 * sc.cs[t];
+        if (tok0 + t >= sl) {
+            lg[0][t] = -INFINITY;
+            lg[1][t] = -INFINITY;
+        }
     }
-    float S[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         float m = lg[e][0];
@@ -321,18 +348,37 @@ __device__ __forceinline__ void r8_tile_tail(const R8Params& p,
         const float mm = m == -INFINITY ? 0.f : m;
         float se = 0.f;
 #pragma unroll
-        for (int t = 0; t < TPL; ++t) se += __expf(lg[e][t] - mm);
+        for (int t = 0; t < TPL; ++t) se += __builtin_amdgcn_exp2f(lg[e][t] - mm);
         if constexpr (GP == 2) se += __shfl_xor(se, 32, WAVE);
         if constexpr (GP == 1) {
             se += __shfl_xor(se, 16, WAVE);
             se += __shfl_xor(se, 32, WAVE);
         }
-        S[e] = acc.qmu[e] + (m + __logf(se));
+        lse[e] = 0.69314718055994531f * (m + __builtin_amdgcn_logf(se));
+    }
+}
+
+// CLSE: acc.qt carries scale log2 e, so |q~|^2 takes p.iso_k = iso_coef / (scale log2 e)^2.
+template <int RP, int CBITS, int G, bool CLSE>
+__device__ __forceinline__ void r8_tile_tail(const R8Params& p,
+                                             const R8GroupC<R8Split<G>::TPL * RP * CBITS / 8>& b,
+                                             const R8Scales<RP, R8Split<G>::TPL>& sc,
+                                             const R8Acc<RP>& acc, int req, int h, int page,
+                                             bool valid, int pair, int part, int kg, int sl,
+                                             float qsq0, float qsq1) {
+    constexpr int TPL = R8Split<G>::TPL;
+    constexpr int GP = R8Split<G>::GP;
+    float lse[2];
+    r8_lse<RP, CBITS, G>(b, sc, acc, page * p.page + part * TPL, sl, lse);
+    float S[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        S[e] = acc.qmu[e] + lse[e];
         if constexpr (CLSE) {
             float qh = 0.f;
 #pragma unroll
-            for (int k = 0; k < RP; ++k) qh += acc.qt[e][k] * acc.qt[e][k];
-            S[e] += fmaxf((e ? qsq1 : qsq0) - qh, 0.f) * sc.resid * p.iso_coef;
+            for (int k = 0; k < RP; ++k) qh = fmaf(acc.qt[e][k], acc.qt[e][k], qh);
+            S[e] += fmaxf((e ? qsq1 : qsq0) * p.iso_coef - qh * p.iso_k, 0.f) * sc.resid;
         }
     }
     if (CLSE && p.combine == 1) {             // per-head scores (the nrm combine's input)

@@ -90,6 +90,12 @@ __device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
 template <int RP>
 __device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) {
     constexpr int PP = group_pages<RP>();
+    if constexpr (PP >= 4) {            // r' <= 4: one lane permute per group
+#pragma unroll
+        for (int j = 0; j < RP; ++j)
+            gb[j] = __shfl(blk_own, (threadIdx.x & 48) + (n / RP) * RP + j, WAVE);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < RP; ++j) {
         int b = __builtin_amdgcn_readlane(blk_own, j);
