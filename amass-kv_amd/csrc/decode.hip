@@ -245,8 +245,9 @@ __device__ __forceinline__ int unit_count(const amass_decode_args& a, int r, int
 //   whole (one head per workgroup): the group's nh heads get a workgroup each, whose
 //     waves split the head's pages and merge through LDS into the output (no partials).
 //     Path 2 (the fused single pass), and path 0 when the batch is latency-bound (on
-//     average <= DEC_WHOLE_PPS pages per resident workgroup): the merge launch it saves
-//     costs more than the streaming it loses.
+//     average <= DEC_WHOLE_PPS pages per resident workgroup) and its longest unit over
+//     the workgroup's waves takes at most two page steps more than a split would: the
+//     merge launch it saves costs more than the streaming it loses.
 //   split (one wave per head): S_r = min(smax, max(1, ceil(W_r / tpw))) workgroups, split
 //     s taking pages s, s + S_r, ... of every head; S_r > 1 writes LSE partials.  The
 //     waves of a workgroup read the slices of different heads of (often) the same blocks,
@@ -317,11 +318,15 @@ __device__ __forceinline__ void plan_setup(const amass_decode_args& a, int w0, i
         total += wave_sum_uniform(w);
         wmax = max(wmax, wave_max_uniform(w));
     }
-    if (total <= DEC_WHOLE_PPS * target) {
+    int lo = max(a.pps_min, (total + target - 1) / target);
+    // whole: a batch that cannot fill the resident workgroups, unless its longest unit
+    // spread over one workgroup's waves takes more page steps than a split (lo pages)
+    // plus the merge would -- few units with many pages (e.g. one request's dense
+    // decode) stream faster split
+    if (total <= DEC_WHOLE_PPS * target && (wmax + hw - 1) / hw <= lo + 2) {
         whole = true;
         return;
     }
-    int lo = max(a.pps_min, (total + target - 1) / target);
     if (plan_total(a, w0, kh0, hw, lo, smax) <= target) {   // uniform batches
         tpw = lo;
         return;

@@ -573,7 +573,9 @@ def run_config4(args, boost="sigma", steps=64):
     hot buffer is for).  Each step = quad score + coverage select, residency plan, fetch
     (the fetch kernel, or the copy engine on a side stream after a host-side run plan),
     tiered decode; each phase is timed with HIP events (plan + host run planning for the
-    copy engine: wall clock, it synchronises).  Host bytes = miss pages x 4 KiB."""
+    copy engine: wall clock, it synchronises).  Host bytes = miss pages x 4 KiB; the host
+    link rate is taken over fetch + tiered decode, since misses that find no hot slot are
+    read by the decode itself from the mapped pool."""
     import torch
 
     from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
@@ -674,7 +676,7 @@ def run_config4(args, boost="sigma", steps=64):
                  selected_pages_per_step=round(sel / n_done, 1),
                  miss_pages_per_step=round(miss / n_done, 1),
                  host_bytes_per_step=int(hb),
-                 host_link_gb_s=round(hb / max(r["fetch"], 1e-3) / 1e3, 2),
+                 host_link_gb_s=round(hb / max(r["fetch"] + r["decode"], 1e-3) / 1e3, 2),
                  us_per_step=round(sum(r[k] for k in ("select", "plan", "fetch", "decode")),
                                    1),
                  wall_us_per_step=round(wall, 1))
