@@ -114,7 +114,7 @@ def test_sparse_decode_head_layouts(n_kv, G, path):
 
 
 @pytest.mark.parametrize("G", [4, 8])
-@pytest.mark.parametrize("path", ["split", "fused"])
+@pytest.mark.parametrize("path", ["split", "fused", "auto"])
 def test_dense_decode(G, path):
     announce(f"dense decode G={G} path={path}")
     case = _case(4, G, seed=40 + G)
@@ -129,6 +129,28 @@ def test_dense_decode(G, path):
                        st, out, scale=case.scale, path=path)
     torch.cuda.synchronize()
     got = npf(out)
+    assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("ctx", [4096, 16384])
+def test_dense_decode_one_long_request(ctx):
+    """path "auto" with one request of many pages (config 0's dense baseline shape and
+    beyond): the plan splits the few long units over many workgroups (LSE partials and
+    the merge) instead of one workgroup per head; matches the fp64 oracle."""
+    announce(f"dense decode one request ctx={ctx}")
+    case = make_case(B=1, ctx=(ctx, ctx), n_kv=8, G=4, heavy=0.0, table="perm", seed=90)
+    q, K, V, bt, sl = _np_inputs(case)
+    ref = odec.attend(q, K, V, bt, sl, scale=case.scale, G=4, dense=True)
+    kv = case.kv_cache.to(DEV)
+    st = _St()
+    st.max_reqs, st.n_kv, st.G, st.D = 1, 8, 4, 128
+    ensure_stage_b_buffers(st, DEV)
+    out = torch.full((1, 32, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    dense_paged_decode(case.q.to(DEV), kv, case.block_table.to(DEV), case.seq_lens.to(DEV),
+                       st, out, scale=case.scale, path="auto")
+    torch.cuda.synchronize()
+    got = npf(out)
+    assert np.isfinite(got).all()
     assert np.allclose(got, ref, atol=ATOL, rtol=RTOL), float(np.abs(got - ref).max())
 
 
