@@ -7,11 +7,13 @@ Buffers and invariants follow the reference ``tier/residency.py:281-577``:
   slot2page  (L, n_kv, S)  int32    block in a slot or -1   (I3: mutual inverses)
   lru_clock  (L, n_kv, S)  int32    last step a slot was touched / claimed
   pool_valid (L, n_kv, NB) int8     block's V is in the pinned pool
-  clock (1,), overflow (1,)         step clock, hot-buffer exhaustion latch
+  clock (1,), overflow (1,)         step clock (a view of a 2-element buffer whose second
+                                    word the plan launch uses), hot-buffer exhaustion latch
   miss_pages / victim_slots (R, n_kv, MP), miss_cnt (R, n_kv), fetch_list (FCAP, 3),
   fetch_cnt (1,), first_pos (n_kv, NB) (dedup scratch, INT32_MAX at rest)
 
-``gather_plan`` (one launch chain: clock, hits/misses, victims) and ``gather_fetch``
+``gather_plan`` (two launches: hits/misses, then the victims, whose last workgroup
+advances the clock) and ``gather_fetch``
 (flat fetch kernel) are the HIP entry points ``amass_tier_gather_plan`` and
 ``amass_tier_fetch``; both are fixed-shape, host-sync free and graph capturable.
 ``build_dma_plan`` / ``issue_dma_plan`` are the host-planned copy-engine alternative
@@ -46,7 +48,9 @@ class Residency:
         self.slot2page = torch.full((num_layers, n_kv, hot_slots), -1, dtype=i32, device=dev)
         self.lru_clock = torch.zeros((num_layers, n_kv, hot_slots), dtype=i32, device=dev)
         self.pool_valid = torch.zeros((num_layers, n_kv, num_blocks), dtype=i8, device=dev)
-        self.clock = torch.ones((1,), dtype=i32, device=dev)
+        # [step clock, the plan launch's arrival count (zero between calls)]
+        self._clock2 = torch.tensor([1, 0], dtype=i32, device=dev)
+        self.clock = self._clock2[:1]
         self.overflow = torch.zeros((1,), dtype=i32, device=dev)
         self.miss_pages = torch.zeros((max_reqs, n_kv, max_pages), dtype=i32, device=dev)
         self.miss_cnt = torch.zeros((max_reqs, n_kv), dtype=i32, device=dev)
@@ -83,7 +87,7 @@ class Residency:
             block_table=ptr(block_table), bt_st=block_table.stride(0),
             seq_lens=ptr(seq_lens), page2slot=ptr(self.page2slot[layer]),
             slot2page=ptr(self.slot2page[layer]), lru_clock=ptr(self.lru_clock[layer]),
-            clock=ptr(self.clock), miss_pages=ptr(self.miss_pages),
+            clock=ptr(self._clock2), miss_pages=ptr(self.miss_pages),
             miss_cnt=ptr(self.miss_cnt), victim_slots=ptr(self.victim_slots),
             overflow=ptr(self.overflow), fetch_list=ptr(self.fetch_list),
             fetch_cnt=ptr(self.fetch_cnt), first_pos=ptr(self.first_pos),

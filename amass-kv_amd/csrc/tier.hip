@@ -8,9 +8,11 @@
 // the slots not touched this step by (lru clock, slot index) and give the k-th DISTINCT
 // new miss (in request, position order) the k-th slot.  The victim kernel does exactly
 // that with one workgroup per kv-head: a dedup pass (atomicMin of the first flat position
-// per physical block), a block scan that ranks the first occurrences, a stable 1-bit LSD
-// radix sort of the untouched slot ids by clock (only over the bits the clocks use), and a
-// parallel apply.  No serial per-miss loop remains.
+// per physical block), a block scan that ranks the first occurrences, an ordering of the
+// untouched slots by (clock, slot) -- a histogram cut plus a rank count
+// over the slots the new misses need, or a stable radix sort of all of them -- and a
+// parallel apply.  No serial per-miss loop remains.  The step's clock is clock[0] + 1; the
+// victims launch's last workgroup stores it (no separate clock launch).
 #include "common.h"
 
 namespace amass {
@@ -21,12 +23,6 @@ constexpr int TP_MAXS = 8192;
 constexpr int TP_MAXREQ = 1024;
 constexpr int MD_THREADS = 256;
 
-__global__ void tier_clock_kernel(int32_t* clock, int32_t* fetch_cnt) {
-    if (threadIdx.x == 0) {
-        clock[0] += 1;
-        fetch_cnt[0] = 0;
-    }
-}
 
 template <int NT>
 __device__ __forceinline__ int blk_excl_scan(int v, int* red, int& total) {
@@ -58,7 +54,8 @@ __global__ __launch_bounds__(MD_THREADS) void miss_diff_kernel(const amass_tier_
     const int kv = blockIdx.x, r = blockIdx.y;
     const int n = a.page_cnt[(int64_t)r * a.pc_sr + kv];
     const int sl = a.seq_lens[r];
-    const int clk = a.clock[0];
+    const int clk = a.clock[0] + 1;                    // this step's clock
+    if (kv == 0 && r == 0 && threadIdx.x == 0) a.fetch_cnt[0] = 0;
     const int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kv * a.pt_sh;
     const int32_t* bt = a.block_table + (int64_t)r * a.bt_st;
     int32_t* mp = a.miss_pages + ((int64_t)r * a.n_kv + kv) * a.max_pages;
@@ -91,9 +88,13 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     __shared__ int off[TP_MAXREQ + 1];
     __shared__ uint16_t sb[2][TP_MAXS];
     __shared__ int red[TP_WAVES];
-    __shared__ int smax_s[TP_WAVES];
+    __shared__ int smax_s[TP_WAVES], smin_s[TP_WAVES];
+    __shared__ int hist[256], cum[256];
+    __shared__ uint32_t cand[TP_THREADS];
+    __shared__ int sel_bin, sel_quota;
     const int kv = blockIdx.x, tid = threadIdx.x;
-    const int clk = a.clock[0];
+    const int clk = a.clock[0] + 1;                    // this step's clock
+    if (a.n_req == 0 && kv == 0 && tid == 0) a.fetch_cnt[0] = 0;   // (else: miss_diff's)
     const int S = a.slots;
     const int64_t mbase_kv = (int64_t)kv * a.max_pages;
     int32_t* fp = a.first_pos + (int64_t)kv * a.nb;
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     if (tid < a.n_req) off[tid] = o;
     if (tid == 0) off[a.n_req] = M;
     __syncthreads();
-    if (M == 0) return;
+    if (M > 0) {                                       // uniform
 
     const int C = (M + TP_THREADS - 1) / TP_THREADS;
     const int f0 = min(tid * C, M), f1 = min(f0 + C, M);
@@ -151,46 +152,144 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     int Mnew;
     const int rank0 = blk_excl_scan<TP_THREADS>(nfirst, red, Mnew);
 
-    // 4. untouched slots in slot order, then a stable radix sort by clock
+    // 4. the order of the untouched slots by (clock, slot).  Only the first Mnew are
+    // used: when they all lie within 255 clock values of the oldest untouched clock and
+    // Mnew <= TP_THREADS, a 256-bin histogram of clock - cmin finds the bin B holding the
+    // Mnew-th slot, the slots of the bins below B and the first ones of bin B (slot order)
+    // are gathered as (clock - cmin) << 13 | slot keys, and each is placed by counting the
+    // smaller keys.  Otherwise (wide clock ranges, more new misses than threads, or fewer
+    // untouched slots than new misses) all untouched slots are sorted: a stable 1-bit LSD
+    // radix sort by clock over the bits the clocks use.
+    constexpr int SPT = TP_MAXS / TP_THREADS;          // slots per thread (S <= TP_MAXS)
     const int CS = (S + TP_THREADS - 1) / TP_THREADS;
     const int s0 = min(tid * CS, S), s1 = min(s0 + CS, S);
-    int nun = 0, kmax = 0;
-    for (int s = s0; s < s1; ++s) {
-        const int c = lru[s];
-        if (c < clk) { ++nun; kmax = max(kmax, c); }
+    int cl[SPT];
+    int nun = 0, kmax = 0, kmin = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        const int sidx = s0 + i;
+        cl[i] = (i < CS && sidx < s1) ? lru[sidx] : clk;    // clk: not a candidate
+        if (cl[i] < clk) {
+            ++nun;
+            kmax = max(kmax, cl[i]);
+            kmin = min(kmin, cl[i]);
+        }
     }
     int U;
     int upos = blk_excl_scan<TP_THREADS>(nun, red, U);
-    for (int s = s0; s < s1; ++s)
-        if (lru[s] < clk) sb[0][upos++] = (uint16_t)s;
     {
-        int km = kmax;
+        int km = kmax, kn = kmin;
 #pragma unroll
-        for (int o2 = 32; o2 >= 1; o2 >>= 1) km = max(km, __shfl_xor(km, o2, WAVE));
-        if ((tid & 63) == 0) smax_s[tid >> 6] = km;
+        for (int o2 = 32; o2 >= 1; o2 >>= 1) {
+            km = max(km, __shfl_xor(km, o2, WAVE));
+            kn = min(kn, __shfl_xor(kn, o2, WAVE));
+        }
+        if ((tid & 63) == 0) {
+            smax_s[tid >> 6] = km;
+            smin_s[tid >> 6] = kn;
+        }
     }
+    if (tid < 256) hist[tid] = 0;
     __syncthreads();
-    int kall = 0;
+    int kall = 0, cmin = 0x7FFFFFFF;
 #pragma unroll
-    for (int i = 0; i < TP_WAVES; ++i) kall = max(kall, smax_s[i]);
-    const int nbits = kall > 0 ? 32 - __clz(kall) : 0;
-    const int CU = (U + TP_THREADS - 1) / TP_THREADS;
-    const int u0 = min(tid * CU, U), u1 = min(u0 + CU, U);
-    for (int b = 0; b < nbits; ++b) {
-        const uint16_t* cur = sb[b & 1];
-        uint16_t* nxt = sb[(b + 1) & 1];
-        int nz = 0;
-        for (int i = u0; i < u1; ++i) nz += ((lru[cur[i]] >> b) & 1) == 0;
-        int Z;
-        int zb = blk_excl_scan<TP_THREADS>(nz, red, Z);
-        for (int i = u0; i < u1; ++i) {
-            const uint16_t s = cur[i];
-            if (((lru[s] >> b) & 1) == 0) nxt[zb++] = s;
-            else nxt[Z + (i - zb)] = s;
+    for (int i = 0; i < TP_WAVES; ++i) {
+        kall = max(kall, smax_s[i]);
+        cmin = min(cmin, smin_s[i]);
+    }
+    const uint16_t* sorted = sb[0];
+    bool fast = U >= Mnew && Mnew <= TP_THREADS;
+    if (fast) {
+#pragma unroll
+        for (int i = 0; i < SPT; ++i)
+            if (cl[i] < clk) atomicAdd(&hist[min(cl[i] - cmin, 255)], 1);
+        __syncthreads();
+        // inclusive scan of the 256 bins (first four waves), then B = the first bin whose
+        // running count reaches Mnew and the quota taken from it
+        const int lane = tid & 63, w = tid >> 6;
+        int x = tid < 256 ? hist[tid] : 0;
+#pragma unroll
+        for (int o2 = 1; o2 < 64; o2 <<= 1) {
+            const int y = __shfl_up(x, o2, WAVE);
+            if (lane >= o2) x += y;
+        }
+        if (tid < 256 && lane == 63) red[w] = x;
+        __syncthreads();
+        if (tid < 256) {
+            int base = 0;
+            for (int i = 0; i < w; ++i) base += red[i];
+            cum[tid] = base + x;
         }
         __syncthreads();
+        if (tid < 256) {
+            const int incl = cum[tid], excl = tid ? cum[tid - 1] : 0;
+            if (excl < Mnew && incl >= Mnew) {
+                sel_bin = tid;
+                sel_quota = Mnew - excl;
+            }
+        }
+        __syncthreads();
+        const int B = sel_bin, quota = sel_quota;
+        fast = B < 255;                               // uniform
+        if (fast) {
+            // ranks in slot order of this thread's bin-B slots
+            int nb = 0;
+#pragma unroll
+            for (int i = 0; i < SPT; ++i) nb += (cl[i] < clk && cl[i] - cmin == B) ? 1 : 0;
+            int tb;
+            const int rb0 = blk_excl_scan<TP_THREADS>(nb, red, tb);
+            bool take[SPT];
+            int nsel = 0, rb = rb0;
+#pragma unroll
+            for (int i = 0; i < SPT; ++i) {
+                const int rel = cl[i] - cmin;
+                take[i] = false;
+                if (cl[i] < clk) {
+                    if (rel < B) take[i] = true;
+                    else if (rel == B) take[i] = rb++ < quota;
+                }
+                nsel += take[i] ? 1 : 0;
+            }
+            int tsel;
+            int cp = blk_excl_scan<TP_THREADS>(nsel, red, tsel);   // tsel == Mnew
+#pragma unroll
+            for (int i = 0; i < SPT; ++i)
+                if (take[i]) cand[cp++] = ((uint32_t)(cl[i] - cmin) << 13) | (uint32_t)(s0 + i);
+            __syncthreads();
+            if (tid < Mnew) {
+                const uint32_t key = cand[tid];
+                int rank = 0;
+                for (int j = 0; j < Mnew; ++j) rank += cand[j] < key ? 1 : 0;
+                sb[0][rank] = (uint16_t)(key & 0x1FFFu);
+            }
+            __syncthreads();
+        }
     }
-    const uint16_t* sorted = sb[nbits & 1];
+    if (!fast) {
+        for (int i = 0; i < SPT; ++i) {
+            const int sidx = s0 + i;
+            if (cl[i] < clk) sb[0][upos++] = (uint16_t)sidx;
+        }
+        __syncthreads();
+        const int nbits = kall > 0 ? 32 - __clz(kall) : 0;
+        const int CU = (U + TP_THREADS - 1) / TP_THREADS;
+        const int u0 = min(tid * CU, U), u1 = min(u0 + CU, U);
+        for (int b = 0; b < nbits; ++b) {
+            const uint16_t* cur = sb[b & 1];
+            uint16_t* nxt = sb[(b + 1) & 1];
+            int nz = 0;
+            for (int i = u0; i < u1; ++i) nz += ((lru[cur[i]] >> b) & 1) == 0;
+            int Z;
+            int zb = blk_excl_scan<TP_THREADS>(nz, red, Z);
+            for (int i = u0; i < u1; ++i) {
+                const uint16_t sv = cur[i];
+                if (((lru[sv] >> b) & 1) == 0) nxt[zb++] = sv;
+                else nxt[Z + (i - zb)] = sv;
+            }
+            __syncthreads();
+        }
+        sorted = sb[nbits & 1];
+    }
 
     // 5. apply: the k-th new miss takes sorted[k]; duplicates and overflow get -1
     {
@@ -232,6 +331,18 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         for (int f = f0; f < f1; ++f) {
             locate(f, r);
             fp[*miss_at(r, f)] = 0x7FFFFFFF;
+        }
+    }
+    }
+    // the last workgroup to finish advances the clock (every workgroup has read it) and
+    // clears the arrival count for the next call
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(&a.clock[1], 1, __ATOMIC_ACQ_REL,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (int)gridDim.x - 1) {
+            __hip_atomic_store(&a.clock[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.clock[0], clk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -280,12 +391,13 @@ extern "C" int amass_tier_gather_plan(const amass_tier_plan_args* a, void* strea
         return AMASS_ERR_GEOMETRY;
     if (a->slots > TP_MAXS || a->n_req > TP_MAXREQ) return AMASS_ERR_CAPACITY;
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(tier_clock_kernel, dim3(1), dim3(64), 0, s, a->clock, a->fetch_cnt);
     int rc = check_launch();
-    if (rc || a->n_req == 0) return rc;
-    hipLaunchKernelGGL(miss_diff_kernel, dim3(a->n_kv, a->n_req), dim3(MD_THREADS), 0, s, *a);
-    rc = check_launch();
     if (rc) return rc;
+    if (a->n_req > 0) {          // (with no requests the victims launch alone advances the clock)
+        hipLaunchKernelGGL(miss_diff_kernel, dim3(a->n_kv, a->n_req), dim3(MD_THREADS), 0, s, *a);
+        rc = check_launch();
+        if (rc) return rc;
+    }
     hipLaunchKernelGGL(victims_kernel, dim3(a->n_kv), dim3(TP_THREADS), 0, s, *a);
     return check_launch();
 }

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 8
+#define AMASS_ABI_VERSION 9
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -297,7 +297,10 @@ int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
  * (resident: its LRU clock is touched) or a miss; per kv-head the distinct new misses, in
  * (request, position) order, take the least-recently-used slots not touched this step
  * (ties -> lower slot), evicting their old pages; installed misses are appended to the
- * flat fetch list (kv, blk, slot).  clock is advanced by one on device first. */
+ * flat fetch list (kv, blk, slot).  The step uses clock[0] + 1 and leaves it in clock[0]
+ * (two launches; the victims launch's last workgroup advances it).  clock[1] is that
+ * launch's arrival count: zero when the buffer is allocated, and every call leaves it
+ * zero. */
 typedef struct amass_tier_plan_args {
     const int32_t* page_table; int64_t pt_sr, pt_sh;
     const int32_t* page_cnt;   int64_t pc_sr;
@@ -306,7 +309,7 @@ typedef struct amass_tier_plan_args {
     int32_t* page2slot;      /* (n_kv,NB) this layer   */
     int32_t* slot2page;      /* (n_kv,S) this layer    */
     int32_t* lru_clock;      /* (n_kv,S) this layer    */
-    int32_t* clock;          /* (1,)                   */
+    int32_t* clock;          /* (2,) step clock, arrival count */
     int32_t* miss_pages;     /* (R,n_kv,MP) scratch    */
     int32_t* miss_cnt;       /* (R,n_kv)               */
     int32_t* victim_slots;   /* (R,n_kv,MP)            */

@@ -77,6 +77,57 @@ def test_plan_matches_oracle_over_steps(slots):
         p2s, s2p, lru, clock = ref["page2slot"], ref["slot2page"], ref["lru"], ref["clock"]
 
 
+@pytest.mark.parametrize("slots,span,fill", [(3000, 40, 0.75), (700, 200, 1.0),
+                                            (700, 5000, 1.0)])
+def test_plan_matches_oracle_with_aged_clocks(slots, span, fill):
+    """Victim order over an aged hot buffer: slots already hold pages with LRU clocks
+    spread over `span` steps (clocks within 255 of the oldest take the histogram path,
+    wider spans the full radix sort), more slots than threads per kv head (3000), and
+    repeated clocks (ties broken by slot index), empty slots (clock 0) or a full buffer.
+    Bit-exact against the sequential oracle over four steps."""
+    announce(f"tier plan aged clocks slots={slots} span={span} fill={fill}")
+    case = make_case(B=4, ctx=(2000, 6000), n_kv=8, G=4, heavy=0.0, seed=15)
+    tier = _tier(case, slots)
+    r5 = tier.residency
+    NB = case.kv_cache.shape[0]
+    gen = np.random.default_rng(slots + span)
+    assert NB >= 700
+    p2s = np.full((8, NB), -1, np.int64)
+    s2p = np.full((8, slots), -1, np.int64)
+    lru = np.zeros((8, slots), np.int64)
+    clock = span + 10
+    for kv in range(8):
+        nres = int(min(slots, NB) * fill)
+        blks = gen.choice(NB, nres, replace=False)
+        sl_ = gen.choice(slots, nres, replace=False)
+        p2s[kv, blks] = sl_
+        s2p[kv, sl_] = blks
+        lru[kv, sl_] = gen.integers(clock - span, clock, nres)   # repeats at small spans
+    r5.page2slot[0].copy_(torch.from_numpy(p2s.astype(np.int32)))
+    r5.slot2page[0].copy_(torch.from_numpy(s2p.astype(np.int32)))
+    r5.lru_clock[0].copy_(torch.from_numpy(lru.astype(np.int32)))
+    r5.clock.fill_(clock)
+    bt, sl = case.block_table.to(DEV), case.seq_lens.to(DEV)
+    for step in range(4):
+        tab, cnt = _selection(case, 0.3, seed=10 + step)
+        ref = otier.plan(tab, cnt, npi(case.block_table), npi(case.seq_lens), p2s, s2p, lru,
+                         clock, page=16)
+        r5.overflow.zero_()
+        r5.gather_plan(0, torch.from_numpy(tab).to(DEV), torch.from_numpy(cnt).to(DEV), bt, sl,
+                       4)
+        torch.cuda.synchronize()
+        assert int(r5.clock[0]) == ref["clock"]
+        assert np.array_equal(npi(r5.page2slot[0]), ref["page2slot"])
+        assert np.array_equal(npi(r5.slot2page[0]), ref["slot2page"])
+        assert np.array_equal(npi(r5.lru_clock[0]), ref["lru"])
+        assert bool(r5.overflow[0]) == ref["overflow"]
+        vs = npi(r5.victim_slots)
+        for r in range(4):
+            for kv in range(8):
+                assert list(vs[r, kv, :len(ref["miss"][r][kv])]) == ref["victims"][r][kv]
+        p2s, s2p, lru, clock = ref["page2slot"], ref["slot2page"], ref["lru"], ref["clock"]
+
+
 @pytest.mark.parametrize("fetch", ["kernel", "dma", "off"])
 def test_tiered_decode_bitexact_vs_resident(fetch):
     announce(f"tiered decode fetch={fetch}")
