@@ -201,8 +201,17 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     bool fast = U >= Mnew && Mnew <= TP_THREADS;
     if (fast) {
 #pragma unroll
-        for (int i = 0; i < SPT; ++i)
-            if (cl[i] < clk) atomicAdd(&hist[min(cl[i] - cmin, 255)], 1);
+        for (int i = 0; i < SPT; ++i) {
+            // a wave whose 64 lanes share a bin adds once (a cold buffer puts every slot
+            // in bin 0)
+            const int bin = cl[i] < clk ? min(cl[i] - cmin, 255) : -1;
+            const int b0 = __builtin_amdgcn_readfirstlane(bin);
+            if (__ballot(bin == b0) == ~0ull) {
+                if (b0 >= 0 && (tid & 63) == 0) atomicAdd(&hist[b0], WAVE);
+            } else if (bin >= 0) {
+                atomicAdd(&hist[bin], 1);
+            }
+        }
         __syncthreads();
         // inclusive scan of the 256 bins (first four waves), then B = the first bin whose
         // running count reaches Mnew and the quota taken from it
