@@ -128,6 +128,30 @@ def test_plan_matches_oracle_with_aged_clocks(slots, span, fill):
         p2s, s2p, lru, clock = ref["page2slot"], ref["slot2page"], ref["lru"], ref["clock"]
 
 
+def test_plan_without_requests_advances_the_clock():
+    """A plan over zero requests changes no map, installs nothing, and still advances the
+    step clock (the victims launch runs alone and its last workgroup stores it)."""
+    announce("tier plan with no requests")
+    case = make_case(B=2, ctx=(500, 900), n_kv=8, G=4, heavy=0.0, seed=3)
+    tier = _tier(case, 64)
+    r5 = tier.residency
+    bt, sl = case.block_table.to(DEV), case.seq_lens.to(DEV)
+    tab, cnt = _selection(case, 0.5, seed=1)
+    r5.gather_plan(0, torch.from_numpy(tab).to(DEV), torch.from_numpy(cnt).to(DEV), bt, sl, 2)
+    torch.cuda.synchronize()
+    before = [npi(x).copy() for x in (r5.page2slot, r5.slot2page, r5.lru_clock)]
+    clk = int(r5.clock[0])
+    r5.fetch_cnt.fill_(5)
+    for i in range(3):
+        r5.gather_plan(0, torch.from_numpy(tab).to(DEV), torch.from_numpy(cnt).to(DEV), bt,
+                       sl, 0)
+        torch.cuda.synchronize()
+        assert int(r5.clock[0]) == clk + 1 + i
+        assert int(r5._clock2[1]) == 0 and int(r5.fetch_cnt[0]) == 0
+    for x, y in zip(before, (r5.page2slot, r5.slot2page, r5.lru_clock)):
+        assert np.array_equal(x, npi(y))
+
+
 @pytest.mark.parametrize("fetch", ["kernel", "dma", "off"])
 def test_tiered_decode_bitexact_vs_resident(fetch):
     announce(f"tiered decode fetch={fetch}")
