@@ -11,9 +11,12 @@ config 1: the headline shape at its full batch -- B = 32, 16384-token contexts (
           reference's defaults (r'=2, int4 V and coordinates) at the same shape;
 config 2: r8 score, 6 ragged sequences spanning 2048..65536 tokens, fixed 5 % budget,
           random pool block tables -> r8 int32 sums exact, scores 1e-3, page sets exact,
-          decode 2e-2 / 1e-2;
+          decode 2e-2 / 1e-2; and the benched full batch (64 sequences): scores of three
+          requests, all page tables, top-b properties, decode, graph replay == eager;
 config 3: 70B GQA shape (G = 8), 131072-token contexts (8192 pages), 2 % heavy pages,
-          quad r'=8 nrm, coverage 0.95 -> scores 1e-3, page sets exact, decode;
+          quad r'=8 nrm, coverage 0.95 -> scores 1e-3, page sets exact, decode; and the
+          benched full batch (B = 8) with the same checks plus the coverage properties
+          and graph replay == eager;
 config 4: mem-v, 32768-token contexts, hot buffer = 10 % of the pages per kv head,
           64 decode steps with a fresh query each step: every step's tiered decode is
           bit-identical to the resident decode of the same selection, the residency plan
@@ -286,6 +289,117 @@ def test_config3_g8_131k_coverage():
                               max_pages=MP, mode=1, coverage=0.95, score_kind=1)
     assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)
     _decode_check(case, st, range(B))
+
+
+def _topb_properties(st, sink=1, window=1):
+    """Top-b with the index tie rule: every unit keeps its sinks and window and exactly b
+    selectable pages, ascending with -1 padding, and no dropped selectable page scores
+    above a kept one (ties at the cut go to the lower page index)."""
+    sc, tab, cnt = npf(st.score), npi(st.page_table), npi(st.page_cnt)
+    nsh, npg, bfix = npi(st.n_sel_hi), npi(st.n_pages), npi(st.b_fix)
+    for r in range(sc.shape[0]):
+        n, S = int(nsh[r]), int(nsh[r]) - sink
+        if S <= 1:
+            continue
+        b = min(max(int(bfix[r]), 1), S)
+        for kh in range(sc.shape[1]):
+            c = int(cnt[r, kh])
+            assert c == b + sink + (int(npg[r]) - n), (r, kh, c, b)
+            pages = tab[r, kh, :c]
+            assert np.all(np.diff(pages) > 0) and np.all(tab[r, kh, c:] == -1)
+            sel = pages[(pages >= sink) & (pages < n)]
+            rest = np.setdiff1d(np.arange(sink, n), sel)
+            if rest.size:
+                lo_kept = sc[r, kh, sel].min()
+                assert sc[r, kh, rest].max() <= lo_kept, (r, kh)
+                tied = rest[sc[r, kh, rest] == lo_kept]
+                assert tied.size == 0 or tied.min() > sel[sc[r, kh, sel] == lo_kept].max()
+
+
+def test_config2_full_batch():
+    """Config 2 at its full batch, the benched workload: 64 ragged sequences (2928..65104
+    tokens), r8 r=8 int8, top-b 5 %.  Scores of three requests against the oracle over
+    their own blocks, the page tables of all 64 on the GPU's scores, the top-b properties,
+    the decode of two requests, and four graph replays of the step equal to eager."""
+    announce("config 2 full batch: B=64 ragged, r8, top-b 5%")
+    case = config_case(2, seed=2, device=DEV)
+    B, MP = case.q.shape[0], case.max_pages
+    assert B == 64
+    st = build_r8_state(case, rank=8, vk_bits=8, c_bits=8, budget=0.05)
+    from amass.selection import select_pages_r8
+    out = torch.zeros(B, 32, 128, dtype=torch.bfloat16, device=DEV)
+    vsrc = ResidentVSource(case.kv_cache)
+    derive_page_params(st, case.seq_lens, B)
+
+    def step():
+        select_pages_r8(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                        derive=False)
+        sparse_paged_decode_batched(case.q, case.kv_cache, case.block_table, case.seq_lens,
+                                    st, out, vsrc, scale=case.scale)
+
+    step()
+    torch.cuda.synchronize()
+    mu, mus, _, Vks, c, cs, _ = st.layer_state(0)
+    Vk = st.reference_Vk(0)
+    nsh = npi(st.n_sel_hi)
+    lens = npi(case.seq_lens)
+    rows = [int(np.argmin(lens)), int(np.argmax(lens)), 17]
+    for r in rows:
+        n = int(nsh[r])
+        idx, bt = _row_blocks(case, r, n)
+        ref = osc.r8_score(npf(case.q[r:r + 1]), npi(mu[idx]), npf(mus[idx]), npi(Vk[idx]),
+                           npf(Vks[idx]), npi(c[idx]), npf(cs[idx]), bt, lens[r:r + 1],
+                           np.array([n]), scale=case.scale, page=16, G=4, vk_bits=8,
+                           c_bits=8, max_pages=n)
+        assert rel_close(npf(st.score[r, :, :n]), ref[0], 1) <= 1e-3, r
+    tab, cnt, _ = osel.select(npf(st.score), npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                              max_pages=MP, mode=0)
+    assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)
+    _topb_properties(st)
+    _decode_check(case, st, rows[:2])
+    _graph_replay_equals_eager(step, [out, st.page_table, st.page_cnt])
+
+
+def test_config3_full_batch():
+    """Config 3 at its full batch, the benched workload: B = 8, 131072-token contexts
+    (8192 pages), G = 8, quad r'=8 int8 nrm, coverage 0.95 -- the nrm pre-pass and the
+    1024-thread selection.  Per-head scores of one request against the oracle, the page
+    tables of all 8 on the GPU's scores, the coverage properties, the decode of two
+    requests, and four graph replays of the step equal to eager."""
+    announce("config 3 full batch: B=8, 131072 tokens, G=8, coverage 0.95")
+    case = config_case(3, seed=3, device=DEV)
+    B, MP = case.q.shape[0], case.max_pages
+    assert B == 8 and MP == 8192
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", coverage=0.95)
+    out = torch.zeros(B, 64, 128, dtype=torch.bfloat16, device=DEV)
+    vsrc = ResidentVSource(case.kv_cache)
+    derive_page_params(st, case.seq_lens, B)
+
+    def step():
+        select_pages_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                          derive=False)
+        sparse_paged_decode_batched(case.q, case.kv_cache, case.block_table, case.seq_lens,
+                                    st, out, vsrc, scale=case.scale)
+
+    step()
+    torch.cuda.synchronize()
+    mu, mus, _, Vs, sg, _ = st.layer_state(0)
+    V = st.reference_V(0)
+    nsh = npi(st.n_sel_hi)
+    r, n = 5, int(nsh[5])
+    idx, bt = _row_blocks(case, r, n)
+    ref_h = osc.quad_score(npf(case.q[r:r + 1]), npi(mu[idx]), npf(mus[idx]), npi(V[idx]),
+                           npf(Vs[idx]), npf(sg[idx]), bt, np.array([n]), scale=case.scale,
+                           page=16, G=8, v_bits=8, max_pages=n, combine="nrm")
+    assert rel_close(npf(st.score_h[r, :, :, :n]), ref_h[0], 1) <= 1e-3
+    ref_n = osc.nrm_combine(npf(st.score_h).astype(np.float64), nsh)
+    assert rel_close(npf(st.score)[:, :, :n], ref_n[:, :, :n], 1) <= 1e-5
+    tab, cnt, _ = osel.select(npf(st.score), npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                              max_pages=MP, mode=1, coverage=0.95, score_kind=1)
+    assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)
+    _coverage_properties(st)
+    _decode_check(case, st, [0, 7])
+    _graph_replay_equals_eager(step, [out, st.page_table, st.page_cnt])
 
 
 @pytest.mark.parametrize("boost", ["sigma", "keynorm"])
