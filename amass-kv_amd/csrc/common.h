@@ -178,23 +178,25 @@ __device__ __forceinline__ float u2f(uint32_t x) {
 }
 
 // ---------------------------------------------------------------- deterministic exp
-// exp(x) for x <= 0 built only from correctly rounded fp32 +,-,*, rint and ldexp (no FMA
-// contraction), so the host oracle reproduces it bit for bit.  Cody-Waite reduction by
-// ln2 (hi part has 16 trailing zero bits so n*hi is exact), degree-7 Taylor on
-// |r| <= ln2/2, ldexp back.  x <= -80 returns 0 (far below the 2^-32 mass quantum).
+// exp(x) for x <= 0 built only from correctly rounded fp32 +,-,*, rint and ldexp, so the
+// host oracle reproduces it bit for bit.  Cody-Waite reduction by ln2 (hi part has 16
+// trailing zero bits so n*hi is exact), degree-7 Taylor on |r| <= ln2/2, ldexp back.
+// x <= -80 returns 0 (far below the 2^-32 mass quantum).  HIP compiles with FMA
+// contraction on (and its __fmul_rn / __fadd_rn are plain * and +, fused like any
+// other): the pragma keeps every product and sum below separately rounded.
 __device__ __forceinline__ float exp_det(float x) {
+#pragma clang fp contract(off)
     if (!(x > -80.0f)) return 0.0f;
-    const float n = rintf(__fmul_rn(x, 0x1.715476p+0f));
-    const float r = __fsub_rn(__fsub_rn(x, __fmul_rn(n, 0x1.62e400p-1f)),
-                              __fmul_rn(n, 0x1.7f7d1cp-20f));
-    float p = 0x1.a01a02p-13f;                       // 1/5040
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.6c16c2p-10f); // 1/720
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.111112p-7f);  // 1/120
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-5f);  // 1/24
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-3f);  // 1/6
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.000000p-1f);  // 1/2
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    const float n = rintf(x * 0x1.715476p+0f);
+    const float r = (x - n * 0x1.62e400p-1f) - n * 0x1.7f7d1cp-20f;
+    float p = 0x1.a01a02p-13f;           // 1/5040
+    p = p * r + 0x1.6c16c2p-10f;         // 1/720
+    p = p * r + 0x1.111112p-7f;          // 1/120
+    p = p * r + 0x1.555556p-5f;          // 1/24
+    p = p * r + 0x1.555556p-3f;          // 1/6
+    p = p * r + 0x1.000000p-1f;          // 1/2
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
     return ldexpf(p, (int)n);
 }
 

@@ -12,7 +12,7 @@ import torch
 import oracle.select as osel
 from amass.selection import QuadState, coverage_select, derive_page_params, topb_select
 from amass.selection.select import select_pages
-from helpers import announce, npf, npi
+from helpers import announce, mass_cut_case, npf, npi
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -93,6 +93,30 @@ def test_coverage(kind, tie, cov, ties):
     R, MP = 6, 700
     st = _state(R, MP)
     _run(st, R, 1, tie, kind, cov, gen, ties, MP)
+
+
+def test_coverage_cut_on_exact_exp_mass():
+    """Coverage by exp mass (the group-max combine) with the cut exactly on the mass of
+    the top 11 selectable pages: the GPU keeps what the oracle keeps, so every page mass
+    is exp_det's separately rounded value (an FMA anywhere in it moves masses by an ulp
+    and the cut by a page)."""
+    announce("coverage cut on exact exp mass")
+    sc, cov = mass_cut_case(osel.exp_det)
+    R, MP = 1, sc.size
+    st = _state(R, MP)
+    derive_page_params(st, torch.tensor([MP * 16], dtype=torch.int32, device=DEV), R)
+    full = np.broadcast_to(sc, (R, st.n_kv, MP)).copy()
+    st.score.copy_(torch.from_numpy(full).to(DEV))
+    st.combine = "max"
+    coverage_select(st, R, cov, tie_mode="index")
+    torch.cuda.synchronize()
+    ref_tab, ref_cnt, ref_nsel = osel.select(full, npi(st.n_pages), npi(st.n_sel_hi),
+                                             npi(st.b_fix), sink=1, max_pages=MP, mode=1,
+                                             coverage=cov, tie_mode=0, score_kind=0)
+    assert (ref_nsel == 11).all()
+    assert np.array_equal(npi(st.n_sel), ref_nsel)
+    assert np.array_equal(npi(st.page_cnt), ref_cnt)
+    assert np.array_equal(npi(st.page_table), ref_tab)
 
 
 def test_budget_one_keeps_all():

@@ -19,6 +19,7 @@ import oracle.quant as oq
 import oracle.score as osc
 import oracle.select as osel
 import oracle.tier as otier
+from helpers import exp_det_fused, mass_cut_case
 
 
 def _hadamard(n):
@@ -257,6 +258,25 @@ def test_exp_det_accuracy():
     assert np.all(np.abs(got[m] - want[m]) <= 4 * ulp[m])
     assert np.all(got[~m] == 0)
     assert osel.exp_det(np.float32(0.0)) == 1.0
+
+
+def test_mass_cut_case_separates_fused_exp():
+    """The coverage case of the GPU test for exact exp masses is sensitive: with every
+    multiply-add of exp_det fused (a planted mistake, one rounding instead of two) the
+    oracle's nucleus keeps one more page."""
+    sc, cov = mass_cut_case(osel.exp_det)
+    MP = sc.size
+    npg, nsh, b = osel.derive([MP * 16], 0.05, page=16, window=1, sink=1)
+    args = dict(sink=1, max_pages=MP, mode=1, coverage=cov, score_kind=0)
+    _, cnt, nsel = osel.select(sc[None, None], npg, nsh, b, **args)
+    assert int(nsel[0, 0]) == 11
+    real = osel.exp_det
+    try:
+        osel.exp_det = exp_det_fused
+        _, cnt_f, nsel_f = osel.select(sc[None, None], npg, nsh, b, **args)
+    finally:
+        osel.exp_det = real
+    assert int(nsel_f[0, 0]) == 12 and int(cnt_f[0, 0]) == int(cnt[0, 0]) + 1
 
 
 def test_f2u_order_preserving():
