@@ -1,0 +1,174 @@
+"""Property-based GPU parity: selection and sparse decode over generated cases.
+
+hypothesis draws the batch shape, the sequence lengths, the score pattern and the
+selection parameters (derandomized, so every run checks the same examples); each example
+runs the HIP path and compares with the oracle under the same bars as the fixed-case
+tests: page_table / page_cnt / chosen count bit-exact for the selection, outputs within
+2e-2 absolute / 1e-2 relative of the fp64 attention for the decode.
+
+Score patterns target the selection's radix search: i.i.d. normal, a small value pool
+(many exact ties), a run of keys a few ulps apart (every digit of the 32-bit key decides,
+bins of more than 64 candidates), +0.0 / -0.0 mixtures (one tie class), and magnitudes
+over 60 decades.  Page counts span every thread layout of the selection (1..8 pages per
+thread of 512, 8 of 1024, 32 of 512) and the decode's whole / split / fused layouts with
+ragged and empty units and NaN-poisoned slots past each sequence's end.
+"""
+import numpy as np
+import pytest
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as hs
+
+import oracle.decode as odec
+import oracle.select as osel
+from amass.attention import ensure_stage_b_buffers
+from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
+from amass.bench.synth import make_case
+from amass.selection import QuadState, coverage_select, derive_page_params, topb_select
+from helpers import announce, npf, npi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+PROPS = settings(max_examples=25, deadline=None, derandomize=True, database=None,
+                 suppress_health_check=list(HealthCheck))
+
+PATTERNS = ("normal", "ties", "ulps", "zeros", "wide")
+# row widths of every thread layout of the selection: 1, 2, 4 and 8 pages per thread of
+# 512, 8 per thread of 1024, 32 per thread of 512
+MPS = (2, 63, 513, 1024, 2047, 4096, 8192, 8193, 16384)
+
+
+def _scores(rng, shape, pattern):
+    if pattern == "normal":
+        return (rng.standard_normal(shape) * 3).astype(np.float32)
+    if pattern == "ties":
+        pool = np.array([-2.0, 0.5, 0.5, 3.0], np.float32)
+        return pool[rng.integers(0, pool.size, shape)]
+    if pattern == "ulps":
+        base = np.float32(rng.uniform(0.1, 4.0))
+        bits = base.view(np.int32) + rng.integers(0, 300, shape).astype(np.int32)
+        return bits.view(np.float32)
+    if pattern == "zeros":
+        pool = np.array([0.0, -0.0, 0.0, 1.5, -1.0], np.float32)
+        return pool[rng.integers(0, pool.size, shape)]
+    mag = 10.0 ** rng.uniform(-30, 30, shape)
+    return (np.sign(rng.standard_normal(shape)) * mag).astype(np.float32)
+
+
+@hs.composite
+def selection_cases(draw, MP):
+    R = draw(hs.integers(1, 4))
+    n_kv = draw(hs.sampled_from([1, 2, 8]))
+    lens = draw(hs.lists(hs.integers(0, MP * 16), min_size=R, max_size=R))
+    return dict(R=R, n_kv=n_kv, MP=MP, lens=lens,
+                pattern=draw(hs.sampled_from(PATTERNS)),
+                seed=draw(hs.integers(0, 2 ** 31 - 1)),
+                mode=draw(hs.integers(0, 1)), tie=draw(hs.integers(0, 1)),
+                kind=draw(hs.integers(0, 1)),
+                cov=draw(hs.floats(0.01, 1.0)), budget=draw(hs.floats(0.001, 1.0)))
+
+
+@pytest.mark.parametrize("MP", MPS)
+def test_selection_matches_oracle(MP):
+    @PROPS
+    @given(c=selection_cases(MP))
+    def prop(c):
+        _selection_example(c)
+    prop()
+
+
+def _selection_example(c):
+    announce(f"selection property case {c}")
+    R, n_kv, MP = c["R"], c["n_kv"], c["MP"]
+    rng = np.random.default_rng(c["seed"])
+    sc = _scores(rng, (R, n_kv, MP), c["pattern"])
+    st = QuadState(DEV, num_layers=1, num_blocks=4, n_kv=n_kv, G=4, head_dim=128, page=16,
+                   max_reqs=R, max_pages=MP, rank=2, budget=c["budget"],
+                   combine="nrm" if c["kind"] == 1 else "max")
+    derive_page_params(st, torch.tensor(c["lens"], dtype=torch.int32, device=DEV), R)
+    st.score.copy_(torch.from_numpy(sc).to(DEV))
+    st.page_table.fill_(-7)
+    tie = ["index", "all"][c["tie"]]
+    if c["mode"] == 0:
+        topb_select(st, R, tie_mode=tie)
+    else:
+        coverage_select(st, R, c["cov"], tie_mode=tie)
+    torch.cuda.synchronize()
+    npg, nsh, bfix = npi(st.n_pages), npi(st.n_sel_hi), npi(st.b_fix)
+    ref_npg, ref_nsh, ref_b = osel.derive(c["lens"], c["budget"], 16, 1, 1)
+    assert np.array_equal(npg, ref_npg) and np.array_equal(nsh, ref_nsh)
+    assert np.array_equal(bfix, ref_b)
+    tab, cnt, nsel = osel.select(sc, npg, nsh, bfix, sink=1, max_pages=MP, mode=c["mode"],
+                                 coverage=c["cov"], tie_mode=c["tie"], score_kind=c["kind"])
+    assert np.array_equal(npi(st.page_cnt), cnt)
+    assert np.array_equal(npi(st.page_table), tab)
+    if c["tie"] == 0:
+        assert np.array_equal(npi(st.n_sel), nsel)
+
+
+@hs.composite
+def decode_cases(draw, path):
+    n_kv, G = draw(hs.sampled_from([(1, 8), (2, 4), (8, 1), (8, 4), (8, 8)]))
+    return dict(B=draw(hs.integers(1, 5)), n_kv=n_kv, G=G,
+                hi=draw(hs.sampled_from([40, 600, 3000])),
+                shape=draw(hs.sampled_from(["sparse", "ragged", "full"])),
+                path=path, seed=draw(hs.integers(0, 2 ** 31 - 1)))
+
+
+@pytest.mark.parametrize("path", ["auto", "split", "fused"])
+def test_sparse_decode_matches_oracle(path):
+    @PROPS
+    @given(c=decode_cases(path))
+    def prop(c):
+        _decode_example(c)
+    prop()
+
+
+def _decode_example(c):
+    announce(f"decode property case {c}")
+    B, n_kv, G = c["B"], c["n_kv"], c["G"]
+    rng = np.random.default_rng(c["seed"])
+    case = make_case(B=B, ctx=(1, c["hi"]), n_kv=n_kv, G=G, heavy=0.0, table="perm",
+                     seed=c["seed"] % 100003)
+    sl = case.seq_lens - torch.from_numpy(rng.integers(0, 16, B)).to(case.seq_lens.dtype)
+    sl = torch.clamp(sl, min=1).to(torch.int32)
+    for r in range(B):                          # poison the slots past each sequence's end
+        n = int(sl[r])
+        last = (n - 1) // 16
+        if n - last * 16 < 16:
+            case.kv_cache[int(case.block_table[r, last]), :, n - last * 16:] = float("nan")
+    case.seq_lens = sl
+    MP = case.max_pages
+    npg = (npi(sl) + 15) // 16
+    tab = np.full((B, n_kv, MP), -1, np.int32)
+    cnt = np.zeros((B, n_kv), np.int32)
+    for r in range(B):
+        for kh in range(n_kv):
+            P = int(npg[r])
+            if c["shape"] == "full":
+                k = P
+            elif c["shape"] == "sparse":
+                k = int(rng.integers(0, min(P, 4) + 1))
+            else:
+                k = int(rng.integers(0, P + 1))
+            pages = np.sort(rng.choice(P, size=k, replace=False)).astype(np.int32)
+            tab[r, kh, :k] = pages
+            cnt[r, kh] = k
+    q, K, V = npf(case.q), npf(case.kv_cache[:, 0]), npf(case.kv_cache[:, 1])
+    ref = odec.attend(q, K, V, npi(case.block_table), npi(sl), tab, cnt, scale=case.scale, G=G)
+
+    class _St:
+        pass
+    st = _St()
+    st.max_reqs, st.n_kv, st.G, st.D = B, n_kv, G, case.d
+    st.page_table = torch.from_numpy(tab).to(DEV)
+    st.page_cnt = torch.from_numpy(cnt).to(DEV)
+    ensure_stage_b_buffers(st, DEV)
+    kv = case.kv_cache.to(DEV)
+    out = torch.full((B, n_kv * G, case.d), float("nan"), dtype=torch.bfloat16, device=DEV)
+    sparse_paged_decode_batched(case.q.to(DEV), kv, case.block_table.to(DEV), sl.to(DEV), st,
+                                out, ResidentVSource(kv), scale=case.scale, path=c["path"])
+    torch.cuda.synchronize()
+    got = npf(out)
+    assert np.isfinite(got).all()
+    assert np.allclose(got, ref, atol=2e-2, rtol=1e-2), float(np.abs(got - ref).max())
