@@ -1,10 +1,16 @@
-"""Property-based GPU parity: selection and sparse decode over generated cases.
+"""Property-based GPU parity: scores, selection and sparse decode over generated cases.
 
 hypothesis draws the batch shape, the sequence lengths, the score pattern and the
 selection parameters (derandomized, so every run checks the same examples); each example
 runs the HIP path and compares with the oracle under the same bars as the fixed-case
 tests: page_table / page_cnt / chosen count bit-exact for the selection, outputs within
 2e-2 absolute / 1e-2 relative of the fp64 attention for the decode.
+
+The score kernels (quad, r8, CLSE) run over generated record layouts (rank, V / Vk bits, c
+bits and c-scale grain), GQA groups, kv-head counts (workgroups of 1, 2, 4 and 8 heads
+and two head groups), combines, batch sizes and lengths from one token up; their int32
+contractions are bit-exact against int64 brute force and their scores within
+1e-3 * max(|ref|, 1) of the fp64 oracle (quad: also 2e-5 of the limb oracle).
 
 Score patterns target the selection's radix search: i.i.d. normal, a small value pool
 (many exact ties), a run of keys a few ulps apart (every digit of the 32-bit key decides,
@@ -20,12 +26,15 @@ from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as hs
 
 import oracle.decode as odec
+import oracle.score as osc
 import oracle.select as osel
 from amass.attention import ensure_stage_b_buffers
 from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
-from amass.bench.synth import make_case
-from amass.selection import QuadState, coverage_select, derive_page_params, topb_select
-from helpers import announce, npf, npi
+from amass.bench.synth import build_quad_state, build_r8_state, make_case
+from amass.selection import (QuadState, coverage_select, derive_page_params, r8_score,
+                             topb_select)
+from amass.selection.quad_score import clse_score, quad_score_launch
+from helpers import announce, case_to, npf, npi, rel_close, to_device
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -172,3 +181,97 @@ def _decode_example(c):
     got = npf(out)
     assert np.isfinite(got).all()
     assert np.allclose(got, ref, atol=2e-2, rtol=1e-2), float(np.abs(got - ref).max())
+
+
+# ---------------------------------------------------------------------------- scores
+# Score kernels over generated record layouts, GQA groups, kv-head counts (workgroups of
+# 1, 2, 4 and 8 heads, and two head groups), batch sizes and lengths from one token up:
+# int32 contractions bit-exact against int64 brute force, scores within 1e-3 * max(|ref|,
+# 1) of the fp64 oracle (quad: also 2e-5 of the limb oracle).
+SCORE_PROPS = settings(max_examples=30, deadline=None, derandomize=True, database=None,
+                       suppress_health_check=list(HealthCheck))
+
+
+@hs.composite
+def score_cases(draw, kind):
+    G = draw(hs.integers(1, 8) if kind == "quad" else hs.sampled_from([1, 2, 4, 8]))
+    rank = draw(hs.sampled_from({"quad": [2, 4, 8], "r8": [4, 8], "clse": [2, 4, 8]}[kind]))
+    c = dict(kind=kind, B=draw(hs.integers(1, 6)), n_kv=draw(hs.sampled_from([1, 2, 4, 8, 16])),
+             G=G, rank=rank, v_bits=draw(hs.sampled_from([8, 4])),
+             c_bits=draw(hs.sampled_from([8, 4])),
+             hi=draw(hs.sampled_from([16, 300, 1500, 4000])),
+             combine=draw(hs.sampled_from(["max", "nrm"])),
+             seed=draw(hs.integers(0, 100000)))
+    c["c_grain"] = draw(hs.sampled_from({"quad": ["token"], "r8": ["page", "page_f32"],
+                                         "clse": ["token", "page"]}[kind]))
+    return c
+
+
+def _score_example(c):
+    announce(f"score property case {c}")
+    kind, B, n_kv, G, rank = c["kind"], c["B"], c["n_kv"], c["G"], c["rank"]
+    case = make_case(B=B, ctx=(1, c["hi"]), n_kv=n_kv, G=G, heavy=0.05, table="perm",
+                     seed=c["seed"])
+    rng = np.random.default_rng(c["seed"])
+    case.seq_lens = torch.clamp(case.seq_lens - torch.from_numpy(rng.integers(0, 16, B)).to(
+        case.seq_lens.dtype), min=1).to(torch.int32)
+    if kind == "r8":
+        st = build_r8_state(case, rank=rank, vk_bits=c["v_bits"], c_bits=c["c_bits"],
+                            c_grain=c["c_grain"])
+    else:
+        st = build_quad_state(case, rank=rank, v_bits=c["v_bits"], combine=c["combine"],
+                              coords="lse" if kind == "clse" else "none", c_bits=c["c_bits"],
+                              c_grain=c["c_grain"], budget=0.05)
+    to_device(st, DEV)
+    case_to(case, DEV)
+    derive_page_params(st, case.seq_lens, B)
+    MP = st.max_pages
+    comb = torch.zeros(B, n_kv, MP, G, rank + 1, dtype=torch.int32, device=DEV)
+    if kind == "quad":
+        quad_score_launch(st, 0, case.q, case.block_table, B, case.scale, comb_out=comb)
+    elif kind == "r8":
+        r8_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale, comb_out=comb)
+    else:
+        clse_score(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                   comb_out=comb)
+    torch.cuda.synchronize()
+    q, bt, sl, nsh = npf(case.q), npi(case.block_table), npi(case.seq_lens), npi(st.n_sel_hi)
+    kw = dict(scale=case.scale, page=16, G=G, max_pages=MP)
+    if kind == "r8":
+        mu, mus, _, Vks, cc, cs, _ = st.layer_state(0)
+        Vk = npi(st.reference_Vk(0))
+        ref_comb = osc.r8_comb(q, npi(mu), Vk, bt, nsh, G=G, vk_bits=c["v_bits"], max_pages=MP)
+        refs = [(osc.r8_score(q, npi(mu), npf(mus), Vk, npf(Vks), npi(cc), npf(cs), bt, sl,
+                              nsh, vk_bits=c["v_bits"], c_bits=c["c_bits"], **kw), 1e-3)]
+        got = npf(st.score)
+    else:
+        mu, mus, _, Vs, sg, _ = st.layer_state(0)
+        V = npi(st.reference_V(0))
+        ref_comb = osc.quad_comb(q, npi(mu), V, bt, nsh, G=G, v_bits=c["v_bits"], max_pages=MP)
+        if kind == "quad":
+            o = dict(q=q, mu=npi(mu), mu_scale=npf(mus), V=V, V_scale=npf(Vs), sig2=npf(sg),
+                     block_table=bt, n_sel_hi=nsh)
+            refs = [(osc.quad_score(**o, **kw, v_bits=c["v_bits"], combine=c["combine"],
+                                    q_mode=m), tol) for m, tol in (("float", 1e-3),
+                                                                   ("limbs", 2e-5))]
+        else:
+            refs = [(osc.clse_score(q, npi(mu), npf(mus), V, npf(Vs), npi(st.quad_c[0]),
+                                    npf(st.c_scale[0]), npf(st.quad_resid[0]), bt, sl, nsh,
+                                    v_bits=c["v_bits"], c_bits=c["c_bits"],
+                                    combine=c["combine"], **kw), 1e-3)]
+        got = npf(st.score_h if c["combine"] == "nrm" else st.score)
+    gc = npi(comb).astype(np.int64)
+    for r in range(B):
+        n = int(nsh[r])
+        assert np.array_equal(gc[r, :, :n], ref_comb[r, :, :n]), f"contractions, request {r}"
+        for ref, tol in refs:
+            assert rel_close(got[r, ..., :n], ref[r, ..., :n], 1) <= tol, f"scores, request {r}"
+
+
+@pytest.mark.parametrize("kind", ["quad", "r8", "clse"])
+def test_scores_match_oracle(kind):
+    @SCORE_PROPS
+    @given(c=score_cases(kind))
+    def prop(c):
+        _score_example(c)
+    prop()
