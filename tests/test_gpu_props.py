@@ -1,4 +1,5 @@
-"""Property-based GPU parity: scores, selection and sparse decode over generated cases.
+"""Property-based GPU parity: scores, selection, sparse decode and the tier plan over
+generated cases.
 
 hypothesis draws the batch shape, the sequence lengths, the score pattern and the
 selection parameters (derandomized, so every run checks the same examples); each example
@@ -28,12 +29,14 @@ from hypothesis import strategies as hs
 import oracle.decode as odec
 import oracle.score as osc
 import oracle.select as osel
+import oracle.tier as otier
 from amass.attention import ensure_stage_b_buffers
 from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
 from amass.bench.synth import build_quad_state, build_r8_state, make_case
 from amass.selection import (QuadState, coverage_select, derive_page_params, r8_score,
                              topb_select)
 from amass.selection.quad_score import clse_score, quad_score_launch
+from amass.tier import Tier
 from helpers import announce, case_to, npf, npi, rel_close, to_device
 
 pytestmark = pytest.mark.gpu
@@ -274,4 +277,89 @@ def test_scores_match_oracle(kind):
     @given(c=score_cases(kind))
     def prop(c):
         _score_example(c)
+    prop()
+
+
+# ---------------------------------------------------------------------------- tier plan
+# The mem-v gather plan over generated hot-buffer states and request streams: slot counts
+# from 1 to 3000 (more slots than threads per kv head), buffers empty, half full or full
+# with LRU clocks spread over 1 .. 5000 steps (the histogram cut up to 255 steps of age,
+# the radix sort beyond), several steps of top-b selections of 2 .. 100 % of the pages
+# (hits, misses, evictions, overflow), bit-exact against the sequential oracle: maps,
+# clocks, miss and victim lists, overflow flag, fetch list as a set.
+TIER_PROPS = settings(max_examples=12, deadline=None, derandomize=True, database=None,
+                      suppress_health_check=list(HealthCheck))
+
+
+@hs.composite
+def tier_cases(draw, slots):
+    return dict(B=draw(hs.integers(1, 5)), n_kv=draw(hs.sampled_from([1, 2, 8])),
+                hi=draw(hs.sampled_from([300, 2000, 6000])), slots=slots,
+                fill=draw(hs.sampled_from([0.0, 0.5, 1.0])),
+                span=draw(hs.sampled_from([1, 40, 255, 256, 5000])),
+                fracs=draw(hs.lists(hs.sampled_from([0.02, 0.15, 0.5, 1.0]), min_size=1,
+                                    max_size=4)),
+                seed=draw(hs.integers(0, 100000)))
+
+
+def _tier_example(c):
+    announce(f"tier property case {c}")
+    B, n_kv, slots = c["B"], c["n_kv"], c["slots"]
+    case = make_case(B=B, ctx=(16, c["hi"]), n_kv=n_kv, G=4, heavy=0.0, seed=c["seed"])
+    NB = case.kv_cache.shape[0]
+    tier = Tier(num_layers=1, num_blocks=NB, n_kv=n_kv, page=16, d=128, hot_slots=slots,
+                max_reqs=B, max_pages=case.max_pages, device=DEV, v_blocks=4)
+    tier.flush_layer(0, case.kv_cache[:, 1])
+    r5 = tier.residency
+    rng = np.random.default_rng(c["seed"])
+    p2s = np.full((n_kv, NB), -1, np.int64)
+    s2p = np.full((n_kv, slots), -1, np.int64)
+    lru = np.zeros((n_kv, slots), np.int64)
+    clock = c["span"] + 10
+    for kv in range(n_kv):
+        nres = int(min(slots, NB) * c["fill"])
+        blks = rng.choice(NB, nres, replace=False)
+        sl_ = rng.choice(slots, nres, replace=False)
+        p2s[kv, blks] = sl_
+        s2p[kv, sl_] = blks
+        lru[kv, sl_] = rng.integers(clock - c["span"], clock, nres)
+    r5.page2slot[0].copy_(torch.from_numpy(p2s.astype(np.int32)))
+    r5.slot2page[0].copy_(torch.from_numpy(s2p.astype(np.int32)))
+    r5.lru_clock[0].copy_(torch.from_numpy(lru.astype(np.int32)))
+    r5.clock.fill_(clock)
+    bt, sl = case.block_table.to(DEV), case.seq_lens.to(DEV)
+    MP = case.max_pages
+    for frac in c["fracs"]:
+        sc = rng.standard_normal((B, n_kv, MP)).astype(np.float32)
+        npg, nsh, bfix = osel.derive(npi(case.seq_lens), frac, 16, 1, 1)
+        tab, cnt, _ = osel.select(sc, npg, nsh, bfix, sink=1, max_pages=MP, mode=0)
+        ref = otier.plan(tab, cnt, npi(case.block_table), npi(case.seq_lens), p2s, s2p, lru,
+                         clock, page=16)
+        r5.overflow.zero_()
+        r5.gather_plan(0, torch.from_numpy(tab).to(DEV), torch.from_numpy(cnt).to(DEV), bt,
+                       sl, B)
+        torch.cuda.synchronize()
+        assert int(r5.clock[0]) == ref["clock"]
+        assert np.array_equal(npi(r5.page2slot[0]), ref["page2slot"])
+        assert np.array_equal(npi(r5.slot2page[0]), ref["slot2page"])
+        assert np.array_equal(npi(r5.lru_clock[0]), ref["lru"])
+        assert bool(r5.overflow[0]) == ref["overflow"]
+        mc, mp, vs = npi(r5.miss_cnt), npi(r5.miss_pages), npi(r5.victim_slots)
+        for r in range(B):
+            for kv in range(n_kv):
+                m = ref["miss"][r][kv]
+                assert mc[r, kv] == len(m)
+                assert list(mp[r, kv, :len(m)]) == m
+                assert list(vs[r, kv, :len(m)]) == ref["victims"][r][kv]
+        n = int(r5.fetch_cnt[0])
+        assert set(map(tuple, npi(r5.fetch_list[:n]).tolist())) == ref["fetch"]
+        p2s, s2p, lru, clock = ref["page2slot"], ref["slot2page"], ref["lru"], ref["clock"]
+
+
+@pytest.mark.parametrize("slots", [1, 7, 64, 600, 3000])
+def test_tier_plan_matches_oracle(slots):
+    @TIER_PROPS
+    @given(c=tier_cases(slots))
+    def prop(c):
+        _tier_example(c)
     prop()
