@@ -1,5 +1,5 @@
-"""Property-based GPU parity: scores, selection, sparse decode and the tier plan over
-generated cases.
+"""Property-based GPU parity: scores, selection, sparse decode, the tier plan and the mem-v
+write path over generated cases.
 
 hypothesis draws the batch shape, the sequence lengths, the score pattern and the
 selection parameters (derandomized, so every run checks the same examples); each example
@@ -363,3 +363,34 @@ def test_tier_plan_matches_oracle(slots):
     def prop(c):
         _tier_example(c)
     prop()
+
+
+# ---------------------------------------------------------------------------- write path
+# The mem-v write path over generated schedules: per step, each of three requests appends
+# 0 .. 5 tokens (prefill chunks, decode steps and idle steps in any order, pages of 4
+# tokens), with or without a block shared by two requests, flush lists of 1, 3 or 64
+# entries per step; staging holds every page a schedule can write, so no step exhausts
+# it.  After every step the staging map, flush state, token slots, staged and pinned
+# pools, pool validity and residency maps equal the oracle's bit for bit.
+STAGE_PROPS = settings(max_examples=40, deadline=None, derandomize=True, database=None,
+                       suppress_health_check=list(HealthCheck))
+
+
+@hs.composite
+def write_schedules(draw):
+    steps = draw(hs.integers(1, 14))
+    return dict(shared=draw(hs.booleans()), maxf=draw(hs.sampled_from([1, 3, 64])),
+                seed=draw(hs.integers(0, 100000)),
+                sched=draw(hs.lists(hs.lists(hs.integers(0, 5), min_size=3, max_size=3),
+                                    min_size=steps, max_size=steps)))
+
+
+@STAGE_PROPS
+@given(c=write_schedules())
+def test_write_path_matches_oracle_on_generated_schedules(c):
+    from test_gpu_stage import _Scenario
+    announce(f"write path property case {c}")
+    sc = _Scenario(seed=c["seed"], NV=64, maxf=c["maxf"], shared=c["shared"])
+    for ql in c["sched"]:
+        sc.step(ql)
+    sc.stg.assert_free_partition()
