@@ -1,5 +1,6 @@
 """The tier's host-side copy-engine planner (Residency.build_dma_plan, reference
-tier/residency.py:438-493) on the CPU: a hand-worked miss list and the runs it must give.
+tier/residency.py:438-493) on the CPU: a hand-worked miss list and the runs it must give,
+and generated miss lists against a plain sequential walk.
 
 A run is a chain of misses that follow each other in one (request, kv head) miss list
 with victim slot and block both one higher than the previous one's and V valid in the
@@ -9,6 +10,8 @@ import types
 
 import numpy as np
 import torch
+from hypothesis import given, settings
+from hypothesis import strategies as hs
 
 from amass.tier.residency import Residency
 
@@ -74,3 +77,64 @@ def test_dma_runs_never_cross_lists():
     _miss(r, 1, 0, [9], [8])
     runs, _ = r.build_dma_plan(0, pool, 2)
     assert list(runs[:, 5]) == [8, 2, 1]
+
+
+def _sequential_runs(r, layer, n_req):
+    """The plan by a plain walk over each (request, kv head) miss list: a run starts at a
+    fetchable miss (slot >= 0, V valid in the pool) that does not continue the previous
+    entry, and grows while the next entry is fetchable with slot and block one higher."""
+    out, staged = [], False
+    n_kv = r.n_kv
+    for req in range(n_req):
+        for kv in range(n_kv):
+            m = int(r.miss_cnt[req, kv])
+            blk = [int(x) for x in r.miss_pages[req, kv, :m]]
+            slot = [int(x) for x in r.victim_slots[req, kv, :m]]
+            ok = [slot[i] >= 0 and int(r.pool_valid[layer, kv, blk[i]]) == 1 for i in range(m)]
+            staged |= any(slot[i] >= 0 and not ok[i] for i in range(m))
+            i = 0
+            while i < m:
+                if not ok[i]:
+                    i += 1
+                    continue
+                j = i + 1
+                while j < m and ok[j] and slot[j] == slot[j - 1] + 1 and blk[j] == blk[j - 1] + 1:
+                    j += 1
+                out.append((kv, slot[i], blk[i], j - i))
+                i = j
+    return out, staged
+
+
+@settings(max_examples=200, deadline=None, derandomize=True, database=None)
+@given(data=hs.data())
+def test_dma_runs_match_a_sequential_walk(data):
+    """Generated miss lists (chains of consecutive slots and blocks broken at random, slots
+    -1, pages valid only in staging, leftover entries past each count): the planner's run
+    table equals the sequential walk's, run for run, and has_staged agrees."""
+    n_req, n_kv, NB, MP, S = 3, 2, 64, 12, 24
+    r = Residency(num_layers=1, num_blocks=NB, n_kv=n_kv, hot_slots=S, page=16, d=128,
+                  max_reqs=n_req, max_pages=MP, dtype=torch.bfloat16, device="cpu")
+    valid = data.draw(hs.lists(hs.booleans(), min_size=n_kv * NB, max_size=n_kv * NB))
+    r.pool_valid[0] = torch.tensor(valid, dtype=torch.int8).view(n_kv, NB).to(r.pool_valid.dtype)
+    for req in range(n_req):
+        for kv in range(n_kv):
+            m = data.draw(hs.integers(0, MP))
+            b0, s0 = data.draw(hs.integers(0, NB - 1)), data.draw(hs.integers(0, S - 1))
+            blocks, slots = [], []
+            for _ in range(m):
+                if data.draw(hs.booleans()):      # continue the chain
+                    b0, s0 = (b0 + 1) % NB, (s0 + 1) % S
+                else:
+                    b0, s0 = data.draw(hs.integers(0, NB - 1)), data.draw(hs.integers(0, S - 1))
+                blocks.append(b0)
+                slots.append(-1 if data.draw(hs.integers(0, 9)) == 0 else s0)
+            _miss(r, req, kv, blocks, slots)
+    n = data.draw(hs.integers(0, n_req))
+    pool = types.SimpleNamespace(_host_ptr=1 << 40)
+    runs, staged = r.build_dma_plan(0, pool, n)
+    want, want_staged = _sequential_runs(r, 0, n)
+    hot = r.hot[0].data_ptr()
+    exp = np.array([[hot + (kv * S + s) * PB, (1 << 40) + (b * n_kv + kv) * PB, PB,
+                     n_kv * PB, PB, h] for kv, s, b, h in want], np.int64).reshape(-1, 6)
+    assert staged == want_staged
+    assert np.array_equal(runs, exp)
