@@ -20,7 +20,7 @@ per kv head:
       Vk_scale (L, NB, n_kv, r)       half 0..r-1
       c_scale  (L, NB, n_kv, page)    half 8..23 (c_grain "page" / "tensor")
       c_scale_f32 (L, NB, n_kv)       fp32 at bytes 16..19 (c_grain "page_f32": one fp32 c
-               scale per page, BASELINE's per-page fp32 scale; halves 10..23 zero)
+               scale per page, config 2's per-page fp32 scale; halves 10..23 zero)
       mu_scale (L, NB, n_kv)          half 24; the other halves are zero
   r8_tag   (L, NB, n_kv, TAGW)  bf16  NaN-init content tag (separate)
 

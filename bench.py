@@ -340,7 +340,7 @@ def cpu_path(case, st, *, mode, coverage, budget_s, warmup=3, iters=10):
 
 
 def cpu_baseline(case1, st1, args):
-    """BASELINE's CPU plan: the fp32 torch path with torch.set_num_threads(cores), config 0
+    """The CPU baseline: the fp32 torch path with torch.set_num_threads(cores), config 0
     (B=1 ctx 4096, fixed 5 %: b = 13) and config 1 (the headline), each split into score /
     select / attend; `value` is config 1's us per layer."""
     import torch
@@ -483,7 +483,7 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
 
 
 def run_secondary(idx, args, boost="sigma", c_grain="page", name=None):
-    """A BASELINE configuration other than the headline, measured like config 1
+    """A BASELINE.json configuration other than the headline, measured like config 1
     (config 2 with c_grain "page_f32": one fp32 c scale per page and head).  `name` keys
     the profiled counter files of the workload (profiles/*_<name>.txt)."""
     from amass.bench.synth import CONFIGS, build_quad_state, build_r8_state, config_case
@@ -568,7 +568,7 @@ def run_summary_build(args):
 def run_config4(args, boost="sigma", steps=64):
     """mem-v at config 4: V in the pinned, device-mapped host pool, a 10 % hot buffer, 64
     decode steps over a fixed boosted page set, each from a cold hot buffer.  Two query
-    streams: "fresh" (BASELINE's literal N(0, 1) each step) and "correlated" (the case's
+    streams: "fresh" (config 4's literal N(0, 1) each step) and "correlated" (the case's
     queries + 0.3 N(0, 1): the boosted set stays the relevant one, which is the regime a
     hot buffer is for).  Each step = quad score + coverage select, residency plan, fetch
     (the fetch kernel, or the copy engine on a side stream after a host-side run plan),

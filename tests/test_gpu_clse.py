@@ -3,7 +3,7 @@
 CLSE (reference selection/quad_score.py:156-393) = the quad storage + per-key coordinates
 + the residual energy.  Bars: int32 d-contractions bit-exact (comb_out vs int64 brute
 force); scores within 1e-3 * max(|ref|, 1) of the float64 oracle with unquantised q
-(BASELINE's 1e-3 for the score kernels), per head (combine "nrm") and group max ("max");
+(the 1e-3 bar for the score kernels), per head (combine "nrm") and group max ("max");
 the HIP builder's resid within 2e-3 relative (+1e-4 of the page's trace), c codes within
 one step on separated columns, and the scores from its summaries within 2e-2 of the
 oracle-built ones; select_pages_clse + decode end to end against the oracle.

@@ -1,6 +1,6 @@
 """GPU parity of the sparse / dense paged decode against the fp64 oracle.
 
-Bar (BASELINE): outputs within 2e-2 absolute / 1e-2 relative of the fp64 softmax
+Bar: outputs within 2e-2 absolute / 1e-2 relative of the fp64 softmax
 attention.  Covers split-K + merge, the fused single pass, the dense baseline, G = 4 / 8,
 partial last pages whose unused slots hold NaN (must be masked), padded rows (zero
 output), empty and single-page selections.

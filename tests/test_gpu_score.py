@@ -2,7 +2,7 @@
 
 Bar: the int32 d-contractions (comb_out) are bit-exact against int64 brute force; quad
 scores within |d| <= 1e-3 * max(|ref|, 1) of the fp64 oracle with unquantised q (the
-Triton reference semantics, BASELINE tolerance 1e-3 relative) and within 2e-5 of the
+Triton reference semantics, tolerance 1e-3 relative) and within 2e-5 of the
 oracle that uses the 2-limb q code; nrm-combined scores within 1e-4 relative; r8 scores
 within 1e-3 likewise.
 """
@@ -217,7 +217,7 @@ def test_r8_head_layouts(n_kv, G):
 
 @pytest.mark.parametrize("vk_bits,c_bits,G", [(8, 8, 4), (8, 4, 8), (4, 8, 2)])
 def test_r8_page_f32_scale(vk_bits, c_bits, G):
-    """The per-page fp32 c scale (c_grain "page_f32", BASELINE config 2's "per-page fp32
+    """The per-page fp32 c scale (c_grain "page_f32", config 2's "per-page fp32
     scale"): int32 contractions exact (they do not depend on the scale format), scores
     within 1e-3 of the fp64 oracle fed the same fp32 scales."""
     announce(f"r8 page_f32 vk={vk_bits} c={c_bits} G={G}")
