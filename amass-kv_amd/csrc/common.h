@@ -113,6 +113,67 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
+// Wave-uniform reductions and an inclusive scan of other types, the same DPP row steps
+// and readlane across rows (every lane gets the result).  All 64 lanes must be active.
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_maxf_uniform(float v) {
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)),
+                 fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)dpp_i<CTRL>((int)v);
+}
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int l) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ uint32_t wave_minu_uniform(uint32_t v) {
+    v = min(v, dpp_u<DPP_HALF_MIRROR>(v));
+    v = min(v, dpp_u<DPP_XOR2>(v));
+    v = min(v, dpp_u<DPP_XOR1>(v));
+    v = min(v, dpp_u<DPP_ROW_MIRROR>(v));
+    return min(min(readlane_u(v, 0), readlane_u(v, 16)), min(readlane_u(v, 32), readlane_u(v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_maxu_uniform(uint32_t v) {
+    v = max(v, dpp_u<DPP_HALF_MIRROR>(v));
+    v = max(v, dpp_u<DPP_XOR2>(v));
+    v = max(v, dpp_u<DPP_XOR1>(v));
+    v = max(v, dpp_u<DPP_ROW_MIRROR>(v));
+    return max(max(readlane_u(v, 0), readlane_u(v, 16)), max(readlane_u(v, 32), readlane_u(v, 48)));
+}
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const uint32_t lo = dpp_u<CTRL>((uint32_t)v), hi = dpp_u<CTRL>((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long v, int l) {
+    return ((unsigned long long)readlane_u((uint32_t)(v >> 32), l) << 32) |
+           readlane_u((uint32_t)v, l);
+}
+__device__ __forceinline__ unsigned long long wave_sum_u64_uniform(unsigned long long v) {
+    v += dpp_u64<DPP_HALF_MIRROR>(v);
+    v += dpp_u64<DPP_XOR2>(v);
+    v += dpp_u64<DPP_XOR1>(v);
+    v += dpp_u64<DPP_ROW_MIRROR>(v);
+    return (readlane_u64(v, 0) + readlane_u64(v, 16)) + (readlane_u64(v, 32) + readlane_u64(v, 48));
+}
+__device__ __forceinline__ unsigned long long wave_incl_scan_u64(unsigned long long v) {
+    v += dpp_u64<DPP_ROW_SHR1>(v);
+    v += dpp_u64<DPP_ROW_SHR2>(v);
+    v += dpp_u64<DPP_ROW_SHR4>(v);
+    v += dpp_u64<DPP_ROW_SHR8>(v);
+    const unsigned long long r0 = readlane_u64(v, 15), r1 = readlane_u64(v, 31),
+                             r2 = readlane_u64(v, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    return v + (row >= 1 ? r0 : 0ull) + (row >= 2 ? r1 : 0ull) + (row >= 3 ? r2 : 0ull);
+}
+
 // full-wave reductions (result in every lane)
 __device__ __forceinline__ float wave_maxf(float v) {
 #pragma unroll

@@ -41,16 +41,6 @@ __global__ void derive_kernel(const int32_t* __restrict__ sl, int32_t* __restric
 }
 
 // ------------------------------------------------------------------ wave helpers
-__device__ __forceinline__ unsigned int wave_minu(unsigned int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = min(v, (unsigned int)__shfl_xor((int)v, o, WAVE));
-    return v;
-}
-__device__ __forceinline__ unsigned int wave_maxu(unsigned int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = max(v, (unsigned int)__shfl_xor((int)v, o, WAVE));
-    return v;
-}
 // number of set bits of `m` below this lane
 __device__ __forceinline__ int lanes_below(unsigned long long m) {
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -68,7 +58,7 @@ __device__ __forceinline__ void head_max(float* m, int G, float (*red)[SEL_WAVES
 #pragma unroll
     for (int g = 0; g < 8; ++g)
         if (g < G) {
-            const float x = wave_maxf(m[g]);
+            const float x = wave_maxf_uniform(m[g]);
             if ((threadIdx.x & 63) == 0) red[g][w] = x;
         }
     __syncthreads();
@@ -350,7 +340,7 @@ __device__ __forceinline__ void block_head_max(float* m, int G, float (*red)[CAP
 #pragma unroll
     for (int g = 0; g < 8; ++g)
         if (g < G) {
-            const float x = wave_maxf(m[g]);
+            const float x = wave_maxf_uniform(m[g]);
             if ((threadIdx.x & 63) == 0) red[g][w] = x;
         }
     __syncthreads();
@@ -431,12 +421,7 @@ __device__ void xs_scan(XSel& s, bool by_mass, unsigned long long target, int sh
         m[i] = by_mass ? s.hmass[b0 - i] : (unsigned long long)s.hcnt[b0 - i];
         own += m[i];
     }
-    unsigned long long incl = own;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const unsigned long long y = __shfl_up(incl, o, WAVE);
-        if (lane >= o) incl += y;
-    }
+    const unsigned long long incl = wave_incl_scan_u64(own);
     if (lane == WAVE - 1) s.wm[wv] = incl;
     const unsigned long long above0 = by_mass ? s.mass_above : (unsigned long long)s.cnt_above;
     __syncthreads();
@@ -563,9 +548,9 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 }
             }
         }
-        pmax = wave_maxf(pmax);
-        kmin = wave_minu(kmin);
-        kmax = wave_maxu(kmax);
+        pmax = wave_maxf_uniform(pmax);
+        kmin = wave_minu_uniform(kmin);
+        kmax = wave_maxu_uniform(kmax);
         if (lane == 0) { s.fred[wv] = pmax; s.kred[0][wv] = kmin; s.kred[1][wv] = kmax; }
     }
     __syncthreads();
@@ -613,8 +598,8 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 }
             }
             if (coverage) {
-                tot = wave_sum_u64(tot);
-                snk = wave_sum_u64(snk);
+                tot = wave_sum_u64_uniform(tot);
+                snk = wave_sum_u64_uniform(snk);
                 if (lane == 0) { s.ured[0][wv] = tot; s.ured[1][wv] = snk; }
             }
         }
@@ -660,7 +645,7 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                     if (bal) {
                         int base = 0;
                         if (lane == 0) base = atomicAdd(&s.ncand, __popcll(bal));
-                        base = __shfl(base, 0, WAVE);
+                        base = __builtin_amdgcn_readlane(base, 0);
                         if (in) {
                             const int idx = base + lanes_below(bal);
                             if (idx < XS_CAND) {
@@ -728,9 +713,10 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 const bool win = lane < c && above < target && target <= above + own;
                 const unsigned long long wb = __ballot(win);
                 const int src = wb ? __ffsll((long long)wb) - 1 : 0;   // ties of kt agree
-                const unsigned int fk = __shfl(kt, src, WAVE);
-                const int feq = __shfl((int)eq, src, WAVE), fab = __shfl((int)ab, src, WAVE);
-                const unsigned long long fam = __shfl(am, src, WAVE);
+                const unsigned int fk = readlane_u(kt, src);
+                const int feq = __builtin_amdgcn_readlane((int)eq, src);
+                const int fab = __builtin_amdgcn_readlane((int)ab, src);
+                const unsigned long long fam = readlane_u64(am, src);
                 if (lane == 0) {
                     s.f_key = wb ? fk : s.prefix << shift;
                     s.f_cab = s.cnt_above + (wb ? fab : 0);
