@@ -260,6 +260,7 @@ constexpr int XS_THREADS_L = 1024;            // units of 4097 .. 8192 pages
 constexpr int XS_WAVES = XS_THREADS_L / WAVE; // exchange arrays sized for the larger block
 constexpr int XS_BITS = 11;                   // key bits per histogram digit
 constexpr int XS_BINS = 1 << XS_BITS;         // four bins per thread in the scan
+constexpr int XS_PBINS = XS_BINS + XS_BINS / 32;   // one unused slot after every 32 bins
 constexpr int XS_CAND = WAVE;                 // a bin this small is ranked by one wave
 constexpr int XS_TILE = 16;                   // pages per per-tile maximum of score_h
 constexpr int XS_FUSED = 64;                  // PPT * G floats of the fused nrm staging
@@ -267,18 +268,19 @@ constexpr int XS_MAXNC = 8;                   // chunks per thread at PPT = 32
 constexpr int NP_THREADS = 256;               // nrm pre-pass workgroup
 constexpr int NP_PAGES = 4 * NP_THREADS;      // pages per pre-pass workgroup
 
+// Histogram slot of bin b: one unused slot after every 32 bins, so the 64 lanes that each
+// read one 32-bin group (lane i: slots 33 i ..) spread evenly over the LDS banks.
+__device__ __forceinline__ unsigned int xs_pad(unsigned int b) { return b + (b >> 5); }
+
 struct __align__(16) XSel {
-    unsigned long long hmass[XS_BINS];        // histogram: 2^-32 fixed-point masses
-    unsigned int hcnt[XS_BINS];               //            and counts
-    unsigned long long cmass[XS_CAND];        // candidates: masses and relative keys
-    unsigned int ckey[XS_CAND];
-    unsigned long long wm[XS_WAVES];          // bin scan: per-wave totals
-    unsigned int wc[XS_WAVES];
+    unsigned long long hmass[XS_PBINS];       // histogram: 2^-32 fixed-point masses
+    unsigned int hcnt[XS_PBINS];              //            and counts (bin b at xs_pad(b))
+    unsigned int ckey[XS_CAND];               // candidates: relative keys
     unsigned long long ured[2][XS_WAVES];     // total / sink mass
     float hred[8][XS_WAVES];                  // per-head maxima
     float fred[XS_WAVES];                     // score max
     unsigned int kred[2][XS_WAVES];           // selectable key min / max
-    int ccnt[XS_MAXNC][XS_WAVES][2];          // compaction: sure-keep / tie counts
+    int cpk[XS_MAXNC][XS_WAVES];              // compaction: packed tie / sure counts per wave
     int ncand;
     unsigned int prefix, bin, bin_cnt;        // digit search: rel >> shift of the chosen bin
     int cnt_above;                            // keys / mass strictly above the chosen bin
@@ -403,46 +405,49 @@ __global__ __launch_bounds__(NP_THREADS) void nrm_pass_kernel(const amass_select
     st_pages<4>(gs, p0 + 4 * tid, n, vec, acc);
 }
 
-// Block scan of the histogram from the highest bin down: the bin where the cumulative
-// weight (mass in coverage mode, else count) from the top, after what earlier digits put
-// above, reaches `target`.  Thread t owns bins XS_BINS-1-XS_BPT t .. down.  The thread
-// holding it appends the bin to the prefix (digit bits [shift, top)) and adds the bins
-// above it to the running total.  Two barriers.
-template <int NT>
-__device__ void xs_scan(XSel& s, bool by_mass, unsigned long long target, int shift, int top) {
-    constexpr int XS_BPT = XS_BINS / NT;
-    constexpr int NW = NT / WAVE;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int b0 = XS_BINS - 1 - XS_BPT * tid;
-    unsigned long long m[XS_BPT];
-    unsigned long long own = 0;
+// The histogram search from the highest bin down: the bin where the cumulative weight
+// (mass in coverage mode, else count) from the top, after what earlier digits put above,
+// reaches `target`.  Wave 0 alone: lane i sums the 32 bins of super-bin i (bins
+// XS_BINS-1-32i down), one wave scan finds the super-bin and a second one, over its 32
+// bins, the bin; the finding lane appends the bin to the prefix (digit bits
+// [shift, top)) and adds the weight above it to the running total.  One barrier.
+__device__ void xs_find(XSel& s, bool by_mass, unsigned long long target, int shift, int top) {
+    if (threadIdx.x < WAVE) {
+        const int lane = threadIdx.x;
+        const int g = WAVE - 1 - lane;                      // bins 32 g .. 32 g + 31
+        unsigned long long sum = 0;
+        if (by_mass) {
+            const unsigned long long* h = s.hmass + 33 * g;
 #pragma unroll
-    for (int i = 0; i < XS_BPT; ++i) {
-        m[i] = by_mass ? s.hmass[b0 - i] : (unsigned long long)s.hcnt[b0 - i];
-        own += m[i];
-    }
-    const unsigned long long incl = wave_incl_scan_u64(own);
-    if (lane == WAVE - 1) s.wm[wv] = incl;
-    const unsigned long long above0 = by_mass ? s.mass_above : (unsigned long long)s.cnt_above;
-    __syncthreads();
-    unsigned long long base = 0;
+            for (int j = 0; j < 32; ++j) sum += h[j];
+        } else {
+            const unsigned int* h = s.hcnt + 33 * g;
+            unsigned int c = 0;
 #pragma unroll
-    for (int i = 0; i < NW; ++i)
-        if (i < wv) base += s.wm[i];
-    unsigned long long wabove = above0 + base + incl - own;      // weight above bin b0
-    if (wabove < target && target <= wabove + own) {
-#pragma unroll
-        for (int i = 0; i < XS_BPT; ++i) {
-            if (wabove + m[i] >= target) {
-                const unsigned int bin = (unsigned int)(b0 - i);
-                s.bin = bin;
-                s.bin_cnt = by_mass ? 0u : (unsigned int)m[i];
-                if (by_mass) s.mass_above = wabove;
-                else s.cnt_above = (int)wabove;
-                s.prefix = (s.prefix << (top - shift)) | bin;
-                break;
-            }
-            wabove += m[i];
+            for (int j = 0; j < 32; ++j) c += h[j];
+            sum = c;
+        }
+        const unsigned long long above0 =
+            by_mass ? s.mass_above : (unsigned long long)s.cnt_above;
+        const unsigned long long incl = wave_incl_scan_u64(sum);
+        const unsigned long long hit = __ballot(above0 + incl >= target);
+        const int L = hit ? __ffsll((long long)hit) - 1 : WAVE - 1;
+        const unsigned long long base = above0 + readlane_u64(incl - sum, L);
+        const int hL = XS_BINS - 1 - 32 * L;                // group L's highest bin
+        const int sl = 33 * (WAVE - 1 - L) + 31 - lane;     // its slots from the top
+        const unsigned long long m =
+            lane < 32 ? (by_mass ? s.hmass[sl] : (unsigned long long)s.hcnt[sl]) : 0ull;
+        const unsigned long long incl2 = wave_incl_scan_u64(m);
+        const unsigned long long hit2 = __ballot(lane < 32 && base + incl2 >= target);
+        const int j = hit2 ? __ffsll((long long)hit2) - 1 : 31;
+        if (lane == j) {
+            const unsigned int bin = (unsigned int)(hL - j);
+            const unsigned long long wabove = base + incl2 - m;
+            s.bin = bin;
+            s.bin_cnt = by_mass ? 0u : (unsigned int)m;
+            if (by_mass) s.mass_above = wabove;
+            else s.cnt_above = (int)wabove;
+            s.prefix = (s.prefix << (top - shift)) | bin;
         }
     }
     __syncthreads();
@@ -499,7 +504,7 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
     const int lo = sink, hi = nsh;              // selectable [lo, hi) when !keep_all
     int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kh * a.pt_sh;
 
-    for (int i = tid; i < XS_BINS; i += NT) {
+    for (int i = tid; i < XS_PBINS; i += NT) {
         s.hcnt[i] = 0;
         s.hmass[i] = 0;
     }
@@ -532,19 +537,21 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
         }
     }
 
-    // ---- score max and the selectable key range -------------------------------------------
+    // ---- order keys, the score max and the selectable key range --------------------------
+    // From here on every thread holds its pages' order keys (u2f gives the score back).
+    uint32_t key[PPT];
     {
         float pmax = -INFINITY;
         unsigned int kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
         for (int k = 0; k < PPT; ++k) {
             const int p = page_of(k / V, k % V);
+            key[k] = f2u(v[k]);
             if (p < nsc) {
                 pmax = fmaxf(pmax, v[k]);
                 if (p >= lo && p < hi) {
-                    const unsigned int key = f2u(v[k]);
-                    kmin = min(kmin, key);
-                    kmax = max(kmax, key);
+                    kmin = min(kmin, key[k]);
+                    kmax = max(kmax, key[k]);
                 }
             }
         }
@@ -588,12 +595,12 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 if (p < nsc) {
                     const bool sel = p >= lo && p < hi;
                     if (coverage) {
-                        const unsigned long long w = mass_q(v[k], smax, a.score_kind);
+                        const unsigned long long w = mass_q(u2f(key[k]), smax, a.score_kind);
                         tot += w;
                         if (p < sink) snk += w;
-                        if (sel) atomicAdd(&s.hmass[(f2u(v[k]) - kmin) >> shift], w);
+                        if (sel) atomicAdd(&s.hmass[xs_pad((key[k] - kmin) >> shift)], w);
                     } else if (sel && b != 1) {
-                        atomicAdd(&s.hcnt[(f2u(v[k]) - kmin) >> shift], 1u);
+                        atomicAdd(&s.hcnt[xs_pad((key[k] - kmin) >> shift)], 1u);
                     }
                 }
             }
@@ -632,14 +639,14 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
         // counted); a bin of more keys takes the next 11 bits.  Top-b knows the bin's count
         // from its histogram and skips the gather of a large bin.
         for (;;) {
-            xs_scan<NT>(s, coverage, coverage ? need : (unsigned long long)b, shift, top);
+            xs_find(s, coverage, coverage ? need : (unsigned long long)b, shift, top);
             const bool gather = shift == 0 || coverage || s.bin_cnt <= XS_CAND;
             if (gather) {
                 const unsigned int pre = s.prefix;
 #pragma unroll
                 for (int k = 0; k < PPT; ++k) {
                     const int p = page_of(k / V, k % V);
-                    const unsigned int rel = f2u(v[k]) - kmin;
+                    const unsigned int rel = key[k] - kmin;
                     const bool in = p >= lo && p < hi && (rel >> shift) == pre;
                     const unsigned long long bal = __ballot(in);
                     if (bal) {
@@ -648,10 +655,7 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                         base = __builtin_amdgcn_readlane(base, 0);
                         if (in) {
                             const int idx = base + lanes_below(bal);
-                            if (idx < XS_CAND) {
-                                s.ckey[idx] = rel;
-                                s.cmass[idx] = coverage ? mass_q(v[k], smax, a.score_kind) : 0ull;
-                            }
+                            if (idx < XS_CAND) s.ckey[idx] = rel;
                         }
                     }
                 }
@@ -659,7 +663,7 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 if (shift == 0 || s.ncand <= XS_CAND) break;
             }
             // the next 11 bits of the keys inside the chosen bin
-            for (int i = tid; i < XS_BINS; i += NT) {
+            for (int i = tid; i < XS_PBINS; i += NT) {
                 s.hcnt[i] = 0;
                 s.hmass[i] = 0;
             }
@@ -671,10 +675,15 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
 #pragma unroll
             for (int k = 0; k < PPT; ++k) {
                 const int p = page_of(k / V, k % V);
-                const unsigned int rel = f2u(v[k]) - kmin;
+                const unsigned int rel = key[k] - kmin;
                 if (p >= lo && p < hi && (rel >> top) == pre) {
-                    const unsigned int bin = (rel >> shift) & (XS_BINS - 1);
-                    if (coverage) atomicAdd(&s.hmass[bin], mass_q(v[k], smax, a.score_kind));
+                    const unsigned int bin = xs_pad((rel >> shift) & (XS_BINS - 1));
+                    // an opaque copy keeps the compiler from computing every page's mass
+                    // ahead of the digit loop (only pages of the chosen bin need one)
+                    uint32_t kk = key[k];
+                    asm volatile("" : "+v"(kk));
+                    if (coverage)
+                        atomicAdd(&s.hmass[bin], mass_q(u2f(kk), smax, a.score_kind));
                     else atomicAdd(&s.hcnt[bin], 1u);
                 }
             }
@@ -688,7 +697,9 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
             if (wv == 0) {
                 const int c = min(s.ncand, XS_CAND);
                 const unsigned int kt = lane < c ? s.ckey[lane] : 0u;
-                const unsigned long long mt = lane < c ? s.cmass[lane] : 0ull;
+                // the candidates' masses (only they need one: computed here, not per page)
+                const unsigned long long mt =
+                    lane < c && coverage ? mass_q(u2f(kt + kmin), smax, a.score_kind) : 0ull;
                 const uint32_t mlo = (uint32_t)mt, mhi = (uint32_t)(mt >> 32);
                 unsigned int ab = 0, eq = 0;
                 unsigned long long am = 0, em = 0;
@@ -737,12 +748,18 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
         }
         tau = tau_rel + kmin;
         if (coverage) {
+            // ties needed: ceil(rem / wq) clamped to [1, count_eq], from a double estimate
+            // (off by at most one below 2^15) corrected with exact 64-bit products
             const unsigned long long rem = need - mab;
             const unsigned long long wq = mass_q(u2f(tau), smax, a.score_kind);
-            long long t = wq ? (long long)((rem + wq - 1) / wq) : (long long)count_eq;
-            if (t < 1) t = 1;
-            if (t > count_eq) t = count_eq;
-            take = (int)t;
+            int t = count_eq;
+            if (wq) {
+                const double e = ceil((double)rem / (double)wq);
+                t = e < (double)count_eq ? (int)e : count_eq;
+                while (t > 1 && (unsigned long long)(t - 1) * wq >= rem) --t;
+                while (t < count_eq && (unsigned long long)t * wq < rem) ++t;
+            }
+            take = count_eq >= 1 && t < 1 ? 1 : t;
         } else {
             take = b - cab;
         }
@@ -752,9 +769,10 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
     // ---- keep + ascending compaction --------------------------------------------------
     // A page is a sure keep (outside the selectable region, key > tau, or for the
     // threshold rule score >= tau) or a tie (key == tau, index rule); ties are kept in page
-    // order while their rank is < take, so pages kept before p = sure(<p) + min(ties(<p),
-    // take).  Page order is (chunk, thread, slot): per-(chunk, wave) counts, one
-    // exchange, then ballot prefixes inside the wave.
+    // order while their rank is < take, so a kept page goes to position sure(<p) +
+    // min(ties(<p), take).  Page order is (chunk, thread, slot): per chunk a wave scan of
+    // the threads' packed (ties << 16 | sures) counts, one exchange of the waves' totals,
+    // which every wave scans again.  Packed sums stay below 2^15 per field.
     const float ftau = u2f(tau);
     uint32_t sure_m = 0, tie_m = 0;              // bit k: page slot k
 #pragma unroll
@@ -765,66 +783,44 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
             if (keep_all || p < lo || p >= hi) {
                 su = true;
             } else if (a.tie_mode == 1) {
-                su = v[k] >= ftau;
+                su = u2f(key[k]) >= ftau;
             } else {
-                const unsigned int key = f2u(v[k]);
-                su = key > tau;
-                ti = key == tau;
+                su = key[k] > tau;
+                ti = key[k] == tau;
             }
         }
         sure_m |= (uint32_t)su << k;
         tie_m |= (uint32_t)ti << k;
     }
+    constexpr uint32_t VM = (1u << V) - 1u;
+    int excl[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        int sc = 0, tc = 0;
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-            sc += __popcll(__ballot((sure_m >> (c * V + i)) & 1u));
-            tc += __popcll(__ballot((tie_m >> (c * V + i)) & 1u));
-        }
-        if (lane == 0) { s.ccnt[c][wv][0] = sc; s.ccnt[c][wv][1] = tc; }
+        const int own = __popc((sure_m >> (c * V)) & VM) + (__popc((tie_m >> (c * V)) & VM) << 16);
+        const int incl = wave_incl_scan(own);
+        excl[c] = incl - own;
+        if (lane == WAVE - 1) s.cpk[c][wv] = incl;
     }
     __syncthreads();
-    int sure_tot = 0, tie_tot = 0;
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            sure_tot += s.ccnt[c][w][0];
-            tie_tot += s.ccnt[c][w][1];
-        }
-    const int cnt = sure_tot + min(tie_tot, take);
-    int sure_base = 0, tie_base = 0;            // pages of (chunk, wave)s before this one
+    int before = 0;                              // packed counts of the pages before a chunk
+    int base[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        int sb = sure_base, tb = tie_base;
+        const int wincl = wave_incl_scan(lane < NW ? s.cpk[c][lane] : 0);
+        const int wprev = wv > 0 ? __builtin_amdgcn_readlane(wincl, wv > 0 ? wv - 1 : 0) : 0;
+        base[c] = before + wprev + excl[c];
+        before += __builtin_amdgcn_readlane(wincl, NW - 1);
+    }
+    const int cnt = (before & 0xFFFF) + min(before >> 16, take);
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
-            if (w < wv) {
-                sb += s.ccnt[c][w][0];
-                tb += s.ccnt[c][w][1];
-            }
-        int rk = tb;                             // tie rank of this lane's first tie
+    for (int c = 0; c < NC; ++c) {
+        int sb = base[c] & 0xFFFF, tb = base[c] >> 16;
 #pragma unroll
-        for (int i = 0; i < V; ++i) rk += lanes_below(__ballot((tie_m >> (c * V + i)) & 1u));
-        bool keep[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) {            // lane-local ties in slot order
-            const bool ti = (tie_m >> (c * V + i)) & 1u;
-            keep[i] = ((sure_m >> (c * V + i)) & 1u) || (ti && rk < take);
-            rk += ti;
-        }
-        int pos = sb + min(tb, take);
-#pragma unroll
-        for (int i = 0; i < V; ++i) pos += lanes_below(__ballot(keep[i]));
-#pragma unroll
-        for (int i = 0; i < V; ++i)
-            if (keep[i]) tab[pos++] = page_of(c, i);
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            sure_base += s.ccnt[c][w][0];
-            tie_base += s.ccnt[c][w][1];
+        for (int i = 0; i < V; ++i) {
+            const bool su = (sure_m >> (c * V + i)) & 1u, ti = (tie_m >> (c * V + i)) & 1u;
+            if (su || (ti && tb < take)) tab[sb + min(tb, take)] = page_of(c, i);
+            sb += su;
+            tb += ti;
         }
     }
     for (int p = cnt + tid; p < MP; p += NT) tab[p] = -1;
