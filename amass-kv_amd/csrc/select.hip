@@ -260,7 +260,8 @@ constexpr int XS_THREADS_L = 1024;            // units of 4097 .. 8192 pages
 constexpr int XS_WAVES = XS_THREADS_L / WAVE; // exchange arrays sized for the larger block
 constexpr int XS_BITS = 11;                   // key bits per histogram digit
 constexpr int XS_BINS = 1 << XS_BITS;         // four bins per thread in the scan
-constexpr int XS_PBINS = XS_BINS + XS_BINS / 32;   // one unused slot after every 32 bins
+constexpr int XS_PBINS_M = XS_BINS + XS_BINS / 16;  // mass slots: 2 unused after every 32 bins
+constexpr int XS_PBINS_C = XS_BINS + XS_BINS / 8;   // count slots: 4 unused after every 32
 constexpr int XS_CAND = WAVE;                 // a bin this small is ranked by one wave
 constexpr int XS_TILE = 16;                   // pages per per-tile maximum of score_h
 constexpr int XS_FUSED = 64;                  // PPT * G floats of the fused nrm staging
@@ -268,13 +269,15 @@ constexpr int XS_MAXNC = 8;                   // chunks per thread at PPT = 32
 constexpr int NP_THREADS = 256;               // nrm pre-pass workgroup
 constexpr int NP_PAGES = 4 * NP_THREADS;      // pages per pre-pass workgroup
 
-// Histogram slot of bin b: one unused slot after every 32 bins, so the 64 lanes that each
-// read one 32-bin group (lane i: slots 33 i ..) spread evenly over the LDS banks.
-__device__ __forceinline__ unsigned int xs_pad(unsigned int b) { return b + (b >> 5); }
+// Histogram slots: each group of 32 bins starts on a 16-byte boundary followed by 16
+// unused bytes (mass group g at slot 34 g, count group g at slot 36 g), so the 64 lanes
+// that each read one group with 16-byte loads spread evenly over the LDS banks.
+__device__ __forceinline__ unsigned int xs_pad_m(unsigned int b) { return b + 2 * (b >> 5); }
+__device__ __forceinline__ unsigned int xs_pad_c(unsigned int b) { return b + 4 * (b >> 5); }
 
 struct __align__(16) XSel {
-    unsigned long long hmass[XS_PBINS];       // histogram: 2^-32 fixed-point masses
-    unsigned int hcnt[XS_PBINS];              //            and counts (bin b at xs_pad(b))
+    unsigned long long hmass[XS_PBINS_M];     // histogram: 2^-32 fixed-point masses
+    unsigned int hcnt[XS_PBINS_C];            //            and counts (bin b at xs_pad_*(b))
     unsigned int ckey[XS_CAND];               // candidates: relative keys
     unsigned long long ured[2][XS_WAVES];     // total / sink mass
     float hred[8][XS_WAVES];                  // per-head maxima
@@ -407,9 +410,9 @@ __global__ __launch_bounds__(NP_THREADS) void nrm_pass_kernel(const amass_select
 
 // The histogram search from the highest bin down: the bin where the cumulative weight
 // (mass in coverage mode, else count) from the top, after what earlier digits put above,
-// reaches `target`.  Wave 0 alone: lane i sums the 32 bins of super-bin i (bins
-// XS_BINS-1-32i down), one wave scan finds the super-bin and a second one, over its 32
-// bins, the bin; the finding lane appends the bin to the prefix (digit bits
+// reaches `target`.  Wave 0 alone: lane i sums the 32 bins of group 63 - i (bins
+// XS_BINS-1-32i down, 16-byte loads), one wave scan finds the group and a second one, over
+// its 32 bins, the bin; the finding lane appends the bin to the prefix (digit bits
 // [shift, top)) and adds the weight above it to the running total.  One barrier.
 __device__ void xs_find(XSel& s, bool by_mass, unsigned long long target, int shift, int top) {
     if (threadIdx.x < WAVE) {
@@ -417,14 +420,20 @@ __device__ void xs_find(XSel& s, bool by_mass, unsigned long long target, int sh
         const int g = WAVE - 1 - lane;                      // bins 32 g .. 32 g + 31
         unsigned long long sum = 0;
         if (by_mass) {
-            const unsigned long long* h = s.hmass + 33 * g;
+            const ulonglong2* h = reinterpret_cast<const ulonglong2*>(s.hmass + 34 * g);
+            ulonglong2 x[16];
 #pragma unroll
-            for (int j = 0; j < 32; ++j) sum += h[j];
+            for (int j = 0; j < 16; ++j) x[j] = h[j];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sum += x[j].x + x[j].y;
         } else {
-            const unsigned int* h = s.hcnt + 33 * g;
+            const uint4* h = reinterpret_cast<const uint4*>(s.hcnt + 36 * g);
+            uint4 x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = h[j];
             unsigned int c = 0;
 #pragma unroll
-            for (int j = 0; j < 32; ++j) c += h[j];
+            for (int j = 0; j < 8; ++j) c += (x[j].x + x[j].y) + (x[j].z + x[j].w);
             sum = c;
         }
         const unsigned long long above0 =
@@ -434,9 +443,10 @@ __device__ void xs_find(XSel& s, bool by_mass, unsigned long long target, int sh
         const int L = hit ? __ffsll((long long)hit) - 1 : WAVE - 1;
         const unsigned long long base = above0 + readlane_u64(incl - sum, L);
         const int hL = XS_BINS - 1 - 32 * L;                // group L's highest bin
-        const int sl = 33 * (WAVE - 1 - L) + 31 - lane;     // its slots from the top
+        const int gl = WAVE - 1 - L, bl = 31 - lane;         // its bins from the top
         const unsigned long long m =
-            lane < 32 ? (by_mass ? s.hmass[sl] : (unsigned long long)s.hcnt[sl]) : 0ull;
+            lane < 32 ? (by_mass ? s.hmass[34 * gl + bl] : (unsigned long long)s.hcnt[36 * gl + bl])
+                      : 0ull;
         const unsigned long long incl2 = wave_incl_scan_u64(m);
         const unsigned long long hit2 = __ballot(lane < 32 && base + incl2 >= target);
         const int j = hit2 ? __ffsll((long long)hit2) - 1 : 31;
@@ -504,9 +514,9 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
     const int lo = sink, hi = nsh;              // selectable [lo, hi) when !keep_all
     int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kh * a.pt_sh;
 
-    for (int i = tid; i < XS_PBINS; i += NT) {
+    for (int i = tid; i < XS_PBINS_C; i += NT) {
         s.hcnt[i] = 0;
-        s.hmass[i] = 0;
+        if (i < XS_PBINS_M) s.hmass[i] = 0;
     }
     if (tid == 0) {
         s.prefix = 0;
@@ -598,9 +608,9 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                         const unsigned long long w = mass_q(u2f(key[k]), smax, a.score_kind);
                         tot += w;
                         if (p < sink) snk += w;
-                        if (sel) atomicAdd(&s.hmass[xs_pad((key[k] - kmin) >> shift)], w);
+                        if (sel) atomicAdd(&s.hmass[xs_pad_m((key[k] - kmin) >> shift)], w);
                     } else if (sel && b != 1) {
-                        atomicAdd(&s.hcnt[xs_pad((key[k] - kmin) >> shift)], 1u);
+                        atomicAdd(&s.hcnt[xs_pad_c((key[k] - kmin) >> shift)], 1u);
                     }
                 }
             }
@@ -663,9 +673,9 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 if (shift == 0 || s.ncand <= XS_CAND) break;
             }
             // the next 11 bits of the keys inside the chosen bin
-            for (int i = tid; i < XS_PBINS; i += NT) {
+            for (int i = tid; i < XS_PBINS_C; i += NT) {
                 s.hcnt[i] = 0;
-                s.hmass[i] = 0;
+                if (i < XS_PBINS_M) s.hmass[i] = 0;
             }
             __syncthreads();
             if (tid == 0) s.ncand = 0;          // every thread read it before the barrier
@@ -677,14 +687,14 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
                 const int p = page_of(k / V, k % V);
                 const unsigned int rel = key[k] - kmin;
                 if (p >= lo && p < hi && (rel >> top) == pre) {
-                    const unsigned int bin = xs_pad((rel >> shift) & (XS_BINS - 1));
+                    const unsigned int bin = (rel >> shift) & (XS_BINS - 1);
                     // an opaque copy keeps the compiler from computing every page's mass
                     // ahead of the digit loop (only pages of the chosen bin need one)
                     uint32_t kk = key[k];
                     asm volatile("" : "+v"(kk));
                     if (coverage)
-                        atomicAdd(&s.hmass[bin], mass_q(u2f(kk), smax, a.score_kind));
-                    else atomicAdd(&s.hcnt[bin], 1u);
+                        atomicAdd(&s.hmass[xs_pad_m(bin)], mass_q(u2f(kk), smax, a.score_kind));
+                    else atomicAdd(&s.hcnt[xs_pad_c(bin)], 1u);
                 }
             }
             __syncthreads();
