@@ -174,6 +174,40 @@ __device__ __forceinline__ unsigned long long wave_incl_scan_u64(unsigned long l
     return v + (row >= 1 ? r0 : 0ull) + (row >= 2 ? r1 : 0ull) + (row >= 3 ? r2 : 0ull);
 }
 
+// Lane pairs l, l^16 and l, l^32 through the gfx950 permlane swaps (no LDS round trip):
+// with both operands v, permlane16_swap returns (v[l], v[l^16]) up to order and
+// permlane32_swap (v[l], v[l^32]); max and sum are symmetric in the pair.
+__device__ __forceinline__ float xor16_maxf(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xor32_maxf(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xor16_sumf(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor32_sumf(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// max over the 16 lanes of a row (every lane of the row gets it); all lanes active
+__device__ __forceinline__ float row16_maxf(float v) {
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    return v;
+}
+// v[l ^ 32] (the upper half reads the lower one's value and vice versa)
+__device__ __forceinline__ float xor32_f(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? p[0] : p[1]);
+}
+
 // full-wave reductions (result in every lane)
 __device__ __forceinline__ float wave_maxf(float v) {
 #pragma unroll

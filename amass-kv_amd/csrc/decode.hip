@@ -126,8 +126,7 @@ __device__ __forceinline__ void attend_page(const PageData& pd, const bf16x4_t (
         if (t0 + j >= valid_t) s[j] = -INFINITY;
     }
     float ml = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    ml = fmaxf(ml, __shfl_xor(ml, 16, WAVE));
-    ml = fmaxf(ml, __shfl_xor(ml, 32, WAVE));
+    ml = xor32_maxf(xor16_maxf(ml));
     const float mn = fmaxf(st.m, ml);
     const float alpha = __expf(st.m - mn);
     float p[4];
@@ -408,8 +407,7 @@ __global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_de
             load_q(a, r, kh, lane, qb);
             attend_run<VSRC, DENSE>(a, r, kh, sl, w, cnt, hw, lane, qb, st);
         }
-        float lt = st.l + __shfl_xor(st.l, 16, WAVE);
-        lt += __shfl_xor(lt, 32, WAVE);
+        const float lt = xor32_sumf(xor16_sumf(st.l));
         if (lane < a.G) {
             sm_m[w][lane] = st.m;
             sm_l[w][lane] = lt;
@@ -455,8 +453,7 @@ __global__ __launch_bounds__(DEC_WAVES * WAVE) void decode_kernel(const amass_de
         attend_run<VSRC, DENSE>(a, r, kh, sl, s, cnt, S, lane, qb, st);
     }
     if (plan != 2 && s == 0 && lane == 0) *split_count_slot(a, r, kh) = S;
-    float lt = st.l + __shfl_xor(st.l, 16, WAVE);   // sum over lanes g, g+16, g+32, g+48
-    lt += __shfl_xor(lt, 32, WAVE);
+    const float lt = xor32_sumf(xor16_sumf(st.l));   // sum over lanes g, g+16, g+32, g+48
     // this lane holds rows g = 4 (l/16) + j, columns d = 8 (l%16) .. +8 of the O tiles
     const int d0 = 8 * (lane & 15);
     if (S == 1) {

@@ -227,7 +227,7 @@ __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (
         const int64_t row = (int64_t)req * p.sh_sr + (int64_t)h * p.sh_sh;
         if (p.G <= 4) {
             // lanes kg 2,3 take g 1,3 from lanes kg 0,1: one store per lane
-            const float odd = __shfl_xor(S[1], 32, WAVE);
+            const float odd = xor32_f(S[1]);
             const int g = kg < 2 ? 2 * kg : 2 * kg - 3;
             const float v = kg < 2 ? S[0] : odd;
             if (valid && g < p.G) p.score_h[row + g * (int)p.sh_sg + page] = v;
@@ -239,11 +239,8 @@ __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (
         if (p.tmax) {
             // the tile's maximum of S_g0 / S_g1: the 16 lanes of row kg hold its 16 pages
             float m0 = valid ? S[0] : -INFINITY, m1 = valid ? S[1] : -INFINITY;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                m0 = fmaxf(m0, __shfl_xor(m0, o, WAVE));
-                m1 = fmaxf(m1, __shfl_xor(m1, o, WAVE));
-            }
+            m0 = row16_maxf(m0);
+            m1 = row16_maxf(m1);
             if (n == 0) {
                 const int64_t t = (int64_t)req * p.tm_sr + (int64_t)h * p.tm_sh + tile;
                 if (g0 < p.G) p.tmax[t + g0 * p.tm_sg] = m0;
@@ -252,8 +249,8 @@ __device__ __forceinline__ void tile_finish(const QuadParams& p, const i32x4_t (
         }
     } else {
         float m = g0 < p.G ? (g1 < p.G ? fmaxf(S[0], S[1]) : S[0]) : -INFINITY;
-        if (p.G > 2) m = fmaxf(m, __shfl_xor(m, 16, WAVE));
-        if (p.G > 4) m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+        if (p.G > 2) m = xor16_maxf(m);
+        if (p.G > 4) m = xor32_maxf(m);
         if (valid && kg == 0)
             p.score[(int64_t)req * p.sc_sr + (int64_t)h * p.sc_sh + page] = m;
     }

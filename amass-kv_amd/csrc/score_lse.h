@@ -340,20 +340,14 @@ __device__ __forceinline__ void r8_lse(const R8GroupC<R8Split<G>::TPL * RP * CBI
         float m = lg[e][0];
 #pragma unroll
         for (int t = 1; t < TPL; ++t) m = fmaxf(m, lg[e][t]);
-        if constexpr (GP == 2) m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-        if constexpr (GP == 1) {
-            m = fmaxf(m, __shfl_xor(m, 16, WAVE));
-            m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-        }
+        if constexpr (GP == 2) m = xor32_maxf(m);
+        if constexpr (GP == 1) m = xor32_maxf(xor16_maxf(m));
         const float mm = m == -INFINITY ? 0.f : m;
         float se = 0.f;
 #pragma unroll
         for (int t = 0; t < TPL; ++t) se += __builtin_amdgcn_exp2f(lg[e][t] - mm);
-        if constexpr (GP == 2) se += __shfl_xor(se, 32, WAVE);
-        if constexpr (GP == 1) {
-            se += __shfl_xor(se, 16, WAVE);
-            se += __shfl_xor(se, 32, WAVE);
-        }
+        if constexpr (GP == 2) se = xor32_sumf(se);
+        if constexpr (GP == 1) se = xor32_sumf(xor16_sumf(se));
         lse[e] = 0.69314718055994531f * (m + __builtin_amdgcn_logf(se));
     }
 }
@@ -390,11 +384,8 @@ __device__ __forceinline__ void r8_tile_tail(const R8Params& p,
         if (p.tmax) {
             // the tile's maximum per head: the 16 lanes of row kg hold its 16 pages
             float m0 = valid ? S[0] : -INFINITY, m1 = valid ? S[1] : -INFINITY;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                m0 = fmaxf(m0, __shfl_xor(m0, o, WAVE));
-                m1 = fmaxf(m1, __shfl_xor(m1, o, WAVE));
-            }
+            m0 = row16_maxf(m0);
+            m1 = row16_maxf(m1);
             if (part == 0 && (threadIdx.x & 15) == 0) {
                 const int64_t t = (int64_t)req * p.tm_sr + (int64_t)h * p.tm_sh +
                                   page / SC_TILE;
@@ -405,11 +396,8 @@ __device__ __forceinline__ void r8_tile_tail(const R8Params& p,
         return;
     }
     float smax = G >= 2 ? fmaxf(S[0], S[1]) : S[0];
-    if constexpr (GP == 4) {
-        smax = fmaxf(smax, __shfl_xor(smax, 16, WAVE));
-        smax = fmaxf(smax, __shfl_xor(smax, 32, WAVE));
-    }
-    if constexpr (GP == 2) smax = fmaxf(smax, __shfl_xor(smax, 16, WAVE));
+    if constexpr (GP == 4) smax = xor32_maxf(xor16_maxf(smax));
+    if constexpr (GP == 2) smax = xor16_maxf(smax);
     if (valid && kg == 0) p.score[(int64_t)req * p.sc_sr + (int64_t)h * p.sc_sh + page] = smax;
 }
 
@@ -489,8 +477,7 @@ void r8_score_kernel(const R8Params p) {
                 const float lo = bf16lo(qw[t][i]), hi = bf16hi(qw[t][i]);
                 ss += lo * lo + hi * hi;
             }
-        ss += __shfl_xor(ss, 16, WAVE);                // the row's four 32-d quarters
-        ss += __shfl_xor(ss, 32, WAVE);
+        ss = xor32_sumf(xor16_sumf(ss));               // the row's four 32-d quarters
         qsq0 = __shfl(ss, 4 * kg, WAVE);               // rows 4kg, 4kg+2: g0, g1
         qsq1 = __shfl(ss, 4 * kg + 2, WAVE);
     }

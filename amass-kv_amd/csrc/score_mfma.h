@@ -157,8 +157,7 @@ __device__ __forceinline__ float quantize_q_rows(const uint32_t (&qw)[2][8], int
         for (int i = 0; i < 8; ++i)
             amax = max(amax, max(qw[t][i] & 0x7FFFu, (qw[t][i] >> 16) & 0x7FFFu));
     float mx = __uint_as_float(amax << 16);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+    mx = xor32_maxf(xor16_maxf(mx));
     mx = fmaxf(mx, 1e-12f);
     const float qs = mx / 16383.0f;            // correctly rounded divides
     const float inv = 16383.0f / mx;
@@ -312,10 +311,10 @@ __device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int tar
         if (x < before + in_batch) {
             const unsigned long long hit = __ballot(before + incl > x);
             const int src = __ffsll((long long)hit) - 1;
-            const int excl = __shfl(incl - nw, src, WAVE);
-            const int tr = __shfl(t, src, WAVE);
+            const int excl = __builtin_amdgcn_readlane(incl - nw, src);
+            const int tr = __builtin_amdgcn_readlane(t, src);
             w.req = base + src;
-            w.stride = __shfl(nw, src, WAVE);
+            w.stride = __builtin_amdgcn_readlane(nw, src);
             w.first = x - before - excl;
             w.count = (tr - w.first + w.stride - 1) / w.stride;
             return true;
