@@ -250,3 +250,64 @@ def test_tile_maxima_equal_the_max_pass(G, coords):
     tab, cnt, _ = osel.select(outs[0][0], npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
                               max_pages=st.max_pages, mode=1, coverage=0.95, score_kind=1)
     assert np.array_equal(outs[0][1], tab) and np.array_equal(outs[0][2], cnt)
+
+
+def _tile_max(sh, nsh):
+    """Per-16-page-tile per-head maxima of score_h over each row's scored pages (what the
+    score launch writes into st.score_tmax)."""
+    R, n_kv, G, MP = sh.shape
+    nt = (MP + 15) // 16
+    pad = np.full((R, n_kv, G, nt * 16), -np.inf, np.float32)
+    for r in range(R):
+        n = max(int(nsh[r]), 0)
+        pad[r, ..., :n] = sh[r, ..., :n]
+    return pad.reshape(R, n_kv, G, nt, 16).max(axis=-1)
+
+
+@pytest.mark.parametrize("case", ["plain", "sink_covers", "full_coverage_tiny", "wide"])
+def test_fused_coverage_edges(case):
+    """The fused nrm selection (per-head maxima from the tile maxima) at its edge cases:
+    rows whose sinks alone cover the need (one selectable page kept), coverage 1.0 over
+    masses down to e^-60 (the cut falls on the smallest nonzero 2^-32 mass quantum), and
+    wide score spreads.  The page tables equal the oracle's on the GPU's combined
+    scores, and the combined scores equal the standalone nrm combine's."""
+    announce(f"fused coverage {case}")
+    gen = torch.Generator().manual_seed({"plain": 1, "sink_covers": 2,
+                                         "full_coverage_tiny": 3, "wide": 4}[case])
+    R, MP, G = 6, 1000, 4
+    st = _state(R, MP, G=G, combine="nrm")
+    cov = {"plain": 0.95, "sink_covers": 0.95, "full_coverage_tiny": 1.0, "wide": 0.99}[case]
+    st.coverage = cov
+    sl = _seq_lens(R, MP, gen)
+    sl[4] = MP * 16
+    sl[5] = 700 * 16 + 3
+    sl_d = sl.to(DEV)
+    derive_page_params(st, sl_d, R)
+    sh = torch.randn(R, 8, G, MP, generator=gen) * 2
+    if case == "sink_covers":
+        sh[:, :, :, 0] = 40.0                      # page 0 (the sink) holds every head's max
+    elif case == "full_coverage_tiny":
+        sh = -torch.rand(R, 8, G, MP, generator=gen) * 60.0   # exp down to e^-60
+        sh[:, :, :, 1] = 0.5                        # one dominant selectable page
+    elif case == "wide":
+        sh = sh * 12.0
+    st.score_h.copy_(sh.to(DEV))
+    nsh = npi(st.n_sel_hi)
+    st.score_tmax.copy_(torch.from_numpy(_tile_max(sh.numpy(), nsh)).to(DEV))
+    st.page_table.fill_(-7)
+    select_pages(st, R, score_h=st.score_h, tile_max=st.score_tmax)
+    torch.cuda.synchronize()
+    got_score, got_tab, got_cnt = npf(st.score), npi(st.page_table), npi(st.page_cnt)
+    from amass.selection import nrm_combine
+    st.score.fill_(0)
+    nrm_combine(st, R)
+    torch.cuda.synchronize()
+    ref_score = npf(st.score)
+    for r in range(R):
+        n = max(int(nsh[r]), 0)
+        assert np.array_equal(got_score[r, :, :n], ref_score[r, :, :n])
+    ref_tab, ref_cnt, _ = osel.select(got_score, npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                                      max_pages=MP, mode=1, coverage=cov, tie_mode=0,
+                                      score_kind=1)
+    assert np.array_equal(got_cnt, ref_cnt)
+    assert np.array_equal(got_tab, ref_tab)
