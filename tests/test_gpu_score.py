@@ -84,7 +84,8 @@ def test_quad_nrm(rank, v_bits):
         n = int(nsh[r])
         assert rel_close(sh[r, :, :, :n], ref_h[r, :, :, :n], 1) <= 1e-3
     # nrm of the GPU's own per-head scores: fp64 oracle vs the fp32 kernel
-    ref_n = osc.nrm_combine(sh.astype(np.float64), nsh)
+    with np.errstate(invalid="ignore"):   # pages past n_sel_hi hold unwritten bits
+        ref_n = osc.nrm_combine(sh.astype(np.float64), nsh)
     sc = npf(st.score)
     for r in range(B):
         n = int(nsh[r])
