@@ -497,12 +497,21 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) ld_pages<V>(gscore, page_of(c, 0), MP, vec, 0.f, &v[c * V]);
     }
-    // fused: tile t's maxima (tiles < ceil(MP / 16) <= NT, in bounds), masked below
+    // fused: every wave loads all of the row's tile maxima (lane l: tiles l + 64 i, in
+    // bounds: tiles < ceil(MP / 16) <= PPT NT / 16) and reduces them itself, masked below,
+    // so the per-head maxima need no exchange between the waves
+    constexpr int TL = NRM ? (PPT * NT / XS_TILE + WAVE - 1) / WAVE : 1;
+    float tv[NRM ? 8 : 1][TL];
     if constexpr (NRM) {
         const float* tm = a.tile_max + (int64_t)r * a.tm_sr + (int64_t)kh * a.tm_sh;
         const int ntm = (MP + XS_TILE - 1) / XS_TILE;
 #pragma unroll
-        for (int g = 0; g < 8; ++g) m[g] = (g < a.G && tid < ntm) ? tm[g * a.tm_sg + tid] : -INFINITY;
+        for (int g = 0; g < 8; ++g)
+#pragma unroll
+            for (int i = 0; i < TL; ++i) {
+                const int t = lane + WAVE * i;
+                tv[g][i] = (g < a.G && t < ntm) ? tm[g * a.tm_sg + t] : -INFINITY;
+            }
     }
     const int np = min(a.n_pages[r], MP);       // a row never exceeds its table width
     const int nsh = min(a.n_sel_hi[r], np);
@@ -527,11 +536,15 @@ __global__ __launch_bounds__(NT) void select_kernel(const amass_select_args a) {
         s.ncand = 0;
     }
     if constexpr (NRM) {
-        if (tid >= (nsc + XS_TILE - 1) / XS_TILE) {
+        const int nt = (nsc + XS_TILE - 1) / XS_TILE;
 #pragma unroll
-            for (int g = 0; g < 8; ++g) m[g] = -INFINITY;
+        for (int g = 0; g < 8; ++g) {
+            float x = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < TL; ++i)
+                if (lane + WAVE * i < nt) x = fmaxf(x, tv[g][i]);
+            m[g] = g < a.G ? wave_maxf_uniform(x) : -INFINITY;
         }
-        block_head_max<NW, XS_WAVES>(m, a.G, s.hred);
         const bool vec = (((uintptr_t)gscore) & 15) == 0;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
