@@ -18,7 +18,11 @@ Score patterns target the selection's radix search: i.i.d. normal, a small value
 bins of more than 64 candidates), +0.0 / -0.0 mixtures (one tie class), and magnitudes
 over 60 decades.  Page counts span every thread layout of the selection (1..8 pages per
 thread of 512, 8 of 1024, 32 of 512) and the decode's whole / split / fused layouts with
-ragged and empty units and NaN-poisoned slots past each sequence's end.
+ragged and empty units and NaN-poisoned slots past each sequence's end.  The nrm selection
+from per-head scores and per-tile maxima (the fused staging and the pre-pass) runs over
+generated GQA groups, lengths and head-score patterns (normal, a value pool with ties,
+masses over ~100 nats, a sink page holding every head's maximum): its combined scores are
+bit-identical to the standalone combine and its page tables equal the oracle's.
 """
 import numpy as np
 import pytest
@@ -116,6 +120,86 @@ def _selection_example(c):
     assert np.array_equal(npi(st.page_table), tab)
     if c["tie"] == 0:
         assert np.array_equal(npi(st.n_sel), nsel)
+
+
+# the nrm selection from per-head scores and per-tile maxima: the fused staging (PPT G <=
+# 64) and the multi-workgroup pre-pass (8192 pages at G = 8, or any G beyond 4096 pages)
+NRM_MPS = (2, 63, 513, 1024, 2047, 4096, 8192)
+NRM_PATTERNS = ("normal", "ties", "spread", "sink")
+
+
+def _head_scores(rng, shape, pattern):
+    if pattern == "normal":
+        return (rng.standard_normal(shape) * 3).astype(np.float32)
+    if pattern == "ties":
+        pool = np.array([-6.0, -1.0, 0.0, 0.0, 2.5], np.float32)
+        return pool[rng.integers(0, pool.size, shape)]
+    if pattern == "spread":                    # exp() masses over ~100 nats
+        return (rng.standard_normal(shape) * 25).astype(np.float32)
+    x = (rng.standard_normal(shape) * 2).astype(np.float32)
+    x[..., 0] = 30.0                            # the sink page holds every head's maximum
+    return x
+
+
+@hs.composite
+def nrm_selection_cases(draw, MP):
+    R = draw(hs.integers(1, 3))
+    return dict(R=R, n_kv=draw(hs.sampled_from([1, 2, 8])), G=draw(hs.sampled_from([1, 2, 4, 8])),
+                MP=MP, lens=draw(hs.lists(hs.integers(0, MP * 16), min_size=R, max_size=R)),
+                pattern=draw(hs.sampled_from(NRM_PATTERNS)),
+                seed=draw(hs.integers(0, 2 ** 31 - 1)), mode=draw(hs.integers(0, 1)),
+                tie=draw(hs.integers(0, 1)), cov=draw(hs.floats(0.01, 1.0)),
+                budget=draw(hs.floats(0.001, 1.0)))
+
+
+@pytest.mark.parametrize("MP", NRM_MPS)
+def test_nrm_selection_from_tile_maxima_matches_oracle(MP):
+    """select_pages with score_h and the per-tile maxima (the path the quad and CLSE
+    steps take): the combined scores equal the standalone two-pass nrm combine bit for
+    bit, and the page tables and counts equal the oracle's on those scores."""
+    @PROPS
+    @given(c=nrm_selection_cases(MP))
+    def prop(c):
+        _nrm_selection_example(c)
+    prop()
+
+
+def _nrm_selection_example(c):
+    announce(f"nrm selection property case {c}")
+    from amass.selection import nrm_combine
+    from amass.selection.select import _select
+    R, n_kv, G, MP = c["R"], c["n_kv"], c["G"], c["MP"]
+    rng = np.random.default_rng(c["seed"])
+    sh = _head_scores(rng, (R, n_kv, G, MP), c["pattern"])
+    st = QuadState(DEV, num_layers=1, num_blocks=4, n_kv=n_kv, G=G, head_dim=128, page=16,
+                   max_reqs=R, max_pages=MP, rank=2, budget=c["budget"], combine="nrm")
+    derive_page_params(st, torch.tensor(c["lens"], dtype=torch.int32, device=DEV), R)
+    nsh = npi(st.n_sel_hi)
+    nt = (MP + 15) // 16
+    pad = np.full((R, n_kv, G, nt * 16), -np.inf, np.float32)
+    for r in range(R):
+        n = max(int(nsh[r]), 0)
+        pad[r, ..., :n] = sh[r, ..., :n]
+    st.score_h.copy_(torch.from_numpy(sh).to(DEV))
+    st.score_tmax.copy_(torch.from_numpy(pad.reshape(R, n_kv, G, nt, 16).max(-1)).to(DEV))
+    st.page_table.fill_(-7)
+    tie = ["index", "all"][c["tie"]]
+    _select(st, R, mode="coverage" if c["mode"] else "topb", coverage=c["cov"],
+            score_h=st.score_h, tile_max=st.score_tmax, tie_mode=tie)
+    torch.cuda.synchronize()
+    got_sc, got_tab, got_cnt = npf(st.score), npi(st.page_table), npi(st.page_cnt)
+    st.score.fill_(0)
+    nrm_combine(st, R)
+    torch.cuda.synchronize()
+    ref_sc = npf(st.score)
+    for r in range(R):
+        n = max(int(nsh[r]), 0)
+        assert np.array_equal(got_sc[r, :, :n].view(np.uint32), ref_sc[r, :, :n].view(np.uint32))
+    tab, cnt, _ = osel.select(got_sc, npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
+                              max_pages=MP, mode=c["mode"], coverage=c["cov"],
+                              tie_mode=c["tie"], score_kind=1)
+    assert np.array_equal(got_cnt, cnt)
+    assert np.array_equal(got_tab, tab)
 
 
 @hs.composite
