@@ -271,7 +271,7 @@ void quad_score_kernel(const QuadParams p) {
     TileWalk tw;
     if (!tile_walk(p.nsh, p.n_req, p.target, blockIdx.x, tw) || tw.count <= 0) return;
     const int req = tw.req;
-    const int nsh = p.nsh[req];
+    const int nsh = tw.nsh;
     const int cnt = tw.count;
     const int t0 = tw.first;
     const int wstride = tw.stride;

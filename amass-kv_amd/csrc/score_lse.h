@@ -419,7 +419,7 @@ void r8_score_kernel(const R8Params p) {
     TileWalk tw;
     if (!tile_walk(p.nsh, p.n_req, p.target, blockIdx.x, tw) || tw.count <= 0) return;
     const int req = tw.req;
-    const int nsh = p.nsh[req];
+    const int nsh = tw.nsh;
     const int sl = p.sl[req];
     const int cnt = tw.count;
     const int t0 = tw.first;

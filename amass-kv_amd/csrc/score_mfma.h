@@ -256,6 +256,7 @@ struct TileWalk {
     int first;     // first tile
     int stride;    // tile stride (workgroups of the request)
     int count;     // tiles walked
+    int nsh;       // the request's n_sel_hi (taken from the walk's own loads)
 };
 
 __device__ __forceinline__ int tiles_of(int nsh) {
@@ -300,11 +301,13 @@ __device__ __forceinline__ int walk_tpw(const int32_t* nsh, int n_req, int targe
 __device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int target, int x,
                                           TileWalk& w) {
     const int lane = threadIdx.x & 63;
-    const int t0 = lane_tiles(nsh, n_req, 0);
+    const int v0 = lane < n_req ? nsh[lane] : 0;
+    const int t0 = tiles_of(v0);
     const int tpw = walk_tpw(nsh, n_req, target, t0);
     int before = 0;                                     // workgroups of earlier batches
     for (int base = 0; base < n_req; base += WAVE) {
-        const int t = base == 0 ? t0 : lane_tiles(nsh, n_req, base);
+        const int v = base == 0 ? v0 : (base + lane < n_req ? nsh[base + lane] : 0);
+        const int t = tiles_of(v);
         const int nw = (t + tpw - 1) / tpw;
         const int incl = wave_incl_scan(nw);
         const int in_batch = __builtin_amdgcn_readlane(incl, WAVE - 1);
@@ -314,6 +317,7 @@ __device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int tar
             const int excl = __builtin_amdgcn_readlane(incl - nw, src);
             const int tr = __builtin_amdgcn_readlane(t, src);
             w.req = base + src;
+            w.nsh = __builtin_amdgcn_readlane(v, src);
             w.stride = __builtin_amdgcn_readlane(nw, src);
             w.first = x - before - excl;
             w.count = (tr - w.first + w.stride - 1) / w.stride;
