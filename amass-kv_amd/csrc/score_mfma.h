@@ -161,7 +161,7 @@ __device__ __forceinline__ float quantize_q_rows(const uint32_t (&qw)[2][8], int
     mx = fmaxf(mx, 1e-12f);
     const float qs = mx / 16383.0f;            // correctly rounded divides
     const float inv = 16383.0f / mx;
-    const int limb = n & 1;
+    const bool lo_limb = n & 1;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -172,11 +172,13 @@ __device__ __forceinline__ float quantize_q_rows(const uint32_t (&qw)[2][8], int
                 const int e = 4 * wi + j;
                 const uint32_t wv = qw[t][e >> 1];
                 const float fv = (e & 1) ? bf16hi(wv) : bf16lo(wv);
-                int qi = (int)rintf(__fmul_rn(fv, inv));
-                qi = max(-16383, min(16383, qi));
-                int hi = (int)rintf((float)qi * 0.0078125f);
-                hi = max(-127, min(127, hi));
-                const int v = limb ? qi - 128 * hi : hi;
+                // qi = rint(q / qs) clamped to +-16383, hi = rint(qi / 128) clamped to
+                // +-127, lo = qi - 128 hi: small integers, exact in fp32, so the limbs are
+                // formed without integer round trips and converted once
+                const float qf = __builtin_amdgcn_fmed3f(rintf(__fmul_rn(fv, inv)), -16383.0f,
+                                                         16383.0f);
+                const float hf = __builtin_amdgcn_fmed3f(rintf(qf * 0.0078125f), -127.0f, 127.0f);
+                const int v = (int)(lo_limb ? fmaf(-128.0f, hf, qf) : hf);
                 word |= ((uint32_t)(v & 0xFF)) << (8 * j);
             }
             qa[t][wi] = (int)word;
