@@ -243,15 +243,17 @@ __global__ __launch_bounds__(SEL_THREADS) void nrm_kernel(const amass_nrm_args a
 // registers from the first load to the page-table write, so every phase reads registers
 // and LDS carries only the histogram and small exchanges.  Phases:
 //   stage    plain scores, or the fused nrm combine over score_h with the per-head maxima
-//            taken from the score launch's per-tile maxima; the loads cover the row's
-//            MP pages and are issued before n_sel_hi arrives (the rows are MP wide);
+//            that every wave reduces itself from the score launch's per-tile maxima; the
+//            loads cover the row's MP pages and are issued before n_sel_hi arrives (the
+//            rows are MP wide); from then on each thread holds its pages' order keys;
 //   search   tau = the b-th largest key (count) or the key where the mass from the top
 //            reaches `need` (coverage): 2048-bin histograms of the key relative to the
 //            unit's smallest selectable key, 11 bits at a time from its highest set bit,
-//            each followed by a block scan; a chosen bin of <= 64 keys is ranked by one
-//            wave, exactly;
-//   compact  per-(chunk, wave) keep / tie counts, one exchange, then every thread
-//            writes its kept pages at their ranks (ascending page ids).
+//            each searched by one wave in two levels (xs_find); a chosen bin of <= 64
+//            keys is ranked by one wave, exactly;
+//   compact  per-chunk wave scans of packed keep / tie counts, one exchange, then every
+//            thread writes its kept pages at their ranks (ascending page ids).
+// Every cross-lane reduction and scan uses DPP row steps and readlane (no LDS permutes).
 // Large nrm units (MP G beyond the fused staging's registers) get a pre-pass over many
 // workgroups (nrm_pass_kernel) that writes the combined scores; the selection then reads
 // those.  Without per-tile maxima the standalone two-pass nrm_kernel does that.
@@ -259,7 +261,7 @@ constexpr int XS_THREADS = 512;              // units up to 4096 pages (and abov
 constexpr int XS_THREADS_L = 1024;            // units of 4097 .. 8192 pages
 constexpr int XS_WAVES = XS_THREADS_L / WAVE; // exchange arrays sized for the larger block
 constexpr int XS_BITS = 11;                   // key bits per histogram digit
-constexpr int XS_BINS = 1 << XS_BITS;         // four bins per thread in the scan
+constexpr int XS_BINS = 1 << XS_BITS;         // 64 groups of 32 for the two-level search
 constexpr int XS_PBINS_M = XS_BINS + XS_BINS / 16;  // mass slots: 2 unused after every 32 bins
 constexpr int XS_PBINS_C = XS_BINS + XS_BINS / 8;   // count slots: 4 unused after every 32
 constexpr int XS_CAND = WAVE;                 // a bin this small is ranked by one wave
@@ -280,7 +282,6 @@ struct __align__(16) XSel {
     unsigned int hcnt[XS_PBINS_C];            //            and counts (bin b at xs_pad_*(b))
     unsigned int ckey[XS_CAND];               // candidates: relative keys
     unsigned long long ured[2][XS_WAVES];     // total / sink mass
-    float hred[8][XS_WAVES];                  // per-head maxima
     float fred[XS_WAVES];                     // score max
     unsigned int kred[2][XS_WAVES];           // selectable key min / max
     int cpk[XS_MAXNC][XS_WAVES];              // compaction: packed tie / sure counts per wave
