@@ -23,12 +23,7 @@ constexpr int ST_WAVES = ST_THREADS / WAVE;
 __device__ __forceinline__ int st_excl_scan(int v, int* red, int& total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, WAVE);
-        if (lane >= o) x += y;
-    }
+    const int x = wave_incl_scan(v);                  // DPP row steps + readlane
     __syncthreads();
     if (lane == 63) red[w] = x;
     __syncthreads();

@@ -28,12 +28,7 @@ template <int NT>
 __device__ __forceinline__ int blk_excl_scan(int v, int* red, int& total) {
     constexpr int NW = NT / WAVE;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, WAVE);
-        if (lane >= o) x += y;
-    }
+    const int x = wave_incl_scan(v);                  // DPP row steps + readlane
     __syncthreads();
     if (lane == 63) red[w] = x;
     __syncthreads();
@@ -178,12 +173,9 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     int U;
     int upos = blk_excl_scan<TP_THREADS>(nun, red, U);
     {
-        int km = kmax, kn = kmin;
-#pragma unroll
-        for (int o2 = 32; o2 >= 1; o2 >>= 1) {
-            km = max(km, __shfl_xor(km, o2, WAVE));
-            kn = min(kn, __shfl_xor(kn, o2, WAVE));
-        }
+        // clocks are >= 0: their unsigned order is their order
+        const int km = (int)wave_maxu_uniform((uint32_t)kmax);
+        const int kn = (int)wave_minu_uniform((uint32_t)kmin);
         if ((tid & 63) == 0) {
             smax_s[tid >> 6] = km;
             smin_s[tid >> 6] = kn;
@@ -216,12 +208,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         // inclusive scan of the 256 bins (first four waves), then B = the first bin whose
         // running count reaches Mnew and the quota taken from it
         const int lane = tid & 63, w = tid >> 6;
-        int x = tid < 256 ? hist[tid] : 0;
-#pragma unroll
-        for (int o2 = 1; o2 < 64; o2 <<= 1) {
-            const int y = __shfl_up(x, o2, WAVE);
-            if (lane >= o2) x += y;
-        }
+        const int x = wave_incl_scan(tid < 256 ? hist[tid] : 0);
         if (tid < 256 && lane == 63) red[w] = x;
         __syncthreads();
         if (tid < 256) {
