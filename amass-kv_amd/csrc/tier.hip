@@ -132,7 +132,9 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
             atomicMin(&fp[*miss_at(r, f)], f);
         }
     }
-    __threadfence();
+    // the atomics act at L2 and the agent-scope loads below read L2; the barrier's release
+    // waits for this workgroup's atomics, so no device-scope fence is needed (one cost
+    // ~4 us here: it writes back and invalidates the XCD's L2)
     __syncthreads();
 
     // 3. rank the distinct new misses in flat order
