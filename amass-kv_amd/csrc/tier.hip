@@ -250,17 +250,28 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
             }
             int tsel;
             int cp = blk_excl_scan<TP_THREADS>(nsel, red, tsel);   // tsel == Mnew
+            if (B == 0) {
+                // every candidate lies in the oldest bin: their order is the slot order,
+                // which is the order of the scan (the usual case once the buffer has aged
+                // in whole steps: the oldest clock holds many slots)
 #pragma unroll
-            for (int i = 0; i < SPT; ++i)
-                if (take[i]) cand[cp++] = ((uint32_t)(cl[i] - cmin) << 13) | (uint32_t)(s0 + i);
-            __syncthreads();
-            if (tid < Mnew) {
-                const uint32_t key = cand[tid];
-                int rank = 0;
-                for (int j = 0; j < Mnew; ++j) rank += cand[j] < key ? 1 : 0;
-                sb[0][rank] = (uint16_t)(key & 0x1FFFu);
+                for (int i = 0; i < SPT; ++i)
+                    if (take[i]) sb[0][cp++] = (uint16_t)(s0 + i);
+                __syncthreads();
+            } else {
+#pragma unroll
+                for (int i = 0; i < SPT; ++i)
+                    if (take[i])
+                        cand[cp++] = ((uint32_t)(cl[i] - cmin) << 13) | (uint32_t)(s0 + i);
+                __syncthreads();
+                if (tid < Mnew) {
+                    const uint32_t key = cand[tid];
+                    int rank = 0;
+                    for (int j = 0; j < Mnew; ++j) rank += cand[j] < key ? 1 : 0;
+                    sb[0][rank] = (uint16_t)(key & 0x1FFFu);
+                }
+                __syncthreads();
             }
-            __syncthreads();
         }
     }
     if (!fast) {
