@@ -565,7 +565,8 @@ def run_summary_build(args):
                 tail_us_1layer=round(us_tail, 2), tail_us_32layers=round(us_tail32, 2))
 
 
-def run_config4(args, boost="sigma", steps=64):
+def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
+                fetches=("kernel", "dma")):
     """mem-v at config 4: V in the pinned, device-mapped host pool, a 10 % hot buffer, 64
     decode steps over a fixed boosted page set, each from a cold hot buffer.  Two query
     streams: "fresh" (config 4's literal N(0, 1) each step) and "correlated" (the case's
@@ -688,9 +689,9 @@ def run_config4(args, boost="sigma", steps=64):
                         f"hot buffer {slots} slots per kv head (10 %), {steps} steps from a "
                         f"cold buffer, boost {boost}; streams: fresh N(0,1) queries "
                         f"(literal) and correlated (case q + 0.3 N(0,1))")
-    for stream in ("fresh", "correlated"):
+    for stream in streams:
         qs = queries(stream)
-        res[stream] = {f: run(qs, f) for f in ("kernel", "dma")}
+        res[stream] = {f: run(qs, f) for f in fetches}
         # the same steps with V resident in HBM
         a, b = ev(), ev()
         a.record()
@@ -701,11 +702,14 @@ def run_config4(args, boost="sigma", steps=64):
         b.record()
         torch.cuda.synchronize()
         res[stream]["resident_us_per_step"] = round(a.elapsed_time(b) / steps * 1e3, 1)
-        k = res[stream]["kernel"]
-        log(f"config 4 ({boost}, {stream}): hit {k['hit_rate']}, kernel fetch "
-            f"{k['us_per_step']} us/step (select {k['select']}, plan {k['plan']}, fetch "
-            f"{k['fetch']}, decode {k['decode']}), dma {res[stream]['dma']['us_per_step']}, "
-            f"resident {res[stream]['resident_us_per_step']}")
+        k = res[stream].get("kernel")
+        dma = res[stream].get("dma")
+        if k is not None:
+            log(f"config 4 ({boost}, {stream}): hit {k['hit_rate']}, kernel fetch "
+                f"{k['us_per_step']} us/step (select {k['select']}, plan {k['plan']}, fetch "
+                f"{k['fetch']}, decode {k['decode']}), dma "
+                f"{dma['us_per_step'] if dma else '-'}, "
+                f"resident {res[stream]['resident_us_per_step']}")
         del qs
     res["write_path"] = write_path_times(tier, case, args)
     return res
@@ -769,6 +773,9 @@ SECONDARY = {
 }
 ONLY = {"1": run_headline_only, "clse": lambda a: run_clse(a),
         "clsek": lambda a: run_clse(a, "keynorm"),
+        # the mem-v tier kernels at config 4 (key-norm, correlated stream, fetch kernel)
+        "4k": lambda a: run_config4(a, "keynorm", streams=("correlated",),
+                                    fetches=("kernel",)),
         **{k: v[1] for k, v in SECONDARY.items()}}
 
 
