@@ -82,7 +82,7 @@ __device__ __forceinline__ int load_agent(const int32_t* p) {
 __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_plan_args a) {
     __shared__ int off[TP_MAXREQ + 1];
     __shared__ uint16_t sb[2][TP_MAXS];
-    __shared__ int red[TP_WAVES];
+    __shared__ int red[TP_WAVES], red2[TP_WAVES];
     __shared__ int smax_s[TP_WAVES], smin_s[TP_WAVES];
     __shared__ int hist[256], cum[256];
     __shared__ uint32_t cand[TP_THREADS];
@@ -96,6 +96,19 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     int32_t* p2s = a.page2slot + (int64_t)kv * a.nb;
     int32_t* s2p = a.slot2page + (int64_t)kv * S;
     int32_t* lru = a.lru_clock + (int64_t)kv * S;
+
+    // the slots' clocks are loaded first (nothing in this launch writes them before the
+    // apply), so their latency hides under the miss bookkeeping; INT_MAX marks a lane
+    // position past the buffer (never below the step's clock: not a candidate)
+    constexpr int SPT = TP_MAXS / TP_THREADS;          // slots per thread (S <= TP_MAXS)
+    const int CS = (S + TP_THREADS - 1) / TP_THREADS;
+    const int s0 = min(tid * CS, S), s1 = min(s0 + CS, S);
+    int cl[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        const int sidx = s0 + i;
+        cl[i] = (i < CS && sidx < s1) ? lru[sidx] : 0x7FFFFFFF;
+    }
 
     // 1. flat offsets of every request's miss list
     int mc = tid < a.n_req ? a.miss_cnt[(int64_t)tid * a.n_kv + kv] : 0;
@@ -146,8 +159,6 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
             nfirst += (load_agent(&fp[*miss_at(r, f)]) == f);
         }
     }
-    int Mnew;
-    const int rank0 = blk_excl_scan<TP_THREADS>(nfirst, red, Mnew);
 
     // 4. the order of the untouched slots by (clock, slot).  Only the first Mnew are
     // used: when they all lie within 255 clock values of the oldest untouched clock and
@@ -157,34 +168,45 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     // smaller keys.  Otherwise (wide clock ranges, more new misses than threads, or fewer
     // untouched slots than new misses) all untouched slots are sorted: a stable 1-bit LSD
     // radix sort by clock over the bits the clocks use.
-    constexpr int SPT = TP_MAXS / TP_THREADS;          // slots per thread (S <= TP_MAXS)
-    const int CS = (S + TP_THREADS - 1) / TP_THREADS;
-    const int s0 = min(tid * CS, S), s1 = min(s0 + CS, S);
-    int cl[SPT];
     int nun = 0, kmax = 0, kmin = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < SPT; ++i) {
-        const int sidx = s0 + i;
-        cl[i] = (i < CS && sidx < s1) ? lru[sidx] : clk;    // clk: not a candidate
         if (cl[i] < clk) {
             ++nun;
             kmax = max(kmax, cl[i]);
             kmin = min(kmin, cl[i]);
         }
     }
-    int U;
-    int upos = blk_excl_scan<TP_THREADS>(nun, red, U);
+    // one exchange for both block scans (distinct new misses, untouched slots) and the
+    // clock range (clocks are >= 0: their unsigned order is their order); every thread
+    // read the last scan's totals before the barriers since, so `red` is free
+    int Mnew, U, rank0, upos;
     {
-        // clocks are >= 0: their unsigned order is their order
+        const int lane = tid & 63, w = tid >> 6;
+        const int xf = wave_incl_scan(nfirst), xu = wave_incl_scan(nun);
         const int km = (int)wave_maxu_uniform((uint32_t)kmax);
         const int kn = (int)wave_minu_uniform((uint32_t)kmin);
-        if ((tid & 63) == 0) {
-            smax_s[tid >> 6] = km;
-            smin_s[tid >> 6] = kn;
+        if (lane == 63) {
+            red[w] = xf;
+            red2[w] = xu;
+            smax_s[w] = km;
+            smin_s[w] = kn;
         }
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        int bf = 0, bu = 0, tf = 0, tu = 0;
+#pragma unroll
+        for (int i = 0; i < TP_WAVES; ++i) {
+            const int f = red[i], u = red2[i];
+            if (i < w) { bf += f; bu += u; }
+            tf += f;
+            tu += u;
+        }
+        Mnew = tf;
+        U = tu;
+        rank0 = bf + xf - nfirst;
+        upos = bu + xu - nun;
     }
-    if (tid < 256) hist[tid] = 0;
-    __syncthreads();
     int kall = 0, cmin = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < TP_WAVES; ++i) {
