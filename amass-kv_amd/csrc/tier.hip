@@ -84,7 +84,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     __shared__ uint16_t sb[2][TP_MAXS];
     __shared__ int red[TP_WAVES], red2[TP_WAVES];
     __shared__ int smax_s[TP_WAVES], smin_s[TP_WAVES];
-    __shared__ int hist[256], cum[256];
+    __shared__ __align__(16) int hist[256];
     __shared__ uint32_t cand[TP_THREADS];
     __shared__ int sel_bin, sel_quota;
     const int kv = blockIdx.x, tid = threadIdx.x;
@@ -229,37 +229,46 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
             }
         }
         __syncthreads();
-        // inclusive scan of the 256 bins (first four waves), then B = the first bin whose
-        // running count reaches Mnew and the quota taken from it
-        const int lane = tid & 63, w = tid >> 6;
-        const int x = wave_incl_scan(tid < 256 ? hist[tid] : 0);
-        if (tid < 256 && lane == 63) red[w] = x;
-        __syncthreads();
-        if (tid < 256) {
-            int base = 0;
-            for (int i = 0; i < w; ++i) base += red[i];
-            cum[tid] = base + x;
-        }
-        __syncthreads();
-        if (tid < 256) {
-            const int incl = cum[tid], excl = tid ? cum[tid - 1] : 0;
-            if (excl < Mnew && incl >= Mnew) {
-                sel_bin = tid;
-                sel_quota = Mnew - excl;
+        // B = the first bin whose running count reaches Mnew (>= 1: M > 0 has a first
+        // occurrence) and the quota taken from it: wave 0 alone, lane l summing bins
+        // 4l .. 4l + 3 (every untouched slot has a bin, so the total U >= Mnew is reached)
+        if (tid < WAVE) {
+            const int4 h = reinterpret_cast<const int4*>(hist)[tid];
+            const int sum = (h.x + h.y) + (h.z + h.w);
+            const int incl = wave_incl_scan(sum);
+            const unsigned long long hit = __ballot(incl >= Mnew);
+            if (tid == __ffsll((long long)hit) - 1) {
+                int c = incl - sum, b = 4 * tid;
+                if (c + h.x < Mnew) {
+                    c += h.x; ++b;
+                    if (c + h.y < Mnew) {
+                        c += h.y; ++b;
+                        if (c + h.z < Mnew) { c += h.z; ++b; }
+                    }
+                }
+                sel_bin = b;
+                sel_quota = Mnew - c;
             }
         }
         __syncthreads();
         const int B = sel_bin, quota = sel_quota;
         fast = B < 255;                               // uniform
         if (fast) {
-            // ranks in slot order of this thread's bin-B slots
-            int nb = 0;
+            // one scan of packed (bin-B slots << 16 | slots below bin B) counts: a thread's
+            // first taken slot goes to (below-B slots before it) + min(bin-B slots before
+            // it, quota), its bin-B slots taken in slot order while their rank < quota
+            int nl = 0, nb = 0;
 #pragma unroll
-            for (int i = 0; i < SPT; ++i) nb += (cl[i] < clk && cl[i] - cmin == B) ? 1 : 0;
-            int tb;
-            const int rb0 = blk_excl_scan<TP_THREADS>(nb, red, tb);
+            for (int i = 0; i < SPT; ++i)
+                if (cl[i] < clk) {
+                    nl += cl[i] - cmin < B ? 1 : 0;
+                    nb += cl[i] - cmin == B ? 1 : 0;
+                }
+            int tpk;
+            const int pk = blk_excl_scan<TP_THREADS>(nl | (nb << 16), red, tpk);
+            int rb = pk >> 16;
+            int cp = (pk & 0xFFFF) + min(rb, quota);
             bool take[SPT];
-            int nsel = 0, rb = rb0;
 #pragma unroll
             for (int i = 0; i < SPT; ++i) {
                 const int rel = cl[i] - cmin;
@@ -268,10 +277,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
                     if (rel < B) take[i] = true;
                     else if (rel == B) take[i] = rb++ < quota;
                 }
-                nsel += take[i] ? 1 : 0;
             }
-            int tsel;
-            int cp = blk_excl_scan<TP_THREADS>(nsel, red, tsel);   // tsel == Mnew
             if (B == 0) {
                 // every candidate lies in the oldest bin: their order is the slot order,
                 // which is the order of the scan (the usual case once the buffer has aged
