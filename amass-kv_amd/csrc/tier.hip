@@ -86,7 +86,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     __shared__ int smax_s[TP_WAVES], smin_s[TP_WAVES];
     __shared__ __align__(16) int hist[256];
     __shared__ uint32_t cand[TP_THREADS];
-    __shared__ int sel_bin, sel_quota;
+    __shared__ int sel_bin, sel_quota, fbase;
     const int kv = blockIdx.x, tid = threadIdx.x;
     const int clk = a.clock[0] + 1;                    // this step's clock
     if (a.n_req == 0 && kv == 0 && tid == 0) a.fetch_cnt[0] = 0;   // (else: miss_diff's)
@@ -207,6 +207,9 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         rank0 = bf + xf - nfirst;
         upos = bu + xu - nun;
     }
+    // one fetch-list reservation per kv head for its min(Mnew, U) fetches (the k-th new
+    // miss takes entry fbase + k), issued by wave 1 while wave 0 searches the histogram
+    if (tid == WAVE) fbase = atomicAdd(a.fetch_cnt, min(Mnew, U));
     int kall = 0, cmin = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < TP_WAVES; ++i) {
@@ -353,7 +356,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
             s2p[s] = blk;
             lru[s] = clk;
             *vict = s;
-            const int fi = atomicAdd(a.fetch_cnt, 1);
+            const int fi = fbase + k;
             if (fi < a.fcap) {
                 a.fetch_list[3 * (int64_t)fi + 0] = kv;
                 a.fetch_list[3 * (int64_t)fi + 1] = blk;
