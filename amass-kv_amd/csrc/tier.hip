@@ -47,11 +47,14 @@ __device__ __forceinline__ int blk_excl_scan(int v, int* red, int& total) {
 __global__ __launch_bounds__(MD_THREADS) void miss_diff_kernel(const amass_tier_plan_args a) {
     __shared__ int red[MD_THREADS / WAVE];
     const int kv = blockIdx.x, r = blockIdx.y;
+    const int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kv * a.pt_sh;
+    // the first page ids are loaded with the count (rows are max_pages wide), so the
+    // block lookups wait for one round trip less
+    const int pt0 = (int)threadIdx.x < a.max_pages ? tab[threadIdx.x] : 0;
     const int n = a.page_cnt[(int64_t)r * a.pc_sr + kv];
     const int sl = a.seq_lens[r];
     const int clk = a.clock[0] + 1;                    // this step's clock
     if (kv == 0 && r == 0 && threadIdx.x == 0) a.fetch_cnt[0] = 0;
-    const int32_t* tab = a.page_table + (int64_t)r * a.pt_sr + (int64_t)kv * a.pt_sh;
     const int32_t* bt = a.block_table + (int64_t)r * a.bt_st;
     int32_t* mp = a.miss_pages + ((int64_t)r * a.n_kv + kv) * a.max_pages;
     int nmiss = 0;
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(MD_THREADS) void miss_diff_kernel(const amass_tier_
         const int idx = off + threadIdx.x;
         int is_miss = 0, blk = 0;
         if (idx < n) {
-            const int pt = tab[idx];
+            const int pt = off == 0 ? pt0 : tab[idx];
             blk = bt[pt];
             const bool complete = (int64_t)(pt + 1) * a.page <= (int64_t)sl;
             const int slot = a.page2slot[(int64_t)kv * a.nb + blk];
