@@ -140,14 +140,20 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         r0 = lo;
     }
 
-    // 2. first occurrence of each physical block among this step's misses
+    // 2. first occurrence of each physical block among this step's misses (the block of
+    // the thread's first position stays in a register for the passes below: with at most
+    // TP_THREADS misses per kv head it is the thread's only one)
+    int mb0 = 0;
     {
         int r = r0;
         for (int f = f0; f < f1; ++f) {
             locate(f, r);
-            atomicMin(&fp[*miss_at(r, f)], f);
+            const int b = *miss_at(r, f);
+            if (f == f0) mb0 = b;
+            atomicMin(&fp[b], f);
         }
     }
+    auto block_at = [&](int r, int f) -> int { return f == f0 ? mb0 : *miss_at(r, f); };
     // the atomics act at L2 and the agent-scope loads below read L2; the barrier's release
     // waits for this workgroup's atomics, so no device-scope fence is needed (one cost
     // ~4 us here: it writes back and invalidates the XCD's L2)
@@ -159,7 +165,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         int r = r0;
         for (int f = f0; f < f1; ++f) {
             locate(f, r);
-            nfirst += (load_agent(&fp[*miss_at(r, f)]) == f);
+            nfirst += (load_agent(&fp[block_at(r, f)]) == f);
         }
     }
 
@@ -339,7 +345,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         int r = r0, rank = rank0;
         for (int f = f0; f < f1; ++f) {
             locate(f, r);
-            const int32_t blk = *miss_at(r, f);
+            const int32_t blk = block_at(r, f);
             int32_t* vict = a.victim_slots + (int64_t)r * a.n_kv * a.max_pages + mbase_kv +
                             (f - off[r]);
             if (load_agent(&fp[blk]) != f) {
@@ -373,15 +379,18 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
         int r = r0;
         for (int f = f0; f < f1; ++f) {
             locate(f, r);
-            fp[*miss_at(r, f)] = 0x7FFFFFFF;
+            fp[block_at(r, f)] = 0x7FFFFFFF;
         }
     }
     }
-    // the last workgroup to finish advances the clock (every workgroup has read it) and
-    // clears the arrival count for the next call
+    // the last workgroup to finish advances the clock and clears the arrival count for the
+    // next call.  Relaxed: a workgroup that uses the clock has consumed its load (the slot
+    // comparisons) before it arrives, so no later store can be the value it read; the
+    // tables this launch wrote reach the next launches at the kernel boundary (an acq_rel
+    // RMW would write back and invalidate the XCD's L2 on every workgroup)
     __syncthreads();
     if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(&a.clock[1], 1, __ATOMIC_ACQ_REL,
+        const int old = __hip_atomic_fetch_add(&a.clock[1], 1, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
         if (old == (int)gridDim.x - 1) {
             __hip_atomic_store(&a.clock[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
