@@ -21,7 +21,7 @@ constexpr int TP_THREADS = 1024;
 constexpr int TP_WAVES = TP_THREADS / WAVE;
 constexpr int TP_MAXS = 8192;
 constexpr int TP_MAXREQ = 1024;
-constexpr int MD_THREADS = 256;
+constexpr int MD_THREADS = 1024;              // miss diff: a unit's pages in one pass (<= 1024)
 
 
 template <int NT>
