@@ -90,6 +90,7 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     __shared__ __align__(16) int hist[256];
     __shared__ uint32_t cand[TP_THREADS];
     __shared__ int sel_bin, sel_quota, fbase;
+    __shared__ int sclk[TP_MAXS];                      // the slots' clocks (load transpose)
     const int kv = blockIdx.x, tid = threadIdx.x;
     const int clk = a.clock[0] + 1;                    // this step's clock
     if (a.n_req == 0 && kv == 0 && tid == 0) a.fetch_cnt[0] = 0;   // (else: miss_diff's)
@@ -100,26 +101,31 @@ __global__ __launch_bounds__(TP_THREADS) void victims_kernel(const amass_tier_pl
     int32_t* s2p = a.slot2page + (int64_t)kv * S;
     int32_t* lru = a.lru_clock + (int64_t)kv * S;
 
-    // the slots' clocks are loaded first (nothing in this launch writes them before the
-    // apply), so their latency hides under the miss bookkeeping; INT_MAX marks a lane
-    // position past the buffer (never below the step's clock: not a candidate)
+    // 1. flat offsets of every request's miss list.  The slots' clocks are loaded right
+    // after the counts (nothing in this launch writes them before the apply), coalesced
+    // (slot tid + TP_THREADS i), and pass through LDS to each thread's run of CS
+    // consecutive slots, so their latency hides under the miss bookkeeping; INT_MAX marks
+    // a position past the buffer (never below the step's clock: not a candidate).
     constexpr int SPT = TP_MAXS / TP_THREADS;          // slots per thread (S <= TP_MAXS)
-    const int CS = (S + TP_THREADS - 1) / TP_THREADS;
-    const int s0 = min(tid * CS, S), s1 = min(s0 + CS, S);
-    int cl[SPT];
+    int mc = tid < a.n_req ? a.miss_cnt[(int64_t)tid * a.n_kv + kv] : 0;
+    int lv[SPT];
 #pragma unroll
     for (int i = 0; i < SPT; ++i) {
-        const int sidx = s0 + i;
-        cl[i] = (i < CS && sidx < s1) ? lru[sidx] : 0x7FFFFFFF;
+        const int sidx = tid + TP_THREADS * i;
+        lv[i] = sidx < S ? lru[sidx] : 0x7FFFFFFF;
     }
-
-    // 1. flat offsets of every request's miss list
-    int mc = tid < a.n_req ? a.miss_cnt[(int64_t)tid * a.n_kv + kv] : 0;
     int M;
     const int o = blk_excl_scan<TP_THREADS>(mc, red, M);
     if (tid < a.n_req) off[tid] = o;
     if (tid == 0) off[a.n_req] = M;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) sclk[tid + TP_THREADS * i] = lv[i];
     __syncthreads();
+    const int CS = (S + TP_THREADS - 1) / TP_THREADS;
+    const int s0 = min(tid * CS, S), s1 = min(s0 + CS, S);
+    int cl[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) cl[i] = (i < CS && s0 + i < s1) ? sclk[s0 + i] : 0x7FFFFFFF;
     if (M > 0) {                                       // uniform
 
     const int C = (M + TP_THREADS - 1) / TP_THREADS;
