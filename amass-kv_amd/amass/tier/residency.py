@@ -60,6 +60,7 @@ class Residency:
         self.fetch_cnt = torch.zeros((1,), dtype=i32, device=dev)
         self.first_pos = torch.full((n_kv, num_blocks), I32_MAX, dtype=i32, device=dev)
         self.fetch_grid = 1024
+        self.plan_width = max_pages
         elem = torch.empty(0, dtype=dtype).element_size()
         self.hot_gib = self.hot.numel() * elem / 2**30
 
@@ -96,6 +97,8 @@ class Residency:
         if page_table.shape[2] > self.MP or n_req > self.R:
             raise ValueError("selection wider than the residency scratch")
         call("amass_tier_gather_plan", a, current_stream(self.device))
+        # the kernel writes miss_pages / victim_slots rows at this stride
+        self.plan_width = page_table.shape[2]
 
     def gather_fetch(self, layer, staging, pool, n_req=None, stream=None) -> None:
         """Copy every planned miss page into its hot slot (pinned pool, or the staged
@@ -139,8 +142,9 @@ class Residency:
         if n_req <= 0:
             return np.zeros((0, 6), np.int64), False
         dev = self.miss_pages.device
-        blk = self.miss_pages[:n_req].long()
-        slot = self.victim_slots[:n_req].long()
+        rows = n_req * n_kv * self.plan_width   # the last plan's rows, at its row stride
+        blk = self.miss_pages.view(-1)[:rows].view(n_req, n_kv, self.plan_width).long()
+        slot = self.victim_slots.view(-1)[:rows].view(n_req, n_kv, self.plan_width).long()
         live = (torch.arange(blk.shape[-1], device=dev) < self.miss_cnt[:n_req, :, None]) \
             & (slot >= 0)
         kvi = torch.arange(n_kv, device=dev).view(1, n_kv, 1).expand_as(blk)

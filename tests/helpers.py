@@ -28,9 +28,9 @@ def npi(t):
     return t.detach().cpu().numpy()
 
 
-def rel_close(got, ref, tol):
-    """|got - ref| <= tol * max(|ref|, 1) (the quad-score rule: relative error is
-    ill-conditioned near 0)."""
+def rel_err(got, ref):
+    """max |got - ref| / max(|ref|, 1) (the quad-score rule: relative error is
+    ill-conditioned near 0); callers compare it with their tolerance."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     err = np.abs(got - ref) / np.maximum(np.abs(ref), 1.0)

@@ -21,7 +21,7 @@ from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
 from amass.bench.synth import build_quad_state, make_case
 from amass.selection import derive_page_params, select_pages_clse
 from amass.selection.quad_score import clse_score
-from helpers import announce, case_to, npf, npi, rel_close, to_device
+from helpers import announce, case_to, npf, npi, rel_err, to_device
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -71,9 +71,9 @@ def test_clse_score_vs_oracle(rank, v_bits, c_bits, c_grain, G, combine):
         n = int(nsh[r])
         assert np.array_equal(got_comb[r, :, :n], ref_comb[r, :, :n])
         if combine == "nrm":
-            assert rel_close(got[r, :, :, :n], ref[r, :, :, :n], 1) <= 1e-3
+            assert rel_err(got[r, :, :, :n], ref[r, :, :, :n]) <= 1e-3
         else:
-            assert rel_close(got[r, :, :n], ref[r, :, :n], 1) <= 1e-3
+            assert rel_err(got[r, :, :n], ref[r, :, :n]) <= 1e-3
 
 
 @pytest.mark.parametrize("rank,c_bits,c_grain", [(2, 4, "token"), (8, 8, "page")])
@@ -140,7 +140,7 @@ def test_select_pages_clse_end_to_end():
                            c_bits=4, max_pages=st.max_pages, combine="nrm")
     for r in range(B):
         n = int(nsh[r])
-        assert rel_close(npf(st.score_h[r, :, :, :n]), ref_h[r, :, :, :n], 1) <= 1e-3
+        assert rel_err(npf(st.score_h[r, :, :, :n]), ref_h[r, :, :, :n]) <= 1e-3
     tab, cnt, _ = osel.select(npf(st.score), npi(st.n_pages), nsh, npi(st.b_fix), sink=1,
                               max_pages=st.max_pages, mode=1, coverage=0.95, score_kind=1)
     assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)
@@ -181,4 +181,4 @@ def test_clse_head_layouts(n_kv, G, rank, v_bits, c_bits, c_grain):
     for r in range(B):
         n = int(nsh[r])
         assert np.array_equal(got_comb[r, :, :n], ref_comb[r, :, :n])
-        assert rel_close(got[r, :, :, :n], ref[r, :, :, :n], 1) <= 1e-3
+        assert rel_err(got[r, :, :, :n], ref[r, :, :, :n]) <= 1e-3

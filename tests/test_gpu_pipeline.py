@@ -16,7 +16,7 @@ import oracle.select as osel
 from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
 from amass.bench.synth import build_quad_state, config_case, make_case
 from amass.selection import derive_page_params, select_pages_quad
-from helpers import announce, case_to, npf, npi, rel_close, to_device
+from helpers import announce, case_to, npf, npi, rel_err, to_device
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -42,7 +42,7 @@ def _check(case, st, out, *, mode, cov, kind):
     ref_s = osc.nrm_combine(ref_h, nsh)
     sc = npf(st.score)
     for r in range(B):
-        assert rel_close(sc[r, :, :nsh[r]], ref_s[r, :, :nsh[r]], 1) <= 1e-3
+        assert rel_err(sc[r, :, :nsh[r]], ref_s[r, :, :nsh[r]]) <= 1e-3
     tab, cnt, _ = osel.select(sc, npi(st.n_pages), nsh, npi(st.b_fix), sink=1, max_pages=MP,
                               mode=mode, coverage=cov, tie_mode=0, score_kind=kind)
     assert np.array_equal(npi(st.page_table), tab) and np.array_equal(npi(st.page_cnt), cnt)

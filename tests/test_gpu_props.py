@@ -41,7 +41,7 @@ from amass.selection import (QuadState, coverage_select, derive_page_params, r8_
                              topb_select)
 from amass.selection.quad_score import clse_score, quad_score_launch
 from amass.tier import Tier
-from helpers import announce, case_to, npf, npi, rel_close, to_device
+from helpers import announce, case_to, npf, npi, rel_err, to_device
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -352,7 +352,7 @@ def _score_example(c):
         n = int(nsh[r])
         assert np.array_equal(gc[r, :, :n], ref_comb[r, :, :n]), f"contractions, request {r}"
         for ref, tol in refs:
-            assert rel_close(got[r, ..., :n], ref[r, ..., :n], 1) <= tol, f"scores, request {r}"
+            assert rel_err(got[r, ..., :n], ref[r, ..., :n]) <= tol, f"scores, request {r}"
 
 
 @pytest.mark.parametrize("kind", ["quad", "r8", "clse"])

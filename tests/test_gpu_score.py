@@ -15,7 +15,7 @@ import oracle.select as osel
 from amass.bench.synth import build_quad_state, build_r8_state, make_case
 from amass.selection import derive_page_params, nrm_combine, r8_score
 from amass.selection.quad_score import quad_score_launch
-from helpers import announce, npf, npi, rel_close, to_device, case_to
+from helpers import announce, npf, npi, rel_err, to_device, case_to
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -63,8 +63,8 @@ def test_quad_comb_exact_and_scores(rank, v_bits, G):
     sc = npf(st.score)
     for r in range(B):
         n = int(nsh[r])
-        assert rel_close(sc[r, :, :n], ref_f[r, :, :n], 1) <= 1e-3
-        assert rel_close(sc[r, :, :n], ref_l[r, :, :n], 1) <= 2e-5
+        assert rel_err(sc[r, :, :n], ref_f[r, :, :n]) <= 1e-3
+        assert rel_err(sc[r, :, :n], ref_l[r, :, :n]) <= 2e-5
 
 
 @pytest.mark.parametrize("rank,v_bits", [(8, 8), (2, 4)])
@@ -82,14 +82,14 @@ def test_quad_nrm(rank, v_bits):
     nsh = npi(st.n_sel_hi)
     for r in range(B):
         n = int(nsh[r])
-        assert rel_close(sh[r, :, :, :n], ref_h[r, :, :, :n], 1) <= 1e-3
+        assert rel_err(sh[r, :, :, :n], ref_h[r, :, :, :n]) <= 1e-3
     # nrm of the GPU's own per-head scores: fp64 oracle vs the fp32 kernel
     with np.errstate(invalid="ignore"):   # pages past n_sel_hi hold unwritten bits
         ref_n = osc.nrm_combine(sh.astype(np.float64), nsh)
     sc = npf(st.score)
     for r in range(B):
         n = int(nsh[r])
-        assert rel_close(sc[r, :, :n], ref_n[r, :, :n], 1) <= 1e-5
+        assert rel_err(sc[r, :, :n], ref_n[r, :, :n]) <= 1e-5
 
 
 def test_quad_padded_rows_untouched():
@@ -146,10 +146,10 @@ def test_r8_comb_exact_and_scores(rank, vk_bits, c_bits, G):
     sc = npf(st.score)
     for r in range(B):
         n = int(nsh[r])
-        assert rel_close(sc[r, :, :n], sc_comb[r, :, :n], 1) <= 1e-6
+        assert rel_err(sc[r, :, :n], sc_comb[r, :, :n]) <= 1e-6
     for r in range(B):
         n = int(nsh[r])
-        assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3
+        assert rel_err(sc[r, :, :n], ref[r, :, :n]) <= 1e-3
 
 
 HEAD_CASES = [(1, 8), (2, 2), (4, 1), (16, 4)]
@@ -183,7 +183,7 @@ def test_quad_head_layouts(n_kv, G, rank, v_bits):
     for r in range(B):
         n = int(nsh[r])
         assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n]), f"comb mismatch req {r}"
-        assert rel_close(sc[r, :, :n], ref_l[r, :, :n], 1) <= 2e-5
+        assert rel_err(sc[r, :, :n], ref_l[r, :, :n]) <= 2e-5
 
 
 @pytest.mark.parametrize("n_kv,G", HEAD_CASES)
@@ -213,7 +213,7 @@ def test_r8_head_layouts(n_kv, G):
     for r in range(B):
         n = int(nsh[r])
         assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
-        assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3
+        assert rel_err(sc[r, :, :n], ref[r, :, :n]) <= 1e-3
 
 
 @pytest.mark.parametrize("vk_bits,c_bits,G", [(8, 8, 4), (8, 4, 8), (4, 8, 2)])
@@ -248,5 +248,5 @@ def test_r8_page_f32_scale(vk_bits, c_bits, G):
     for r in range(B):
         n = int(nsh[r])
         assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
-        assert rel_close(sc[r, :, :n], sc_comb[r, :, :n], 1) <= 1e-6
-        assert rel_close(sc[r, :, :n], ref[r, :, :n], 1) <= 1e-3
+        assert rel_err(sc[r, :, :n], sc_comb[r, :, :n]) <= 1e-6
+        assert rel_err(sc[r, :, :n], ref[r, :, :n]) <= 1e-3

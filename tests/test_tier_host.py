@@ -138,3 +138,28 @@ def test_dma_runs_match_a_sequential_walk(data):
                      n_kv * PB, PB, h] for kv, s, b, h in want], np.int64).reshape(-1, 6)
     assert staged == want_staged
     assert np.array_equal(runs, exp)
+
+
+def test_dma_runs_at_a_narrower_plan_width():
+    """A selection narrower than the residency's max_pages: the plan kernel writes the
+    miss rows at the page table's width, and the planner reads them at that stride."""
+    W = 5
+    wide, narrow = _res(), Residency(num_layers=2, num_blocks=40, n_kv=2, hot_slots=12,
+                                     page=16, d=128, max_reqs=2, max_pages=W,
+                                     dtype=torch.bfloat16, device="cpu")
+    narrow.pool_valid.fill_(1)
+    pool = types.SimpleNamespace(_host_ptr=1 << 40)
+    lists = {(0, 0): ([5, 6, 7, 9, 10], [2, 3, 4, 5, 6]), (0, 1): ([3, 4], [0, 1]),
+             (1, 0): ([11, 12, 13], [7, 8, 9]), (1, 1): ([20], [11])}
+    for (req, kv), (b, s) in lists.items():
+        _miss(narrow, req, kv, b, s)
+    # the wide residency's buffers hold the same rows at stride W, as the kernel writes them
+    wide.miss_pages.view(-1)[:2 * 2 * W] = narrow.miss_pages.view(-1)
+    wide.victim_slots.view(-1)[:2 * 2 * W] = narrow.victim_slots.view(-1)
+    wide.miss_cnt.copy_(narrow.miss_cnt)
+    wide.plan_width = W
+    runs, staged = wide.build_dma_plan(0, pool, 2)
+    want, _ = narrow.build_dma_plan(0, pool, 2)
+    want[:, 0] += wide.hot[0].data_ptr() - narrow.hot[0].data_ptr()
+    assert not staged and np.array_equal(runs, want)
+    assert list(runs[:, 5]) == [3, 2, 2, 3, 1]

@@ -11,7 +11,7 @@ import oracle.score as osc
 import oracle.select as osel
 import oracle.torch_path as tp
 from amass.bench.synth import build_quad_state, make_case
-from helpers import npf, npi, rel_close
+from helpers import npf, npi, rel_err
 
 
 @pytest.mark.parametrize("v_bits,boost", [(8, "sigma"), (4, "keynorm")])
@@ -34,12 +34,12 @@ def test_torch_path_matches_numpy_oracle(v_bits, boost):
                            v_bits=v_bits, max_pages=MP, combine="nrm")
     for r in range(B):
         n = int(onsh[r])
-        assert rel_close(sh[r, :, :, :n].numpy(), ref_h[r, :, :, :n], 1) <= 1e-4
+        assert rel_err(sh[r, :, :, :n].numpy(), ref_h[r, :, :, :n]) <= 1e-4
     sc = tp.nrm_combine(sh, nsh)
     ref_s = osc.nrm_combine(sh.double().numpy(), onsh)
     for r in range(B):
         n = int(onsh[r])
-        assert rel_close(sc[r, :, :n].numpy(), ref_s[r, :, :n], 1) <= 1e-5
+        assert rel_err(sc[r, :, :n].numpy(), ref_s[r, :, :n]) <= 1e-5
     for mode in (0, 1):
         tab, cnt = tp.select(sc, npg, nsh, bfix, sink=1, max_pages=MP, mode=mode,
                              coverage=0.95, score_kind=1)
