@@ -682,6 +682,14 @@ static int decode_noalloc(const amass_decode_args* ain, hipStream_t s) {
     amass_decode_args a = *ain;
     if (a.n_req < 0 || a.n_kv < 1 || a.G < 1 || a.G > 8 || a.d != DEC_D) return AMASS_ERR_GEOMETRY;
     if (a.path != 2 && a.split < 1) return AMASS_ERR_GEOMETRY;
+    if (a.path != 2 && a.split >= 3 && a.n_req > 0) {
+        // partial slots per unit: at most what the array holds (alignment pad < 256 B);
+        // the device plan never splits a unit into more than split - 1 parts
+        const int64_t per_slot = (int64_t)a.n_req * a.n_kv * a.G * (2 + DEC_D) * (int64_t)sizeof(float);
+        const int64_t fit = (DEC_SCRATCH_BYTES - 256) / per_slot;
+        if (fit < 3) return AMASS_ERR_CAPACITY;
+        if (fit < a.split) a.split = (int)fit;
+    }
     int64_t acc_off = 0;
     const int64_t need = decode_partial_bytes(a, acc_off);
     if (need > DEC_SCRATCH_BYTES) return AMASS_ERR_CAPACITY;

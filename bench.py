@@ -618,8 +618,35 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
                       .to(torch.bfloat16))
         return qs
 
-    def run(qs, fetch, max_runs=20000):
-        """Per-phase us (mean over the steps run) + hit statistics, from cold."""
+    def dma_step(qt):
+        r5.gather_plan(0, st.page_table, st.page_cnt, bt, sl, B)
+        plan, staged = r5.build_dma_plan(0, tier.pool, B)     # synchronises
+        side = tier.copy_engine.next_stream()
+        side.wait_stream(torch.cuda.current_stream())
+        done = tier.copy_engine.issue(plan, side, timing=True)
+        if staged:
+            r5.gather_fetch(0, tier.staging, tier.pool, B)
+        torch.cuda.current_stream().wait_event(done)
+        mem_decode(qt, case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale)
+
+    def check_last(qt):
+        """What was timed is checked: the last step's tiered output equals the resident
+        decode of the same selection bit for bit, and the maps are mutual inverses."""
+        ref = torch.empty_like(out)
+        sparse_paged_decode_batched(qt, case.kv_cache, bt, sl, st, ref, vsrc, scale=case.scale)
+        torch.cuda.synchronize()
+        r5.assert_maps_inverse(0)
+        if not torch.equal(out.view(torch.int16), ref.view(torch.int16)):
+            raise AssertionError("config 4: tiered decode differs from the resident decode")
+        return "tiered == resident (last step, bit-exact); page2slot/slot2page inverse"
+
+    def run(qs, fetch, max_runs=20000, min_steps=8):
+        """Per-phase us (mean over the steps run) + hit statistics, from cold.  The copy
+        engine's first call (host-side planner and copy issue) runs once untimed."""
+        if fetch == "dma":
+            cold()
+            select_pages_quad(st, 0, qs[0], bt, sl, B, case.scale, derive=False)
+            dma_step(qs[0])
         cold()
         torch.cuda.synchronize()
         ph = dict(select=0.0, plan=0.0, fetch=0.0, decode=0.0)
@@ -668,7 +695,7 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
             sel += int(st.page_cnt[:B].sum())
             miss += int(r5.miss_cnt[:B].sum())
             n_done += 1
-            if fetch == "dma" and runs_tot / n_done > max_runs and n_done >= 2:
+            if fetch == "dma" and runs_tot / n_done > max_runs and n_done >= min_steps:
                 break                      # one host API call per run: a bounded sample
         wall = (time.perf_counter() - w0) * 1e6 / n_done
         hb = miss * 16 * 128 * 2 / n_done
@@ -683,7 +710,38 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
                  wall_us_per_step=round(wall, 1))
         if fetch == "dma":
             r["copy_runs_per_step"] = round(runs_tot / n_done, 1)
+        r["check"] = check_last(qs[n_done - 1])
         return r
+
+    def run_graph(qs, eager_state):
+        """The kernel-fetch steps captured in one HIP graph (select + plan + fetch + tiered
+        decode per step, each step's query baked in), replayed from a cold buffer: us per
+        step, and the final maps, clocks and output equal the eager run's."""
+        def all_steps():
+            for qt in qs:
+                select_pages_quad(st, 0, qt, bt, sl, B, case.scale, derive=False)
+                r5.gather_plan(0, st.page_table, st.page_cnt, bt, sl, B)
+                r5.gather_fetch(0, tier.staging, tier.pool, B)
+                mem_decode(qt, case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale)
+        cold()
+        g = graph_of(all_steps)
+        times = []
+        for _ in range(2):                 # the first replay warms up
+            cold()
+            torch.cuda.synchronize()
+            a, b = ev(), ev()
+            a.record()
+            g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) * 1e3 / len(qs))
+        for k, v in eager_state.items():
+            got = out if k == "out" else getattr(r5, k)
+            if not torch.equal(got.view(torch.uint8), v.view(torch.uint8)):
+                raise AssertionError(f"config 4: graph replay differs from eager in {k}")
+        del g
+        return dict(graph_us_per_step=round(times[-1], 1),
+                    graph_check="final out, maps, LRU clocks, step clock == eager run")
 
     res = dict(workload=f"config4: mem-v B={B} ctx 32768 quad r'=8 int8 nrm coverage 0.95, "
                         f"hot buffer {slots} slots per kv head (10 %), {steps} steps from a "
@@ -691,7 +749,15 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
                         f"(literal) and correlated (case q + 0.3 N(0,1))")
     for stream in streams:
         qs = queries(stream)
-        res[stream] = {f: run(qs, f) for f in fetches}
+        res[stream] = {}
+        for f in fetches:
+            res[stream][f] = run(qs, f)
+            if f == "kernel":
+                keep = {k: getattr(r5, k).clone()
+                        for k in ("page2slot", "slot2page", "lru_clock", "_clock2")}
+                keep["out"] = out.clone()
+                res[stream][f].update(run_graph(qs, keep))
+                del keep
         # the same steps with V resident in HBM
         a, b = ev(), ev()
         a.record()
@@ -707,7 +773,7 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
         if k is not None:
             log(f"config 4 ({boost}, {stream}): hit {k['hit_rate']}, kernel fetch "
                 f"{k['us_per_step']} us/step (select {k['select']}, plan {k['plan']}, fetch "
-                f"{k['fetch']}, decode {k['decode']}), dma "
+                f"{k['fetch']}, decode {k['decode']}; in-graph {k['graph_us_per_step']}), dma "
                 f"{dma['us_per_step'] if dma else '-'}, "
                 f"resident {res[stream]['resident_us_per_step']}")
         del qs

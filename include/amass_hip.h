@@ -283,8 +283,12 @@ int amass_dense_paged_decode(const amass_decode_args* a, void* stream); /* force
  * acc_part are ignored: the split-K partials live in the library's own file-scope device
  * array of AMASS_DECODE_SCRATCH_BYTES per GPU (held until the process ends).  The
  * partials take 4 * n_req * n_kv * split * G * (2 + d) bytes (+ <= 256 of alignment),
- * none with path 2 or split < 3; more than AMASS_DECODE_SCRATCH_BYTES returns
- * AMASS_ERR_CAPACITY (e.g. n_req 32, n_kv 8, G 4 fits split <= 63).  Nothing is allocated
+ * none with path 2 or split < 3.  A split larger than the array holds is lowered to the
+ * largest that fits (n_req 32, n_kv 8, G 4: 63 partial slots), so the device plan splits
+ * no unit into more than that many parts minus one; the output equals
+ * amass_sparse_decode's whenever the plan would not split more (config 1 splits a unit
+ * into 8).  Fewer than 3 slots fitting (n_req * n_kv * G > 21509) returns
+ * AMASS_ERR_CAPACITY before anything runs.  Nothing is allocated
  * and nothing needs clearing: every partial the merge reads is written by the same call.
  * All calls on one GPU share its array, so calls that overlap on one GPU (two streams,
  * two host threads) race. */

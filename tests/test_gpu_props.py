@@ -440,7 +440,7 @@ def _tier_example(c):
         p2s, s2p, lru, clock = ref["page2slot"], ref["slot2page"], ref["lru"], ref["clock"]
 
 
-@pytest.mark.parametrize("slots", [1, 7, 64, 600, 3000])
+@pytest.mark.parametrize("slots", [1, 7, 64, 600, 3000, 6553, 8192])
 def test_tier_plan_matches_oracle(slots):
     @TIER_PROPS
     @given(c=tier_cases(slots))

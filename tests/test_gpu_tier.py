@@ -78,20 +78,25 @@ def test_plan_matches_oracle_over_steps(slots):
 
 
 @pytest.mark.parametrize("slots,span,fill", [(3000, 40, 0.75), (700, 200, 1.0),
-                                            (700, 5000, 1.0)])
+                                            (700, 5000, 1.0), (6553, 40, 1.0),
+                                            (8192, 200, 0.9), (8192, 5000, 1.0)])
 def test_plan_matches_oracle_with_aged_clocks(slots, span, fill):
     """Victim order over an aged hot buffer: slots already hold pages with LRU clocks
     spread over `span` steps (clocks within 255 of the oldest take the histogram path,
-    wider spans the full radix sort), more slots than threads per kv head (3000), and
+    wider spans the full radix sort), more slots than threads per kv head (3000; 6553,
+    config 4's buffer, seven slots per thread; 8192, the most a kv head may hold), and
     repeated clocks (ties broken by slot index), empty slots (clock 0) or a full buffer.
     Bit-exact against the sequential oracle over four steps."""
     announce(f"tier plan aged clocks slots={slots} span={span} fill={fill}")
-    case = make_case(B=4, ctx=(2000, 6000), n_kv=8, G=4, heavy=0.0, seed=15)
+    big = slots > 3000
+    case = make_case(B=4, ctx=(40000, 60000) if big else (2000, 6000), n_kv=8, G=4,
+                     heavy=0.0, seed=15, device=DEV if big else "cpu")
+    case.block_table, case.seq_lens = case.block_table.cpu(), case.seq_lens.cpu()
     tier = _tier(case, slots)
     r5 = tier.residency
     NB = case.kv_cache.shape[0]
     gen = np.random.default_rng(slots + span)
-    assert NB >= 700
+    assert NB >= (slots if big else 700)
     p2s = np.full((8, NB), -1, np.int64)
     s2p = np.full((8, slots), -1, np.int64)
     lru = np.zeros((8, slots), np.int64)

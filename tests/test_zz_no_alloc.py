@@ -4,8 +4,12 @@ the reference) against amass_sparse_decode, through the C-ABI.
 Both run the same kernels with the same plan; only the split-K partials live elsewhere
 (the library's file-scope device array instead of the state's buffers), so the outputs
 must be bit-identical.  Two calls in a row, the second with a smaller batch (its merge
-must not see the first call's partials), for every decode path; a launch whose partials
-exceed the array is refused with AMASS_ERR_CAPACITY before anything runs.
+must not see the first call's partials), for every decode path.  The library's default
+split (128) at config 1's batch geometry (32 requests x 8 kv heads x G 4) needs more
+partial slots than the array holds: the entry point lowers the split to the 63 that fit,
+and the output still equals the allocating entry's (the plan splits a unit into 8 there).
+A batch for which fewer than 3 slots fit is refused with AMASS_ERR_CAPACITY before
+anything runs.
 """
 import ctypes as C
 
@@ -87,12 +91,27 @@ def test_noalloc_decode_matches_allocating_entry(path):
         assert np.allclose(npf(got), want, atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("path", ["auto", "split"])
+def test_noalloc_decode_at_the_default_split_of_a_full_batch(path):
+    announce(f"no-alloc decode, path={path}: B=32 at split 128 (63 slots fit)")
+    case, st, dev, tab, cnt = _setup(32, 4096, 0.9, seed=104)
+    assert st.split == 128
+    assert 4 * 32 * 8 * 128 * 4 * (2 + 128) > SCRATCH_BYTES      # the default does not fit
+    ref, got = _both(case, st, dev, path)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    # and again with a smaller batch right after (no leftover partials are read)
+    case, st, dev, tab, cnt = _setup(5, (500, 3000), 0.5, seed=105)
+    ref, got = _both(case, st, dev, path)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
 def test_noalloc_decode_refuses_oversized_partials():
     announce("no-alloc decode: capacity check")
-    case, st, dev, _, _ = _setup(2, (400, 800), 0.5, seed=103)
-    out = torch.zeros(2, 32, 128, dtype=torch.bfloat16, device=DEV)
+    B = 700                               # 700 * 8 * 4 slots per split: only 2 fit
+    case, st, dev, _, _ = _setup(B, (16, 64), 0.5, seed=103)
+    out = torch.zeros(B, 32, 128, dtype=torch.bfloat16, device=DEV)
     a = _args(case, st, dev, out, "split")
-    a.split = 16384                       # 2 * 8 * 16384 * 4 * 130 * 4 B > 32 MiB
+    assert (SCRATCH_BYTES - 256) // (4 * B * 8 * 4 * (2 + 128)) < 3
     lib = _hip.load_library()
     rc = lib.amass_sparse_decode_noalloc(C.byref(a), C.c_void_p(_hip.current_stream()))
     assert rc == -6                       # AMASS_ERR_CAPACITY, nothing launched
