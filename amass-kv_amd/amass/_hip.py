@@ -198,6 +198,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         fn.restype = C.c_int
     lib.amass_tier_dma.argtypes = [C.POINTER(CopyRun), C.c_int32, _P]
     lib.amass_tier_dma.restype = C.c_int
+    lib.amass_quad_select_attend.argtypes = [C.POINTER(QuadScoreArgs), C.POINTER(SelectArgs),
+                                             C.POINTER(DecodeArgs), C.c_int, _P]
+    lib.amass_quad_select_attend.restype = C.c_int
     lib.amass_host_pool_alloc.argtypes = [C.c_size_t, C.POINTER(_P), C.POINTER(_P)]
     lib.amass_host_pool_alloc.restype = C.c_int
     lib.amass_host_pool_free.argtypes = [_P]
@@ -230,6 +233,14 @@ def call(name: str, args, stream: int) -> None:
     """Invoke entry point `name` with struct `args` on `stream` (a hipStream_t int)."""
     lib = load_library()
     check(getattr(lib, name)(C.byref(args), _P(stream)), name)
+
+
+def call_select_attend(score, select, decode, mode: int, stream: int) -> None:
+    """amass_quad_select_attend (decode None: score + select only)."""
+    lib = load_library()
+    check(lib.amass_quad_select_attend(C.byref(score), C.byref(select),
+                                       C.byref(decode) if decode is not None else None,
+                                       mode, _P(stream)), "amass_quad_select_attend")
 
 
 def ptr(t) -> Optional[int]:

@@ -130,6 +130,20 @@ def select(q, kv_cache, block_table, seq_lens, st, n_req: int, scale: float,
         select_pages_r8(st, lidx, q, block_table, seq_lens, n_req, scale, derive=False)
 
 
+def select_and_decode(q, kv_cache, block_table, seq_lens, st, out, vsource, n_req: int,
+                      scale: float, cfg: AmassConfig) -> None:
+    """Stage A + Stage B of one layer (backend/attn.py:66-74): quad states take
+    select_then_attend (one launch for short rows, else score + select then the decode),
+    the r8 and CLSE states select() then decode_dispatch()."""
+    from ..selection import QuadState, select_then_attend
+    if isinstance(st, QuadState) and st.coords != "lse":
+        select_then_attend(st, layer_index(st, kv_cache), q, kv_cache, block_table, seq_lens,
+                           n_req, scale, out, vsource)
+        return
+    select(q, kv_cache, block_table, seq_lens, st, n_req, scale, cfg)
+    decode_dispatch(q, kv_cache, block_table, seq_lens, st, out, vsource, scale, cfg)
+
+
 def decode_dispatch(q, kv_cache, block_table, seq_lens, st, out, vsource, scale: float,
                     cfg: AmassConfig) -> None:
     """Stage B: sparse paged decode over st.page_table (split-K or fused, chosen by the

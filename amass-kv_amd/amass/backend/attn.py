@@ -9,6 +9,9 @@ runs the stock implementation unchanged.  A pure decode step runs
     select(...)           Stage A: score + selection -> st.page_table / st.page_cnt
     decode_dispatch(...)  Stage B: sparse paged decode -> output (in place)
 
+(``_runtime.select_and_decode``; a quad state takes ``select_then_attend``, which runs
+both stages in one launch for rows of <= 256 pages, with the same outputs)
+
 with K and V read from the resident paged cache.  ``forward`` has the reference's
 signature and returns ``output``.
 
@@ -80,10 +83,8 @@ class AmassAttentionImplMixin:
         n_req = m.seq_lens.shape[0]
         out3 = output if output.dim() == 3 else output.view(output.shape[0],
                                                             self.num_heads, -1)
-        _runtime.select(query, kv_cache, m.block_table, m.seq_lens, st, n_req,
-                        self.scale, cfg)
-        _runtime.decode_dispatch(query, kv_cache, m.block_table, m.seq_lens, st, out3,
-                                 ResidentVSource(kv_cache), self.scale, cfg)
+        _runtime.select_and_decode(query, kv_cache, m.block_table, m.seq_lens, st, out3,
+                                   ResidentVSource(kv_cache), n_req, self.scale, cfg)
         global _ANNOUNCED
         if not _ANNOUNCED:
             _ANNOUNCED = True

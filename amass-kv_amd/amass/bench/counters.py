@@ -8,7 +8,8 @@ SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_INSTS_MFMA SQ_BUSY_CY
 GRBM_GUI_ACTIVE MfmaUtil).  Dispatches are walked in dispatch order and grouped into the
 launches bench.py times: a decode dispatch with the merge dispatches after it
 (sparse_decode / dense_decode), an nrm pre-pass with the selection after it (select), a
-score dispatch (named quad_score / clse_score / r8_score after the bench result).
+score dispatch (named quad_score / clse_score / r8_score after the bench result), the
+per-unit pipeline (quad_select_attend).
 
 traffic: bytes per launch = 1024 * (f * FETCH_SIZE + w * WRITE_SIZE) (KiB counters), with
 f and w from torch's neg over 256 MiB fp32 in the same run (reads 256 MiB, writes 256 MiB:
@@ -55,6 +56,8 @@ def classify(name: str) -> str | None:
         return "nrm"
     if "select_kernel" in n:
         return "select"
+    if "unit_kernel" in n:
+        return "quad_select_attend"
     return None
 
 

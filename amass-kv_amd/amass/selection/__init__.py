@@ -13,8 +13,8 @@ from __future__ import annotations
 from .build import r8_build_bulk, r8_build_delta, r8_build_refresh, r8_build_tail
 from .quad_build import (quad_build_bulk, quad_build_delta, quad_build_refresh,
                          quad_build_tail)
-from .quad_score import (clse_score, nrm_combine, quad_score, select_pages_clse,
-                         select_pages_quad)
+from .quad_score import (clse_score, nrm_combine, quad_score, select_attend_quad,
+                         select_pages_clse, select_pages_quad, select_then_attend)
 from .quad_state import QuadState
 from .score import r8_score
 from .select import (coverage_select, derive_page_params, select_pages, select_pages_r8,
@@ -27,4 +27,5 @@ __all__ = [
     "select_pages", "select_pages_r8", "QuadState", "quad_build_refresh",
     "quad_build_tail", "quad_build_bulk", "quad_build_delta", "quad_score",
     "nrm_combine", "select_pages_quad", "clse_score", "select_pages_clse",
+    "select_attend_quad", "select_then_attend",
 ]

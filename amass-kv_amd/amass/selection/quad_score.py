@@ -13,8 +13,21 @@ from __future__ import annotations
 
 import torch
 
-from .._hip import ClseScoreArgs, NrmArgs, QuadScoreArgs, call, current_stream, ptr, require_cuda
-from .select import derive_page_params, select_pages
+import math
+
+from .._hip import (ClseScoreArgs, NrmArgs, QuadScoreArgs, call, call_select_attend,
+                    current_stream, ptr, require_cuda)
+from .select import derive_page_params, select_args, select_pages
+
+# The per-unit pipeline (amass_quad_select_attend): the rows it serves; the rows up to
+# which select_then_attend routes a layer through it (one workgroup streams a unit's
+# summaries at ~40 GB/s, so a unit of 256 pages takes ~8 us where the score kernel's
+# balanced walk would take the launch's fixed ~7 us anyway, and a ragged batch of longer
+# rows could wait on its longest unit); the kept pages per unit up to which it also
+# attends (beyond that the decode's split layout streams faster).
+UNIT_MAX_PAGES = 2048
+UNIT_ROUTE_MAX_PAGES = 256
+UNIT_ATTEND_MAX_PAGES = 32
 
 
 def _tile_max(st):
@@ -142,3 +155,70 @@ def select_pages_clse(st, layer: int, q, block_table, seq_lens, n_req: int, scal
     nrm = st.combine == "nrm"
     select_pages(st, n_req, score_h=st.score_h if nrm else None,
                  tile_max=_tile_max(st) if nrm else None)
+
+
+def unit_step_supported(st) -> bool:
+    """Whether amass_quad_select_attend serves this state: a quad nrm state (score_h and
+    per-tile maxima), r'=8 int8 summaries, G <= 8, rows of <= 2048 pages."""
+    return (getattr(st, "coords", "none") == "none" and st.combine == "nrm"
+            and st.r == 8 and st.v_bits == 8 and st.G <= 8
+            and st.max_pages <= UNIT_MAX_PAGES and _tile_max(st) is not None)
+
+
+def kept_pages_bound(st):
+    """An upper bound of any unit's page count that holds without reading the device, or
+    None: top-b with the index tie rule keeps b_fix = ceil(budget * selectable) <=
+    ceil(budget * max_pages) selectable pages plus the sinks, the recent window and the
+    partial tail page."""
+    if getattr(st, "coverage", None) is not None or getattr(st, "tie_mode", "index") != "index":
+        return None       # coverage: data-dependent; the threshold rule keeps every tie
+    return math.ceil(st.budget * st.max_pages) + st.sink_pages + st.window_pages + 1
+
+
+def select_attend_quad(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
+                       *, kv_cache=None, out=None, vsource=None, derive: bool = False) -> None:
+    """Stage A of one layer in one launch (amass_quad_select_attend): the quad score into
+    st.score_h / st.score_tmax, the nrm combine into st.score and the top-b or coverage
+    selection into st.page_table / st.page_cnt -- the outputs of select_pages_quad, bit
+    for bit -- with one workgroup per (request, kv head).  With ``out`` (and ``kv_cache``,
+    ``vsource``: resident V) the same workgroup then attends the kept pages into out, as
+    sparse_paged_decode_batched(path="fused") would."""
+    if not unit_step_supported(st):
+        raise ValueError("amass_quad_select_attend serves quad nrm states with r'=8 int8 "
+                         f"summaries, G <= 8 and <= {UNIT_MAX_PAGES} pages per row")
+    if n_req > st.max_reqs:
+        raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
+    if derive:
+        derive_page_params(st, seq_lens, n_req)
+    qa = _quad_args(st, layer, q, block_table, n_req, scale)
+    sa = select_args(st, n_req, score_h=st.score_h, tile_max=_tile_max(st))
+    da = None
+    if out is not None:
+        from ..attention.decode import _decode_args, _split_kv
+        if vsource is None or vsource.SRC_ID != 0:
+            raise ValueError("the in-launch attend reads resident V (a ResidentVSource)")
+        k, _ = _split_kv(kv_cache)
+        da = _decode_args(q, k, vsource, block_table, seq_lens, st, out, scale, n_req,
+                          dense=False, path="fused")
+    call_select_attend(qa, sa, da, sa.mode, current_stream(q.device))
+
+
+def select_then_attend(st, layer: int, q, kv_cache, block_table, seq_lens, n_req: int,
+                       scale: float, out, vsource) -> None:
+    """One layer's score + select + attend (quad states): through the per-unit pipeline
+    where that is the faster route -- rows of <= UNIT_ROUTE_MAX_PAGES pages; it also
+    attends when every unit keeps <= UNIT_ATTEND_MAX_PAGES pages, else the decode
+    follows -- otherwise select_pages_quad then sparse_paged_decode_batched.  The outputs
+    are the same either way, bit for bit."""
+    from ..attention.decode import sparse_paged_decode_batched
+    if unit_step_supported(st) and st.max_pages <= UNIT_ROUTE_MAX_PAGES:
+        bound = kept_pages_bound(st)
+        if bound is not None and bound <= UNIT_ATTEND_MAX_PAGES and vsource.SRC_ID == 0:
+            select_attend_quad(st, layer, q, block_table, seq_lens, n_req, scale,
+                               kv_cache=kv_cache, out=out, vsource=vsource)
+            return
+        select_attend_quad(st, layer, q, block_table, seq_lens, n_req, scale)
+    else:
+        select_pages_quad(st, layer, q, block_table, seq_lens, n_req, scale, derive=False)
+    sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out, vsource,
+                                scale=scale)

@@ -46,6 +46,15 @@ def score_kind(st) -> int:
 
 def _select(st, n_req: int, *, mode: str = "auto", score_h=None, tile_max=None,
             coverage=None, tie_mode=None) -> None:
+    a = select_args(st, n_req, mode=mode, score_h=score_h, tile_max=tile_max,
+                    coverage=coverage, tie_mode=tie_mode)
+    name = "amass_coverage_select" if a.mode == 1 else "amass_topb_select"
+    call(name, a, current_stream(st.score.device))
+
+
+def select_args(st, n_req: int, *, mode: str = "auto", score_h=None, tile_max=None,
+                coverage=None, tie_mode=None) -> SelectArgs:
+    """The amass_select_args of this selection (mode 1 = coverage, 0 = top-b)."""
     if n_req > st.max_reqs:
         raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
     if tile_max is not None and score_h is None:
@@ -76,8 +85,7 @@ def _select(st, n_req: int, *, mode: str = "auto", score_h=None, tile_max=None,
         n_req=n_req, n_kv=st.n_kv, G=st.G, max_pages=st.max_pages,
         sink_pages=st.sink_pages, mode=1 if coverage is not None else 0, tie_mode=tm,
         score_kind=score_kind(st))
-    name = "amass_coverage_select" if coverage is not None else "amass_topb_select"
-    call(name, a, current_stream(sc.device))
+    return a
 
 
 def topb_select(st, n_req: int, *, tie_mode=None) -> None:

@@ -1,0 +1,162 @@
+// Per-unit pipeline for small batches on gfx950: quad score -> nrm combine + top-b /
+// coverage selection -> (optionally) the sparse decode, one workgroup per (request, kv
+// head) unit, one launch.
+//
+// The three Stage-A/B launches of a layer (quad_score.hip, select.hip, decode.hip) each
+// spread a small batch over few workgroups and each pays a launch, a chain of dependent
+// memory rounds before its first useful load, and the gap to the next graph node; at
+// batch 1 those fixed costs are most of the step (three launches of 6-10 us for 2.5 MB).
+// Here the unit's workgroup runs the same device code back to back:
+//   score   wave w walks tiles w, w + 8, ... of the unit's kv head (quad_walk, the score
+//           kernel's tile loop), writing score_h and the per-tile maxima;
+//   select  the selection kernel's body (select_unit, fused nrm staging) reads them back
+//           after a workgroup barrier and writes score, page_table, page_cnt;
+//   attend  (ATTEND) the decode's whole layout (attend_whole): the 8 waves split the kept
+//           pages and merge through LDS into the output.
+// Global stores of one phase are read by other waves of the same workgroup in the next;
+// the workgroup barrier orders them (every wave of a workgroup runs on one CU, whose
+// vector L1 is write-through).  The outputs are those of the three separate launches bit
+// for bit: the same instructions compute them (the decode's whole layout is what the
+// separate decode picks for such batches, and what its fused path always runs).
+//
+// Served: quad nrm states (score_h and tile maxima), r' = 8 int8 summaries, G <= 8, rows
+// of at most 2048 pages (4 per selection thread), resident V.  The host asks for the
+// attend phase only when it can bound every unit's kept pages (top-b with a small
+// budget): a unit of many kept pages streams faster through the decode's split layout.
+#include "attend.h"
+#include "quad_tile.h"
+#include "select_unit.h"
+
+namespace amass {
+
+constexpr int UN_THREADS = 512;                 // 8 waves: the selection's and decode's
+constexpr int UN_WAVES = UN_THREADS / WAVE;
+constexpr int UN_MAXP = 4 * UN_THREADS;         // pages per row: 4 per selection thread
+
+template <int RP, int VB, int PPT, bool ATTEND>
+__global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
+                                                          const amass_select_args sa,
+                                                          const amass_decode_args da) {
+    __shared__ QuadLds qlds;
+    __shared__ XSel xs;
+    __shared__ WholeLds wl;
+    const int kh = blockIdx.x, r = blockIdx.y;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    // ---- score: the unit's tiles over the workgroup's waves ----------------------------
+    const int nsh = qp.nsh[r];
+    const int tiles = tiles_of(nsh);
+    if (wave < tiles)
+        quad_walk<RP, VB, true, false>(qp, qlds, wave, kh, r, nsh, wave,
+                                       (tiles - wave + UN_WAVES - 1) / UN_WAVES, UN_WAVES);
+    __syncthreads();
+
+    // ---- select (fused nrm staging over this workgroup's score_h and tile maxima) -------
+    const int cnt = select_unit<UN_THREADS, PPT, true>(sa, r, kh, xs);
+    if constexpr (ATTEND) {
+        __syncthreads();
+        // ---- attend the kept pages (the decode's whole layout) --------------------------
+        attend_whole<0, false>(da, r, kh, da.seq_lens[r], cnt, UN_WAVES, wl);
+    }
+}
+
+template <int PPT>
+static void launch_unit(const QuadParams& qp, const amass_select_args& sa,
+                        const amass_decode_args& da, bool attend, hipStream_t s) {
+    const dim3 grid(sa.n_kv, sa.n_req), blk(UN_THREADS);
+    if (attend) hipLaunchKernelGGL((unit_kernel<8, 8, PPT, true>), grid, blk, 0, s, qp, sa, da);
+    else hipLaunchKernelGGL((unit_kernel<8, 8, PPT, false>), grid, blk, 0, s, qp, sa, da);
+}
+
+static int unit_step(const amass_quad_score_args* q, const amass_select_args* sel,
+                     const amass_decode_args* dec, int mode, hipStream_t s) {
+    if (!q || !sel) return AMASS_ERR_NULL;
+    // score: the nrm combine's outputs are what the selection stages
+    if (!q->q || !q->rec || !q->block_table || !q->n_sel_hi || !q->score_h || !q->tile_max)
+        return AMASS_ERR_NULL;
+    if (q->combine != 1) return AMASS_ERR_UNSUPPORTED;
+    if (q->d != 128 || q->page != 16 || q->n_req < 0 || q->max_pages < 1 || q->n_kv < 1)
+        return AMASS_ERR_GEOMETRY;
+    if (q->G < 1 || q->G > 8) return AMASS_ERR_GEOMETRY;
+    if (q->rank != 8 || q->v_bits != 8) return AMASS_ERR_UNSUPPORTED;
+    if (q->max_pages > UN_MAXP) return AMASS_ERR_UNSUPPORTED;
+    if ((((uintptr_t)q->rec) & 15) != 0 || (q->rec_sb & 15) != 0) return AMASS_ERR_GEOMETRY;
+    if (q->rec_sb < (int64_t)q->n_kv * AMASS_QUAD_REC_BYTES(8, 8)) return AMASS_ERR_GEOMETRY;
+    // select: the same unit geometry, staging from the score's buffers
+    if (!sel->score || !sel->n_pages || !sel->n_sel_hi || !sel->page_table || !sel->page_cnt)
+        return AMASS_ERR_NULL;
+    if (mode != 0 && mode != 1) return AMASS_ERR_GEOMETRY;
+    if (mode == 0 && !sel->b_fix) return AMASS_ERR_NULL;
+    if (sel->n_req != q->n_req || sel->n_kv != q->n_kv || sel->G != q->G ||
+        sel->max_pages != q->max_pages || sel->n_sel_hi != q->n_sel_hi)
+        return AMASS_ERR_GEOMETRY;
+    if (sel->score_h != q->score_h || sel->sh_sr != q->sh_sr || sel->sh_sh != q->sh_sh ||
+        sel->sh_sg != q->sh_sg || sel->tile_max != q->tile_max || sel->tm_sr != q->tm_sr ||
+        sel->tm_sh != q->tm_sh || sel->tm_sg != q->tm_sg)
+        return AMASS_ERR_GEOMETRY;
+    if (sel->sink_pages < 0 || (sel->tie_mode != 0 && sel->tie_mode != 1) ||
+        (sel->score_kind != 0 && sel->score_kind != 1))
+        return AMASS_ERR_GEOMETRY;
+    if (mode == 1 && !(sel->coverage > 0.0 && sel->coverage <= 1.0)) return AMASS_ERR_GEOMETRY;
+    // attend: resident V, the selection's page table, the same unit geometry
+    if (dec) {
+        if (!dec->q || !dec->k || !dec->v || !dec->block_table || !dec->seq_lens || !dec->out)
+            return AMASS_ERR_NULL;
+        if (dec->v_src != 0 || dec->dense) return AMASS_ERR_UNSUPPORTED;
+        if (dec->d != DEC_D || dec->page != DEC_PAGE) return AMASS_ERR_GEOMETRY;
+        if (dec->n_req != q->n_req || dec->n_kv != q->n_kv || dec->G != q->G ||
+            dec->page_table != sel->page_table || dec->pt_sr != sel->pt_sr ||
+            dec->pt_sh != sel->pt_sh || dec->page_cnt != sel->page_cnt ||
+            dec->pc_sr != sel->pc_sr || dec->block_table != q->block_table ||
+            dec->bt_st != q->bt_st)
+            return AMASS_ERR_GEOMETRY;
+        const auto off = [](const void* p, uintptr_t align) {
+            return ((uintptr_t)p & (align - 1)) != 0;
+        };
+        if (off(dec->k, 16) || ((dec->k_sb | dec->k_st | dec->k_sh) & 7)) return AMASS_ERR_GEOMETRY;
+        if (off(dec->v, 16) || ((dec->v_sb | dec->v_st | dec->v_sh) & 7)) return AMASS_ERR_GEOMETRY;
+        if (off(dec->q, 8) || ((dec->q_st | dec->q_hs) & 3)) return AMASS_ERR_GEOMETRY;
+        if (off(dec->out, 4) || ((dec->o_st | dec->o_hs) & 1)) return AMASS_ERR_GEOMETRY;
+    }
+    if (q->n_req == 0) return AMASS_OK;
+
+    QuadParams p;
+    p.q = (const uint16_t*)q->q; p.q_st = q->q_st; p.q_hs = q->q_hs;
+    p.rec = q->rec; p.rec_sb = q->rec_sb;
+    p.bt = q->block_table; p.bt_st = q->bt_st;
+    p.nsh = q->n_sel_hi;
+    p.score = q->score; p.sc_sr = q->sc_sr; p.sc_sh = q->sc_sh;
+    p.score_h = q->score_h; p.sh_sr = q->sh_sr; p.sh_sh = q->sh_sh; p.sh_sg = q->sh_sg;
+    p.tmax = q->tile_max; p.tm_sr = q->tm_sr; p.tm_sh = q->tm_sh; p.tm_sg = q->tm_sg;
+    p.comb_out = nullptr;
+    p.scale = q->scale;
+    p.n_req = q->n_req; p.n_kv = q->n_kv; p.G = q->G; p.page = q->page;
+    p.max_pages = q->max_pages;
+    p.hw = 1;
+    p.target = 1;
+    amass_select_args sa = *sel;
+    sa.mode = mode;
+    amass_decode_args da;
+    if (dec) da = *dec;
+    else __builtin_memset(&da, 0, sizeof(da));
+    int ppt = 1;
+    while (ppt * UN_THREADS < p.max_pages) ppt *= 2;           // <= 4 (UN_MAXP)
+    const bool attend = dec != nullptr;
+    switch (ppt) {
+        case 1: launch_unit<1>(p, sa, da, attend, s); break;
+        case 2: launch_unit<2>(p, sa, da, attend, s); break;
+        default: launch_unit<4>(p, sa, da, attend, s); break;
+    }
+    return check_launch();
+}
+
+}  // namespace amass
+
+using namespace amass;
+
+extern "C" int amass_quad_select_attend(const amass_quad_score_args* score,
+                                        const amass_select_args* select,
+                                        const amass_decode_args* decode, int mode,
+                                        void* stream) {
+    return unit_step(score, select, decode, mode, (hipStream_t)stream);
+}

@@ -398,7 +398,10 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
                                         sparse_paged_decode_batched)
     from amass.selection import (derive_page_params, select_pages_clse, select_pages_quad,
                                  select_pages_r8)
-    from amass.selection.quad_score import clse_score, quad_score_launch
+    from amass.selection.quad_score import (UNIT_ATTEND_MAX_PAGES, UNIT_ROUTE_MAX_PAGES,
+                                            clse_score, kept_pages_bound, quad_score_launch,
+                                            select_attend_quad, select_then_attend,
+                                            unit_step_supported)
     from amass.selection.score import r8_score
     from amass.selection.select import select_pages
 
@@ -419,9 +422,24 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
         else:
             select_pages_r8(st, 0, q, bt, sl, B, case.scale, derive=False)
 
+    # the route the backend takes (select_then_attend): one launch for short rows
+    unit = score == "quad" and unit_step_supported(st) and st.max_pages <= UNIT_ROUTE_MAX_PAGES
+    bound = kept_pages_bound(st) if unit else None
+    unit_attend = unit and bound is not None and bound <= UNIT_ATTEND_MAX_PAGES
+
     def sparse_step():
+        if score == "quad":
+            select_then_attend(st, 0, q, kv, bt, sl, B, case.scale, out, vsrc)
+            return
         stage_a()
         sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc, scale=case.scale)
+
+    def unit_only():
+        if unit_attend:
+            select_attend_quad(st, 0, q, bt, sl, B, case.scale, kv_cache=kv, out=out,
+                               vsource=vsrc)
+        else:
+            select_attend_quad(st, 0, q, bt, sl, B, case.scale)
 
     def dense_step():
         dense_paged_decode(q, kv, bt, sl, st, out_d, scale=case.scale)
@@ -445,6 +463,14 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
     ms_dense_eager = time_eager(dense_step, args.steps, args.warmup)
     reps = 10
     k_steps = max(5, args.steps // 5)
+    # the step captured 10x in one graph, as a model's layers would be: the host's
+    # per-replay launch cost (~7 us) no longer bounds a tiny step
+    g10 = graph_of(sparse_step, reps)
+    us_sparse10 = time_graph(g10, k_steps, 2, reps) * 1e3
+    del g10
+    g10 = graph_of(dense_step, reps)
+    us_dense10 = time_graph(g10, k_steps, 2, reps) * 1e3
+    del g10
     g_score = graph_of(score_only, reps)
     us_score = time_graph(g_score, k_steps, 2, reps) * 1e3
     g_sel = graph_of(lambda: select_pages(st, B, score_h=st.score_h if nrm else None,
@@ -453,6 +479,11 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
     g_att = graph_of(lambda: sparse_paged_decode_batched(q, kv, bt, sl, st, out, vsrc,
                                                           scale=case.scale), reps)
     us_att = time_graph(g_att, k_steps, 2, reps) * 1e3
+    us_unit = None
+    if unit:
+        g_unit = graph_of(unit_only, reps)
+        us_unit = time_graph(g_unit, k_steps, 2, reps) * 1e3
+        del g_unit
     torch.cuda.synchronize()
     del g_sparse, g_dense, g_score, g_sel, g_att
     cnt = st.page_cnt[:B]
@@ -470,13 +501,25 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
                    kernel_entry(us_sel, b_sel, traffic.get("select"), mf.get("select")),
                "sparse_decode": kernel_entry(us_att, b_att, traffic.get("sparse_decode"),
                                              mf.get("sparse_decode"))}
-    return dict(us=round(ms_sparse * 1e3, 2),
+    if unit:
+        # the one-launch route the step takes; the entries above time the same work as
+        # the three separate launches the route replaces
+        b_unit = b_score + b_sel + (b_att if unit_attend else 0)
+        kernels["quad_select_attend"] = kernel_entry(us_unit, b_unit,
+                                                     traffic.get("quad_select_attend"),
+                                                     mf.get("quad_select_attend"))
+    route = ("one launch (amass_quad_select_attend: score, select and attend)" if unit_attend
+             else "amass_quad_select_attend (score, select) + amass_sparse_decode" if unit
+             else "separate launches: score, select, decode")
+    return dict(us=round(ms_sparse * 1e3, 2), route=route,
                 gb_s=round((b_score + b_sel + b_att) / (ms_sparse * 1e-3) / 1e9, 1),
                 dense_us=round(ms_dense * 1e3, 2),
                 dense_gb_s=round(b_dense / (ms_dense * 1e-3) / 1e9, 1),
                 speedup_vs_dense=round(ms_dense / ms_sparse, 3),
                 eager_us=round(ms_sparse_eager * 1e3, 2),
                 dense_eager_us=round(ms_dense_eager * 1e3, 2),
+                graph10_us=round(us_sparse10, 2), dense_graph10_us=round(us_dense10, 2),
+                speedup_vs_dense_graph10=round(us_dense10 / us_sparse10, 3),
                 dense_bytes=b_dense, dense_traffic=traffic.get("dense_decode"),
                 selected_fraction=round(frac, 4), attended_fraction=round(att_frac, 4),
                 kernels=kernels)

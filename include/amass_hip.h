@@ -295,6 +295,26 @@ int amass_dense_paged_decode(const amass_decode_args* a, void* stream); /* force
 #define AMASS_DECODE_SCRATCH_BYTES (32 * 1024 * 1024)
 int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
 
+/* ---- per-unit pipeline (small batches) ---------------------------------------------- */
+/* Replaces, in one launch, the layer's Stage A + Stage B sequence of backend/attn.py:66-74
+ * (select_pages -> quad_score_cuda + nrm/top-b select, then decode_dispatch), for the
+ * same outputs bit for bit: amass_quad_score (combine 1, writing score_h and tile_max),
+ * then amass_topb_select (mode 0) or amass_coverage_select (mode 1) with the fused nrm
+ * staging over that score_h / tile_max, then -- when `decode` is not NULL --
+ * amass_sparse_decode over the new page table in the layout that attends each
+ * (request, kv-head) unit with one workgroup (path 2's).  One workgroup per unit runs
+ * the three phases back to back, so a batch of few units pays one launch instead of
+ * three.  The structs are those of the three entry points and must describe one batch:
+ * select->score_h / tile_max / n_sel_hi are score's, decode->page_table / page_cnt are
+ * select's, decode->block_table is score's.  Served: combine 1, rank 8, v_bits 8,
+ * G <= 8, max_pages <= 2048, resident V (v_src 0); other shapes return
+ * AMASS_ERR_UNSUPPORTED before anything runs.  Pass `decode` only when every unit keeps
+ * few pages (a unit of many pages streams faster through amass_sparse_decode's split
+ * layout); with NULL the caller runs amass_sparse_decode next. */
+int amass_quad_select_attend(const amass_quad_score_args* score,
+                             const amass_select_args* select,
+                             const amass_decode_args* decode, int mode, void* stream);
+
 /* ---- mem-v tier ------------------------------------------------------------------ */
 /* Replaces tier/residency.py:385-407 (gather_plan: _miss_diff_kernel +
  * _select_victims_kernel).  Per (request, kv-head) every selected COMPLETE page is a hit

@@ -52,7 +52,7 @@ _KIND = {"p": ctypes.c_void_p, "int64_t": ctypes.c_int64, "int32_t": ctypes.c_in
 def test_library_loads_and_exports_every_symbol():
     lib = _hip.load_library()
     names = _declared_functions()
-    assert len(names) == 24
+    assert len(names) == 25
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert lib.amass_abi_version() == 9

@@ -299,3 +299,29 @@ def test_k_only_kv_cache_spec_patch(vllm):
         vllm.Attention(vllm.SlidingWindowSpec(16, 8, 128, 4096)).get_kv_cache_spec(None)
     with pytest.raises(ValueError, match="asymmetric"):
         vllm.Attention(vllm.FullAttentionSpec(16, 8, 128, 64)).get_kv_cache_spec(None)
+
+
+def test_quad_states_take_the_one_launch_route(monkeypatch):
+    """_runtime.select_and_decode sends a quad state (not CLSE) through
+    select_then_attend, with the layer the builder bound and the impl's arguments; r8
+    and CLSE states go through select + decode_dispatch."""
+    import amass.selection as sel_mod
+    from amass.selection import QuadState
+    calls = []
+    monkeypatch.setattr(sel_mod, "select_then_attend", lambda *a: calls.append(("one", a)))
+    monkeypatch.setattr(_runtime, "select", lambda *a: calls.append(("select", a)))
+    monkeypatch.setattr(_runtime, "decode_dispatch", lambda *a: calls.append(("decode", a)))
+    cfg = AmassConfig(**FAST)
+    kv = torch.zeros(4, 2, 16, 8, 128)
+    q, out, bt, sl = torch.zeros(3, 32, 128), torch.zeros(3, 32, 128), "bt", "sl"
+    quad = QuadState.__new__(QuadState)
+    quad.coords, quad._layer_of = "none", {kv.data_ptr(): 5}
+    _runtime.select_and_decode(q, kv, bt, sl, quad, out, "vs", 3, 0.088, cfg)
+    assert [c[0] for c in calls] == ["one"]
+    a = calls[0][1]
+    assert a[0] is quad and a[1] == 5 and a[2] is q and a[3] is kv and a[6] == 3
+    assert a[7] == 0.088 and a[8] is out and a[9] == "vs"
+    calls.clear()
+    quad.coords = "lse"
+    _runtime.select_and_decode(q, kv, bt, sl, quad, out, "vs", 3, 0.088, cfg)
+    assert [c[0] for c in calls] == ["select", "decode"]
