@@ -254,14 +254,19 @@ __device__ __forceinline__ void block_head_max(float* m, int G, float (*red)[CAP
         }
 }
 
-// The nrm combine of NP_PAGES pages of one unit (workgroup (chunk, kv-head, request)):
+// The nrm combine of NP_PAGES pages of one unit (workgroup (kv-head, request, chunk)):
 // score[p] = sum_{g ascending} exp(score_h[g][p] - hmax_g), hmax_g = the maximum of the
 // unit's per-tile maxima (the same maxima and sums as the fused staging).  The score_h
 // loads are issued before the maxima are read and reduced.
 __global__ __launch_bounds__(NP_THREADS) void nrm_pass_kernel(const amass_select_args a) {
     constexpr int TPT = (SEL_MAXP / XS_TILE) / NP_THREADS;   // tile maxima per thread
     __shared__ float red[8][NP_THREADS / WAVE];
-    const int chunk = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    // chunk is the slowest grid dimension: workgroups are dealt to the 8 XCDs round-robin
+    // in grid order, so (with n_kv * n_req a multiple of 8) a unit's chunks share one XCD
+    // and its L2 -- the unit's tile maxima, which every chunk reads, come from HBM once
+    // per unit, and the selection launch after (grid (n_kv, n_req)) finds the unit's
+    // combined scores in the same XCD's L2
+    const int kh = blockIdx.x, r = blockIdx.y, chunk = blockIdx.z;
     const int tid = threadIdx.x, G = a.G, MP = a.max_pages;
     const int p0 = chunk * NP_PAGES;
     const float* sh = a.score_h + (int64_t)r * a.sh_sr + (int64_t)kh * a.sh_sh;
@@ -376,7 +381,7 @@ static int select_common(const amass_select_args* a, int mode, void* stream) {
             // the standalone two-pass combine), then the selection over st.score
             if (k.tile_max) {
                 const int chunks = (k.max_pages + NP_PAGES - 1) / NP_PAGES;
-                hipLaunchKernelGGL(nrm_pass_kernel, dim3(chunks, k.n_kv, k.n_req),
+                hipLaunchKernelGGL(nrm_pass_kernel, dim3(k.n_kv, k.n_req, chunks),
                                    dim3(NP_THREADS), 0, st, k);
             } else {
                 amass_nrm_args na;
