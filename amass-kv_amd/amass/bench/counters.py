@@ -136,7 +136,7 @@ def score_name(res):
     return next((k for k in res.get("kernels", {}) if k.endswith("_score")), "score")
 
 
-HOT = ("score", "select", "sparse_decode", "dense_decode")
+HOT = ("score", "select", "sparse_decode", "dense_decode", "quad_select_attend")
 
 
 def traffic(fetch_db, write_db, name, bench_json=None):

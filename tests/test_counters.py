@@ -28,6 +28,8 @@ def test_classify_names():
     assert c("amass::nrm_pass_kernel(amass_select_args)") == "nrm"
     assert c("void amass::select_kernel<512, 2, true>(amass_select_args)") == "select"
     assert c("amass_calib::gather_calib_kernel(unsigned short const*)") == "calib_gather"
+    assert c("void amass::unit_kernel<8, 8, 1, true>(QuadParams, amass_select_args, "
+             "amass_decode_args)") == "quad_select_attend"
     assert c("amass::derive_kernel(amass_derive_args)") is None
 
 
@@ -59,3 +61,13 @@ def test_profiles_cover_every_kernel(name, score):
     e = b.mfma_entry(100.0, m["sparse_decode"])
     assert e["type"] == "bf16" and 0 < e["frac"] < 1 and e["busy_pct"] > 0
     assert b.mfma_entry(100.0, m[score])["type"] == "i8"
+
+
+def test_config0_profile_covers_the_one_launch_route():
+    """Config 0 takes the one-launch route (amass_quad_select_attend); its profile carries a
+    traffic and an MFMA line for that launch beside the separate kernels'."""
+    b = _bench()
+    t, m = b.profiled_traffic("config0"), b.profiled_mfma("config0")
+    for k in ("quad_select_attend", "quad_score", "select", "sparse_decode"):
+        assert t.get(k, 0) > 0, k
+        assert k in m, k
