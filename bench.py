@@ -39,6 +39,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -684,15 +685,20 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
         return "tiered == resident (last step, bit-exact); page2slot/slot2page inverse"
 
     def run(qs, fetch, max_runs=20000, min_steps=8):
-        """Per-phase us (mean over the steps run) + hit statistics, from cold.  The copy
-        engine's first call (host-side planner and copy issue) runs once untimed."""
+        """Per-phase us (mean, median and steady-state mean over the steps run) + hit
+        statistics, from cold.  One untimed step first (the first calls of the copy
+        engine's host-side planner and copy issue, and of the tiered kernels)."""
+        cold()
+        select_pages_quad(st, 0, qs[0], bt, sl, B, case.scale, derive=False)
         if fetch == "dma":
-            cold()
-            select_pages_quad(st, 0, qs[0], bt, sl, B, case.scale, derive=False)
             dma_step(qs[0])
+        else:
+            r5.gather_plan(0, st.page_table, st.page_cnt, bt, sl, B)
+            r5.gather_fetch(0, tier.staging, tier.pool, B)
+            mem_decode(qs[0], case.kv_cache, bt, sl, st, out, tier, 0, scale=case.scale)
         cold()
         torch.cuda.synchronize()
-        ph = dict(select=0.0, plan=0.0, fetch=0.0, decode=0.0)
+        ph = dict(select=[], plan=[], fetch=[], decode=[])     # per step, us
         sel = miss = runs_tot = 0
         n_done = 0
         w0 = time.perf_counter()
@@ -710,14 +716,14 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
                 e4 = ev()
                 e4.record()
                 torch.cuda.synchronize()
-                ph["plan"] += e[1].elapsed_time(e[2]) * 1e3
-                ph["fetch"] += e[2].elapsed_time(e[3]) * 1e3
-                ph["decode"] += e[3].elapsed_time(e4) * 1e3
+                ph["plan"].append(e[1].elapsed_time(e[2]) * 1e3)
+                ph["fetch"].append(e[2].elapsed_time(e[3]) * 1e3)
+                ph["decode"].append(e[3].elapsed_time(e4) * 1e3)
             else:
                 e[2].synchronize()
                 h0 = time.perf_counter()
                 plan, staged = r5.build_dma_plan(0, tier.pool, B)     # synchronises
-                ph["plan"] += (time.perf_counter() - h0) * 1e6 + e[1].elapsed_time(e[2]) * 1e3
+                ph["plan"].append((time.perf_counter() - h0) * 1e6 + e[1].elapsed_time(e[2]) * 1e3)
                 side = tier.copy_engine.next_stream()
                 side.wait_stream(torch.cuda.current_stream())
                 fs = ev()
@@ -731,10 +737,10 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
                 e4 = ev()
                 e4.record()
                 torch.cuda.synchronize()
-                ph["fetch"] += fs.elapsed_time(done) * 1e3
-                ph["decode"] += e[3].elapsed_time(e4) * 1e3
+                ph["fetch"].append(fs.elapsed_time(done) * 1e3)
+                ph["decode"].append(e[3].elapsed_time(e4) * 1e3)
                 runs_tot += len(plan)
-            ph["select"] += e[0].elapsed_time(e[1]) * 1e3
+            ph["select"].append(e[0].elapsed_time(e[1]) * 1e3)
             sel += int(st.page_cnt[:B].sum())
             miss += int(r5.miss_cnt[:B].sum())
             n_done += 1
@@ -742,7 +748,13 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
                 break                      # one host API call per run: a bounded sample
         wall = (time.perf_counter() - w0) * 1e6 / n_done
         hb = miss * 16 * 128 * 2 / n_done
-        r = {k: round(v / n_done, 1) for k, v in ph.items()}
+        r = {k: round(sum(v) / n_done, 1) for k, v in ph.items()}
+        # the cold first steps (every selected page a miss) dominate the means; the
+        # medians and the steady-state means (steps 9 on) are the warm buffer's figures
+        r["median"] = {k: round(statistics.median(v), 1) for k, v in ph.items()}
+        if n_done > 8:
+            r["steady_mean"] = {k: round(sum(v[8:]) / (n_done - 8), 1) for k, v in ph.items()}
+            r["steady_us_per_step"] = round(sum(r["steady_mean"].values()), 1)
         r.update(steps=n_done, hit_rate=round(1.0 - miss / max(sel, 1), 4),
                  selected_pages_per_step=round(sel / n_done, 1),
                  miss_pages_per_step=round(miss / n_done, 1),
@@ -816,7 +828,8 @@ def run_config4(args, boost="sigma", steps=64, streams=("fresh", "correlated"),
         if k is not None:
             log(f"config 4 ({boost}, {stream}): hit {k['hit_rate']}, kernel fetch "
                 f"{k['us_per_step']} us/step (select {k['select']}, plan {k['plan']}, fetch "
-                f"{k['fetch']}, decode {k['decode']}; in-graph {k['graph_us_per_step']}), dma "
+                f"{k['fetch']}, decode {k['decode']}; in-graph {k['graph_us_per_step']}; "
+                f"steady {k.get('steady_us_per_step')}, median {k['median']}), dma "
                 f"{dma['us_per_step'] if dma else '-'}, "
                 f"resident {res[stream]['resident_us_per_step']}")
         del qs
