@@ -51,7 +51,9 @@ void quad_score_kernel(const QuadParams p) {
     // workgroup (unit u = (request, z), head group y): wave w serves head y * hw + w
     const int h = blockIdx.y * p.hw + wave;
     TileWalk tw;
-    if (!tile_walk(p.nsh, p.n_req, p.target, blockIdx.x, tw) || tw.count <= 0) return;
+    if (!tile_walk(p.nsh, p.n_req, p.max_pages, p.target, blockIdx.x, tw) ||
+        tw.count <= 0)
+        return;
     quad_walk<RP, VB, NRM, COMB>(p, lds, wave, h, tw.req, tw.nsh, tw.first, tw.count,
                                  tw.stride);
 }

@@ -417,7 +417,9 @@ void r8_score_kernel(const R8Params p) {
     const int pair = kg % GP, part = kg / GP;
     const int h = blockIdx.y * p.hw + wave;
     TileWalk tw;
-    if (!tile_walk(p.nsh, p.n_req, p.target, blockIdx.x, tw) || tw.count <= 0) return;
+    if (!tile_walk(p.nsh, p.n_req, p.max_pages, p.target, blockIdx.x, tw) ||
+        tw.count <= 0)
+        return;
     const int req = tw.req;
     const int nsh = tw.nsh;
     const int sl = p.sl[req];

@@ -258,57 +258,65 @@ struct TileWalk {
     int first;     // first tile
     int stride;    // tile stride (workgroups of the request)
     int count;     // tiles walked
-    int nsh;       // the request's n_sel_hi (taken from the walk's own loads)
+    int nsh;       // the request's n_sel_hi (from the walk's own loads; <= the row width)
 };
 
 __device__ __forceinline__ int tiles_of(int nsh) {
     return nsh > 0 ? (nsh + SC_TILE - 1) / SC_TILE : 0;
 }
 
+// scored pages of request r: n_sel_hi, at most the rows' width mp (the score rows are mp
+// pages wide whatever lengths a caller passes)
+__device__ __forceinline__ int scored_of(const int32_t* nsh, int r, int mp) {
+    return min(nsh[r], mp);
+}
+
 // tiles of requests base + lane (0 past the batch)
-__device__ __forceinline__ int lane_tiles(const int32_t* nsh, int n_req, int base) {
+__device__ __forceinline__ int lane_tiles(const int32_t* nsh, int n_req, int mp, int base) {
     const int r = base + (threadIdx.x & 63);
-    return r < n_req ? tiles_of(nsh[r]) : 0;
+    return r < n_req ? tiles_of(scored_of(nsh, r, mp)) : 0;
 }
 
 // workgroups the batch takes at tpw tiles per workgroup (every lane gets the sum);
 // t0 = lane_tiles(0)
-__device__ __forceinline__ int walk_total(const int32_t* nsh, int n_req, int t0, int tpw) {
+__device__ __forceinline__ int walk_total(const int32_t* nsh, int n_req, int mp, int t0,
+                                          int tpw) {
     int tot = wave_sum_uniform((t0 + tpw - 1) / tpw);
     for (int base = WAVE; base < n_req; base += WAVE)
-        tot += wave_sum_uniform((lane_tiles(nsh, n_req, base) + tpw - 1) / tpw);
+        tot += wave_sum_uniform((lane_tiles(nsh, n_req, mp, base) + tpw - 1) / tpw);
     return tot;
 }
 
-__device__ __forceinline__ int walk_tpw(const int32_t* nsh, int n_req, int target, int t0) {
+__device__ __forceinline__ int walk_tpw(const int32_t* nsh, int n_req, int mp, int target,
+                                        int t0) {
     int total = wave_sum_uniform(t0), tmax = wave_max_uniform(t0);
     for (int base = WAVE; base < n_req; base += WAVE) {
-        const int t = lane_tiles(nsh, n_req, base);
+        const int t = lane_tiles(nsh, n_req, mp, base);
         total += wave_sum_uniform(t);
         tmax = max(tmax, wave_max_uniform(t));
     }
     if (total <= 0) return 1;
     int lo = (total + target - 1) / target;
-    if (walk_total(nsh, n_req, t0, lo) <= target) return lo;
+    if (walk_total(nsh, n_req, mp, t0, lo) <= target) return lo;
     int hi = max(lo, tmax);                 // at hi every request takes one workgroup
     ++lo;
     while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (walk_total(nsh, n_req, t0, mid) <= target) hi = mid;
+        if (walk_total(nsh, n_req, mp, t0, mid) <= target) hi = mid;
         else lo = mid + 1;
     }
     return lo;
 }
 
-__device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int target, int x,
-                                          TileWalk& w) {
+__device__ __forceinline__ bool tile_walk(const int32_t* nsh, int n_req, int mp, int target,
+                                          int x, TileWalk& w) {
     const int lane = threadIdx.x & 63;
-    const int v0 = lane < n_req ? nsh[lane] : 0;
+    const int v0 = lane < n_req ? scored_of(nsh, lane, mp) : 0;
     const int t0 = tiles_of(v0);
-    const int tpw = walk_tpw(nsh, n_req, target, t0);
+    const int tpw = walk_tpw(nsh, n_req, mp, target, t0);
     int before = 0;                                     // workgroups of earlier batches
     for (int base = 0; base < n_req; base += WAVE) {
-        const int v = base == 0 ? v0 : (base + lane < n_req ? nsh[base + lane] : 0);
+        const int v = base == 0 ? v0 : (base + lane < n_req ? scored_of(nsh, base + lane, mp) : 0);
         const int t = tiles_of(v);
         const int nw = (t + tpw - 1) / tpw;
         const int incl = wave_incl_scan(nw);

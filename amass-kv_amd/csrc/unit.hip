@@ -44,7 +44,7 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
     // ---- score: the unit's tiles over the workgroup's waves ----------------------------
-    const int nsh = qp.nsh[r];
+    const int nsh = scored_of(qp.nsh, r, qp.max_pages);
     const int tiles = tiles_of(nsh);
     if (wave < tiles)
         quad_walk<RP, VB, true, false>(qp, qlds, wave, kh, r, nsh, wave,
