@@ -140,6 +140,24 @@ def test_ragged_batches_match_separate(B, hi, G, mode, tie):
     _compare(case, st, attend=True)
 
 
+@pytest.mark.parametrize("mode", ["topb", "coverage"])
+def test_short_and_padded_rows_match_separate(mode):
+    """Rows with no scored page (1-2 pages: n_sel_hi <= 1), keep-all rows (a selectable
+    region of one page), a padded row (seq_len 0) and a partial last page, beside rows of
+    a few tiles: every output equals the separate launches'."""
+    announce(f"unit pipeline: short and padded rows, {mode}")
+    case = make_case(B=8, ctx=(1, 600), n_kv=8, G=4, heavy=0.05, table="perm", seed=31,
+                     device=DEV)
+    sl = case.seq_lens.clone()
+    sl[0], sl[1], sl[2], sl[3] = 0, 16, 32, 45
+    case.seq_lens.copy_(sl)
+    kw = dict(coverage=0.95) if mode == "coverage" else dict(budget=0.3)
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", **kw)
+    _compare(case, st, attend=False)
+    _compare(case, st, attend=True)
+    assert int(st.page_cnt[0].max()) == 0          # the padded row keeps nothing
+
+
 def test_runtime_route_and_graph_replay():
     """select_then_attend (the route the backend and the bench take) picks the one-launch
     pipeline for config 0; its graph replays equal the eager result."""
