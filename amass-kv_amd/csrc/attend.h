@@ -205,9 +205,10 @@ __device__ __forceinline__ int unit_count(const amass_decode_args& a, int r, int
     return a.page_cnt[(int64_t)r * a.pc_sr + kh];
 }
 
-// The whole layout of one unit (request r, kv head kh, cnt pages): the workgroup's hw
-// waves attend pages w, w + hw, ... of the unit, merge their (m, l, acc) through LDS and
-// write the normalised output (no partials).
+// The whole layout of one unit (request r, kv head kh, cnt pages): waves w < hw of the
+// workgroup attend pages w, w + hw, ... of the unit, merge their (m, l, acc) through LDS
+// and write the normalised output (no partials).  hw fixes the fp32 accumulation order,
+// so callers with the same hw write the same bits.
 struct WholeLds {
     float m[DEC_WAVES][8];
     float l[DEC_WAVES][8];
@@ -220,7 +221,7 @@ __device__ __forceinline__ void attend_whole(const amass_decode_args& a, int r, 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     WaveState st;
     init_state(st);
-    if (w < cnt) {
+    if (w < hw && w < cnt) {          // waves past hw (a larger workgroup) only merge
         bf16x4_t qb[8];
         load_q(a, r, kh, lane, qb);
         attend_run<VSRC, DENSE>(a, r, kh, sl, w, cnt, hw, lane, qb, st);

@@ -56,7 +56,9 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
     if constexpr (ATTEND) {
         __syncthreads();
         // ---- attend the kept pages (the decode's whole layout) --------------------------
-        attend_whole<0, false>(da, r, kh, da.seq_lens[r], cnt, UN_WAVES, wl);
+        // as many waves as the decode's workgroup has (one per kv head, at most 8), so
+        // the pages split, and the output rounds, as in amass_sparse_decode's layout
+        attend_whole<0, false>(da, r, kh, da.seq_lens[r], cnt, min(da.n_kv, UN_WAVES), wl);
     }
 }
 

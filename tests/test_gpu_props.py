@@ -22,7 +22,11 @@ ragged and empty units and NaN-poisoned slots past each sequence's end.  The nrm
 from per-head scores and per-tile maxima (the fused staging and the pre-pass) runs over
 generated GQA groups, lengths and head-score patterns (normal, a value pool with ties,
 masses over ~100 nats, a sink page holding every head's maximum): its combined scores are
-bit-identical to the standalone combine and its page tables equal the oracle's.
+bit-identical to the standalone combine and its page tables equal the oracle's.  The
+per-unit pipeline (score, selection and attend in one launch) runs over generated
+batches (kv-head counts, GQA groups, sink and window widths, lengths from padded rows to
+2048 pages, both selection modes and tie rules, with and without the attend) and equals
+the separate launches bit for bit.
 """
 import numpy as np
 import pytest
@@ -478,3 +482,40 @@ def test_write_path_matches_oracle_on_generated_schedules(c):
     for ql in c["sched"]:
         sc.step(ql)
     sc.stg.assert_free_partition()
+
+
+# ------------------------------------------------------------------ per-unit pipeline
+# amass_quad_select_attend against the separate launches (quad score, selection with the
+# fused nrm staging, the decode's one-workgroup-per-unit layout) over generated batches:
+# kv-head counts, GQA groups (odd ones included), sink and window widths, lengths from 0
+# (padded rows) to 2048 pages, top-b and coverage, both tie rules, both boosts, with and
+# without the attend in the launch.  Every output bit-identical.
+@hs.composite
+def unit_cases(draw):
+    R = draw(hs.integers(1, 6))
+    hi = draw(hs.sampled_from([16, 700, 4096, 16384, 32768]))
+    return dict(R=R, n_kv=draw(hs.sampled_from([1, 2, 4, 8])),
+                G=draw(hs.sampled_from([1, 2, 3, 4, 8])), hi=hi,
+                zero=draw(hs.booleans()), sink=draw(hs.sampled_from([0, 1, 3])),
+                window=draw(hs.sampled_from([1, 2])),
+                mode=draw(hs.sampled_from(["topb", "coverage"])),
+                tie=draw(hs.sampled_from(["index", "all"])),
+                budget=draw(hs.floats(0.01, 0.6)), cov=draw(hs.floats(0.3, 1.0)),
+                boost=draw(hs.sampled_from(["sigma", "keynorm"])),
+                attend=draw(hs.booleans()), seed=draw(hs.integers(0, 100000)))
+
+
+@PROPS
+@given(c=unit_cases())
+def test_unit_pipeline_matches_separate_launches(c):
+    from test_gpu_unit import _compare
+    announce(f"unit pipeline property case {c}")
+    case = make_case(B=c["R"], ctx=(1, c["hi"]), n_kv=c["n_kv"], G=c["G"], heavy=0.05,
+                     table="perm", boost=c["boost"], seed=c["seed"], device=DEV)
+    if c["zero"]:
+        case.seq_lens[0] = 0
+    kw = dict(coverage=c["cov"]) if c["mode"] == "coverage" else dict(budget=c["budget"])
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", sink=c["sink"],
+                          window=c["window"], **kw)
+    st.tie_mode = c["tie"]
+    _compare(case, st, attend=c["attend"])
