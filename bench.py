@@ -970,6 +970,7 @@ def main():
         "gb_s": m["gb_s"], "dense_us": m["dense_us"], "dense_gb_s": m["dense_gb_s"],
         "speedup_vs_dense": m["speedup_vs_dense"],
         "eager_us": m["eager_us"], "dense_eager_us": m["dense_eager_us"],
+        "graph10_us": m["graph10_us"], "dense_graph10_us": m["dense_graph10_us"],
         "selected_fraction": m["selected_fraction"],
         "attended_fraction": m["attended_fraction"],
         "kernels": kernels,
