@@ -199,7 +199,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     lib.amass_tier_dma.argtypes = [C.POINTER(CopyRun), C.c_int32, _P]
     lib.amass_tier_dma.restype = C.c_int
     lib.amass_quad_select_attend.argtypes = [C.POINTER(QuadScoreArgs), C.POINTER(SelectArgs),
-                                             C.POINTER(DecodeArgs), C.c_int, _P]
+                                             C.POINTER(DecodeArgs), C.c_int, _P, C.c_int, _P]
     lib.amass_quad_select_attend.restype = C.c_int
     lib.amass_host_pool_alloc.argtypes = [C.c_size_t, C.POINTER(_P), C.POINTER(_P)]
     lib.amass_host_pool_alloc.restype = C.c_int
@@ -235,12 +235,15 @@ def call(name: str, args, stream: int) -> None:
     check(getattr(lib, name)(C.byref(args), _P(stream)), name)
 
 
-def call_select_attend(score, select, decode, mode: int, stream: int) -> None:
-    """amass_quad_select_attend (decode None: score + select only)."""
+def call_select_attend(score, select, decode, mode: int, tickets, wgs_per_unit: int,
+                       stream: int) -> None:
+    """amass_quad_select_attend (decode None: score + select only; tickets: the device
+    address of the zeroed per-unit int32 tickets, or None with wgs_per_unit 1)."""
     lib = load_library()
     check(lib.amass_quad_select_attend(C.byref(score), C.byref(select),
                                        C.byref(decode) if decode is not None else None,
-                                       mode, _P(stream)), "amass_quad_select_attend")
+                                       mode, _P(tickets) if tickets else None, wgs_per_unit,
+                                       _P(stream)), "amass_quad_select_attend")
 
 
 def ptr(t) -> Optional[int]:

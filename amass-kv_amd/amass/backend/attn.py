@@ -10,7 +10,8 @@ runs the stock implementation unchanged.  A pure decode step runs
     decode_dispatch(...)  Stage B: sparse paged decode -> output (in place)
 
 (``_runtime.select_and_decode``; a quad state takes ``select_then_attend``, which runs
-both stages in one launch for rows of <= 256 pages, with the same outputs)
+small batches through the per-unit pipeline -- both stages in one launch where top-b
+bounds the kept pages -- with the same outputs)
 
 with K and V read from the resident paged cache.  ``forward`` has the reference's
 signature and returns ``output``.

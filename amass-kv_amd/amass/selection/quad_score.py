@@ -11,23 +11,37 @@ score_h once.
 """
 from __future__ import annotations
 
-import torch
-
 import math
+
+import torch
 
 from .._hip import (ClseScoreArgs, NrmArgs, QuadScoreArgs, call, call_select_attend,
                     current_stream, ptr, require_cuda)
 from .select import derive_page_params, select_args, select_pages
 
-# The per-unit pipeline (amass_quad_select_attend): the rows it serves; the rows up to
-# which select_then_attend routes a layer through it (one workgroup streams a unit's
-# summaries at ~40 GB/s, so a unit of 256 pages takes ~8 us where the score kernel's
-# balanced walk would take the launch's fixed ~7 us anyway, and a ragged batch of longer
-# rows could wait on its longest unit); the kept pages per unit up to which it also
-# attends (beyond that the decode's split layout streams faster).
+# The per-unit pipeline (amass_quad_select_attend): the rows it serves and the most
+# workgroups per unit.  select_then_attend's route, measured on MI355X against the
+# separate score / select / decode launches (graphs of 10 steps, 8 kv heads, contexts of
+# 4K-32K tokens): with the attend in the launch it is faster at every batch of 1-64
+# requests while each unit keeps <= ~55 pages, and slower from ~100 kept pages on (one
+# workgroup attends what the decode's split layout spreads over many); without the
+# attend it gains only at <= 16 units with <= 128 pages per workgroup (B <= 2), and is
+# within +-4 us, either way, elsewhere.
 UNIT_MAX_PAGES = 2048
-UNIT_ROUTE_MAX_PAGES = 256
-UNIT_ATTEND_MAX_PAGES = 32
+UNIT_MAX_WGS = 16
+UNIT_ATTEND_MAX_PAGES = 64      # kept-page bound up to which the launch attends
+UNIT_ROUTE_MAX_UNITS = 16       # without the attend: units ...
+UNIT_ROUTE_MAX_PAGES = 128      # ... and pages per workgroup up to which it is taken
+UNIT_MAX_UNITS_PER_CU = 2       # the largest batch measured: 512 units on 256 CUs
+
+_CUS = {}
+
+
+def _num_cus(device) -> int:
+    idx = torch.device(device).index or 0
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CUS[idx]
 
 
 def _tile_max(st):
@@ -175,17 +189,46 @@ def kept_pages_bound(st):
     return math.ceil(st.budget * st.max_pages) + st.sink_pages + st.window_pages + 1
 
 
+def unit_route(st, n_req: int, device, resident: bool = True):
+    """(workgroups per unit, attend in the launch) of the per-unit pipeline for this
+    batch, or None when the separate launches are the faster route.  A unit's tiles are
+    spread over as many workgroups as one resident round holds (one per CU) and the row
+    needs (8 tiles per workgroup at least).  The launch attends when top-b bounds every
+    unit's kept pages by UNIT_ATTEND_MAX_PAGES; without the attend the route is taken for
+    at most UNIT_ROUTE_MAX_UNITS units with at most UNIT_ROUTE_MAX_PAGES pages of the
+    longest possible row per workgroup.  ``resident``: V is read from the paged cache (the
+    launch attends only then)."""
+    if not unit_step_supported(st) or n_req < 1:
+        return None
+    units = n_req * st.n_kv
+    cus = _num_cus(device)
+    if units > UNIT_MAX_UNITS_PER_CU * cus:
+        return None
+    tiles = (st.max_pages + 15) // 16
+    ns = max(1, min(UNIT_MAX_WGS, cus // units, (tiles + 7) // 8))
+    bound = kept_pages_bound(st)
+    if resident and bound is not None and bound <= UNIT_ATTEND_MAX_PAGES:
+        return ns, True
+    if units <= UNIT_ROUTE_MAX_UNITS and (st.max_pages + ns - 1) // ns <= UNIT_ROUTE_MAX_PAGES:
+        return ns, False
+    return None
+
+
 def select_attend_quad(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
-                       *, kv_cache=None, out=None, vsource=None, derive: bool = False) -> None:
+                       *, kv_cache=None, out=None, vsource=None, derive: bool = False,
+                       wgs_per_unit: int = 1) -> None:
     """Stage A of one layer in one launch (amass_quad_select_attend): the quad score into
     st.score_h / st.score_tmax, the nrm combine into st.score and the top-b or coverage
     selection into st.page_table / st.page_cnt -- the outputs of select_pages_quad, bit
     for bit -- with one workgroup per (request, kv head).  With ``out`` (and ``kv_cache``,
     ``vsource``: resident V) the same workgroup then attends the kept pages into out, as
-    sparse_paged_decode_batched(path="fused") would."""
+    sparse_paged_decode_batched(path="fused") would.  ``wgs_per_unit`` workgroups score
+    each unit (the last to finish selects, counted in st.unit_tickets)."""
     if not unit_step_supported(st):
         raise ValueError("amass_quad_select_attend serves quad nrm states with r'=8 int8 "
                          f"summaries, G <= 8 and <= {UNIT_MAX_PAGES} pages per row")
+    if not 1 <= wgs_per_unit <= UNIT_MAX_WGS:
+        raise ValueError(f"wgs_per_unit must be 1..{UNIT_MAX_WGS}")
     if n_req > st.max_reqs:
         raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
     if derive:
@@ -200,24 +243,25 @@ def select_attend_quad(st, layer: int, q, block_table, seq_lens, n_req: int, sca
         k, _ = _split_kv(kv_cache)
         da = _decode_args(q, k, vsource, block_table, seq_lens, st, out, scale, n_req,
                           dense=False, path="fused")
-    call_select_attend(qa, sa, da, sa.mode, current_stream(q.device))
+    tickets = ptr(st.unit_tickets) if wgs_per_unit > 1 else None
+    call_select_attend(qa, sa, da, sa.mode, tickets, wgs_per_unit, current_stream(q.device))
 
 
 def select_then_attend(st, layer: int, q, kv_cache, block_table, seq_lens, n_req: int,
                        scale: float, out, vsource) -> None:
     """One layer's score + select + attend (quad states): through the per-unit pipeline
-    where that is the faster route -- rows of <= UNIT_ROUTE_MAX_PAGES pages; it also
-    attends when every unit keeps <= UNIT_ATTEND_MAX_PAGES pages, else the decode
-    follows -- otherwise select_pages_quad then sparse_paged_decode_batched.  The outputs
-    are the same either way, bit for bit."""
+    where unit_route finds it the faster route -- in one launch when it also attends,
+    else with the decode after it -- otherwise select_pages_quad then
+    sparse_paged_decode_batched.  The outputs are the same either way, bit for bit."""
     from ..attention.decode import sparse_paged_decode_batched
-    if unit_step_supported(st) and st.max_pages <= UNIT_ROUTE_MAX_PAGES:
-        bound = kept_pages_bound(st)
-        if bound is not None and bound <= UNIT_ATTEND_MAX_PAGES and vsource.SRC_ID == 0:
+    route = unit_route(st, n_req, q.device, resident=vsource.SRC_ID == 0)
+    if route is not None:
+        ns, attend = route
+        if attend:
             select_attend_quad(st, layer, q, block_table, seq_lens, n_req, scale,
-                               kv_cache=kv_cache, out=out, vsource=vsource)
+                               kv_cache=kv_cache, out=out, vsource=vsource, wgs_per_unit=ns)
             return
-        select_attend_quad(st, layer, q, block_table, seq_lens, n_req, scale)
+        select_attend_quad(st, layer, q, block_table, seq_lens, n_req, scale, wgs_per_unit=ns)
     else:
         select_pages_quad(st, layer, q, block_table, seq_lens, n_req, scale, derive=False)
     sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out, vsource,

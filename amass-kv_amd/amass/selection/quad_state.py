@@ -35,7 +35,8 @@ quad_resid at half 25; ``quad_sig2`` is None there.
 
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
 (R, n_kv, G, MP) and score_tmax (R, n_kv, G, ceil(MP / 16)), the per-16-page-tile
-per-head maxima the score launch writes beside score_h for the fused nrm combine.
+per-head maxima the score launch writes beside score_h for the fused nrm combine, and
+unit_tickets (R * n_kv,), the zero-at-rest counters of the per-unit pipeline.
 """
 from __future__ import annotations
 
@@ -178,8 +179,10 @@ class QuadState:
             self.score_h = torch.empty(R, n_kv, G, MP, device=device, dtype=f32)
             self.score_tmax = torch.empty(R, n_kv, G, (MP + 15) // 16, device=device,
                                           dtype=f32)
+            # the per-unit pipeline's tickets (several workgroups per unit): zero at rest
+            self.unit_tickets = torch.zeros(R * n_kv, device=device, dtype=i32)
         else:
-            self.score_h = self.score_tmax = None
+            self.score_h = self.score_tmax = self.unit_tickets = None
         self.n_pages = torch.zeros(R, device=device, dtype=i32)
         self.n_sel_hi = torch.zeros(R, device=device, dtype=i32)
         self.b_fix = torch.ones(R, device=device, dtype=i32)

@@ -19,6 +19,12 @@
 // for bit: the same instructions compute them (the decode's whole layout is what the
 // separate decode picks for such batches, and what its fused path always runs).
 //
+// One workgroup streams a unit's summaries at only ~40 GB/s, so a long row's score phase
+// is spread over `ns` workgroups per unit (wgs_per_unit): each scores every ns-th group of
+// 8 tiles, releases its stores device-wide (__threadfence) and takes a ticket; the last of
+// the unit's workgroups acquires the others' stores and runs the selection and attend.
+// The per-unit tickets are the caller's zeroed int32 array, left zero by every launch.
+//
 // Served: quad nrm states (score_h and tile maxima), r' = 8 int8 summaries, G <= 8, rows
 // of at most 2048 pages (4 per selection thread), resident V.  The host asks for the
 // attend phase only when it can bound every unit's kept pages (top-b with a small
@@ -32,26 +38,58 @@ namespace amass {
 constexpr int UN_THREADS = 512;                 // 8 waves: the selection's and decode's
 constexpr int UN_WAVES = UN_THREADS / WAVE;
 constexpr int UN_MAXP = 4 * UN_THREADS;         // pages per row: 4 per selection thread
+constexpr int UN_MAXWG = 16;                    // workgroups per unit: a 2048-page row's
+                                                // 128 tiles at one tile per wave
 
-template <int RP, int VB, int PPT, bool ATTEND>
+template <int RP, int VB, int PPT, bool ATTEND, bool MULTI>
 __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
                                                           const amass_select_args sa,
-                                                          const amass_decode_args da) {
+                                                          const amass_decode_args da,
+                                                          int ns, int32_t* tickets) {
     __shared__ QuadLds qlds;
     __shared__ XSel xs;
     __shared__ WholeLds wl;
-    const int kh = blockIdx.x, r = blockIdx.y;
+    __shared__ int last;
+    // workgroup j < ns of unit (r, kh): MULTI spreads a unit's tiles over ns workgroups
+    const int j = MULTI ? (int)blockIdx.x % ns : 0;
+    const int kh = MULTI ? (int)blockIdx.x / ns : (int)blockIdx.x, r = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-    // ---- score: the unit's tiles over the workgroup's waves ----------------------------
+    // ---- score: the unit's tiles over its workgroups' waves -----------------------------
     const int nsh = scored_of(qp.nsh, r, qp.max_pages);
     const int tiles = tiles_of(nsh);
-    if (wave < tiles)
-        quad_walk<RP, VB, true, false>(qp, qlds, wave, kh, r, nsh, wave,
-                                       (tiles - wave + UN_WAVES - 1) / UN_WAVES, UN_WAVES);
-    __syncthreads();
+    const int gw = j * UN_WAVES + wave, nw = (MULTI ? ns : 1) * UN_WAVES;
+    if (gw < tiles)
+        quad_walk<RP, VB, true, false>(qp, qlds, wave, kh, r, nsh, gw, (tiles - gw + nw - 1) / nw,
+                                       nw);
+    if constexpr (MULTI) {
+        // the unit's last workgroup to finish scoring runs its selection.  Every wave
+        // waits until its score_h / tile-max stores have reached the L2 (a vector store
+        // leaves the counter once the write-through L1 has passed it on), the barrier
+        // gathers the waves, and one thread releases the workgroup's stores device-wide
+        // (an agent-scope fence writes back the XCD's L2) before it takes the ticket; the
+        // last workgroup's thread acquires the others' (an agent-scope fence invalidates
+        // this CU's L1 and the XCD's L2) before the barrier lets its waves read.  One
+        // fence per workgroup: the L2 write-back and invalidate are whole-cache actions,
+        // too dear to repeat per wave.  The ticket returns to zero for the next launch.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            int* t = tickets + (int64_t)r * qp.n_kv + kh;
+            last = atomicAdd(t, 1) == ns - 1;
+            if (last) {
+                atomicExch(t, 0);
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            }
+        }
+        __syncthreads();
+        if (!last) return;
+    } else {
+        __syncthreads();
+    }
 
-    // ---- select (fused nrm staging over this workgroup's score_h and tile maxima) -------
+    // ---- select (fused nrm staging over the unit's score_h and tile maxima) -------------
     const int cnt = select_unit<UN_THREADS, PPT, true>(sa, r, kh, xs);
     if constexpr (ATTEND) {
         __syncthreads();
@@ -62,17 +100,33 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
     }
 }
 
+template <int PPT, bool MULTI>
+static void launch_unit_m(const QuadParams& qp, const amass_select_args& sa,
+                          const amass_decode_args& da, bool attend, int ns, int32_t* tickets,
+                          hipStream_t s) {
+    const dim3 grid(sa.n_kv * ns, sa.n_req), blk(UN_THREADS);
+    if (attend)
+        hipLaunchKernelGGL((unit_kernel<8, 8, PPT, true, MULTI>), grid, blk, 0, s, qp, sa, da, ns,
+                           tickets);
+    else
+        hipLaunchKernelGGL((unit_kernel<8, 8, PPT, false, MULTI>), grid, blk, 0, s, qp, sa, da,
+                           ns, tickets);
+}
+
 template <int PPT>
 static void launch_unit(const QuadParams& qp, const amass_select_args& sa,
-                        const amass_decode_args& da, bool attend, hipStream_t s) {
-    const dim3 grid(sa.n_kv, sa.n_req), blk(UN_THREADS);
-    if (attend) hipLaunchKernelGGL((unit_kernel<8, 8, PPT, true>), grid, blk, 0, s, qp, sa, da);
-    else hipLaunchKernelGGL((unit_kernel<8, 8, PPT, false>), grid, blk, 0, s, qp, sa, da);
+                        const amass_decode_args& da, bool attend, int ns, int32_t* tickets,
+                        hipStream_t s) {
+    if (ns > 1) launch_unit_m<PPT, true>(qp, sa, da, attend, ns, tickets, s);
+    else launch_unit_m<PPT, false>(qp, sa, da, attend, 1, nullptr, s);
 }
 
 static int unit_step(const amass_quad_score_args* q, const amass_select_args* sel,
-                     const amass_decode_args* dec, int mode, hipStream_t s) {
+                     const amass_decode_args* dec, int mode, int32_t* tickets, int ns,
+                     hipStream_t s) {
     if (!q || !sel) return AMASS_ERR_NULL;
+    if (ns < 1 || ns > UN_MAXWG) return AMASS_ERR_GEOMETRY;
+    if (ns > 1 && !tickets) return AMASS_ERR_NULL;
     // score: the nrm combine's outputs are what the selection stages
     if (!q->q || !q->rec || !q->block_table || !q->n_sel_hi || !q->score_h || !q->tile_max)
         return AMASS_ERR_NULL;
@@ -144,10 +198,11 @@ static int unit_step(const amass_quad_score_args* q, const amass_select_args* se
     int ppt = 1;
     while (ppt * UN_THREADS < p.max_pages) ppt *= 2;           // <= 4 (UN_MAXP)
     const bool attend = dec != nullptr;
+    if ((int64_t)q->n_kv * ns > 0x7FFFFFFF) return AMASS_ERR_GEOMETRY;
     switch (ppt) {
-        case 1: launch_unit<1>(p, sa, da, attend, s); break;
-        case 2: launch_unit<2>(p, sa, da, attend, s); break;
-        default: launch_unit<4>(p, sa, da, attend, s); break;
+        case 1: launch_unit<1>(p, sa, da, attend, ns, tickets, s); break;
+        case 2: launch_unit<2>(p, sa, da, attend, ns, tickets, s); break;
+        default: launch_unit<4>(p, sa, da, attend, ns, tickets, s); break;
     }
     return check_launch();
 }
@@ -159,6 +214,6 @@ using namespace amass;
 extern "C" int amass_quad_select_attend(const amass_quad_score_args* score,
                                         const amass_select_args* select,
                                         const amass_decode_args* decode, int mode,
-                                        void* stream) {
-    return unit_step(score, select, decode, mode, (hipStream_t)stream);
+                                        int32_t* tickets, int wgs_per_unit, void* stream) {
+    return unit_step(score, select, decode, mode, tickets, wgs_per_unit, (hipStream_t)stream);
 }

@@ -399,10 +399,9 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
                                         sparse_paged_decode_batched)
     from amass.selection import (derive_page_params, select_pages_clse, select_pages_quad,
                                  select_pages_r8)
-    from amass.selection.quad_score import (UNIT_ATTEND_MAX_PAGES, UNIT_ROUTE_MAX_PAGES,
-                                            clse_score, kept_pages_bound, quad_score_launch,
+    from amass.selection.quad_score import (clse_score, quad_score_launch,
                                             select_attend_quad, select_then_attend,
-                                            unit_step_supported)
+                                            unit_route)
     from amass.selection.score import r8_score
     from amass.selection.select import select_pages
 
@@ -423,10 +422,11 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
         else:
             select_pages_r8(st, 0, q, bt, sl, B, case.scale, derive=False)
 
-    # the route the backend takes (select_then_attend): one launch for short rows
-    unit = score == "quad" and unit_step_supported(st) and st.max_pages <= UNIT_ROUTE_MAX_PAGES
-    bound = kept_pages_bound(st) if unit else None
-    unit_attend = unit and bound is not None and bound <= UNIT_ATTEND_MAX_PAGES
+    # the route the backend takes (select_then_attend): the per-unit pipeline for rows
+    # that few workgroups per unit cover, in one launch when it also attends
+    route = unit_route(st, B, q.device) if score == "quad" else None
+    unit = route is not None
+    ns, unit_attend = route if unit else (1, False)
 
     def sparse_step():
         if score == "quad":
@@ -438,9 +438,9 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
     def unit_only():
         if unit_attend:
             select_attend_quad(st, 0, q, bt, sl, B, case.scale, kv_cache=kv, out=out,
-                               vsource=vsrc)
+                               vsource=vsrc, wgs_per_unit=ns)
         else:
-            select_attend_quad(st, 0, q, bt, sl, B, case.scale)
+            select_attend_quad(st, 0, q, bt, sl, B, case.scale, wgs_per_unit=ns)
 
     def dense_step():
         dense_paged_decode(q, kv, bt, sl, st, out_d, scale=case.scale)
@@ -509,8 +509,10 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
         kernels["quad_select_attend"] = kernel_entry(us_unit, b_unit,
                                                      traffic.get("quad_select_attend"),
                                                      mf.get("quad_select_attend"))
-    route = ("one launch (amass_quad_select_attend: score, select and attend)" if unit_attend
-             else "amass_quad_select_attend (score, select) + amass_sparse_decode" if unit
+    route = (f"one launch (amass_quad_select_attend: score, select and attend; {ns} "
+             f"workgroup(s) per unit)" if unit_attend
+             else f"amass_quad_select_attend (score, select; {ns} workgroup(s) per unit) + "
+                  "amass_sparse_decode" if unit
              else "separate launches: score, select, decode")
     return dict(us=round(ms_sparse * 1e3, 2), route=route,
                 gb_s=round((b_score + b_sel + b_att) / (ms_sparse * 1e-3) / 1e9, 1),

@@ -310,10 +310,16 @@ int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
  * G <= 8, max_pages <= 2048, resident V (v_src 0); other shapes return
  * AMASS_ERR_UNSUPPORTED before anything runs.  Pass `decode` only when every unit keeps
  * few pages (a unit of many pages streams faster through amass_sparse_decode's split
- * layout); with NULL the caller runs amass_sparse_decode next. */
+ * layout); with NULL the caller runs amass_sparse_decode next.  wgs_per_unit (1..16)
+ * workgroups score each unit's tiles (a long row's summaries stream faster over several
+ * CUs); above 1 the last of them to finish runs the selection and attend, counted in
+ * `tickets`, an int32 array of n_req * n_kv entries (unit r * n_kv + kh) that must be zero
+ * before the launch and that every launch leaves zero (so calls that overlap on one
+ * tickets array race); with wgs_per_unit 1 it may be NULL. */
 int amass_quad_select_attend(const amass_quad_score_args* score,
                              const amass_select_args* select,
-                             const amass_decode_args* decode, int mode, void* stream);
+                             const amass_decode_args* decode, int mode, int32_t* tickets,
+                             int wgs_per_unit, void* stream);
 
 /* ---- mem-v tier ------------------------------------------------------------------ */
 /* Replaces tier/residency.py:385-407 (gather_plan: _miss_diff_kernel +

@@ -325,3 +325,39 @@ def test_quad_states_take_the_one_launch_route(monkeypatch):
     quad.coords = "lse"
     _runtime.select_and_decode(q, kv, bt, sl, quad, out, "vs", 3, 0.088, cfg)
     assert [c[0] for c in calls] == ["select", "decode"]
+
+
+def test_unit_route_decisions(monkeypatch):
+    """select_then_attend's route on a 256-CU GPU: workgroups per unit = what one resident
+    round holds and the row needs; the attend in the launch when top-b bounds the kept
+    pages by 64; without it, at most 16 units of at most 128 pages per workgroup."""
+    import importlib
+    from amass.selection import QuadState
+    quad_score = importlib.import_module("amass.selection.quad_score")
+    monkeypatch.setattr(quad_score, "_num_cus", lambda device: 256)
+
+    def st(R, MP, budget=None, coverage=None, G=4, rank=8):
+        s = QuadState("cpu", num_layers=1, num_blocks=2, n_kv=8, G=G, head_dim=128, page=16,
+                      max_reqs=R, max_pages=MP, rank=rank, budget=budget or 0.1,
+                      combine="nrm")
+        s.coverage = coverage
+        return s
+
+    route = quad_score.unit_route
+    assert route(st(1, 256, budget=0.05), 1, "cpu") == (2, True)       # config 0
+    assert route(st(1, 256, coverage=0.95), 1, "cpu") == (2, False)
+    assert route(st(2, 1024, coverage=0.95), 2, "cpu") == (8, False)
+    assert route(st(1, 2048, budget=0.05), 1, "cpu") == (16, False)    # bound 106 > 64
+    assert route(st(8, 1024, budget=0.05), 8, "cpu") == (4, True)     # bound 55
+    assert route(st(32, 1024, budget=0.05), 32, "cpu") == (1, True)
+    assert route(st(64, 256, budget=0.05), 64, "cpu") == (1, True)    # short rows, many units
+    assert route(st(4, 1024, coverage=0.95), 4, "cpu") is None        # 32 units
+    assert route(st(16, 1024, coverage=0.95), 16, "cpu") is None
+    assert route(st(32, 1024, coverage=0.95), 32, "cpu") is None      # config 1
+    assert route(st(4, 2048, budget=0.05), 4, "cpu") is None          # bound 106, 32 units
+    assert route(st(128, 256, budget=0.05), 128, "cpu") is None       # 1024 units
+    assert route(st(1, 4096, budget=0.05), 1, "cpu") is None          # beyond 2048 pages
+    assert route(st(1, 256, budget=0.05, rank=4), 1, "cpu") is None   # r' = 8 only
+    # V not resident (the mem-v tier's sources): the launch does not attend
+    assert route(st(1, 256, budget=0.05), 1, "cpu", resident=False) == (2, False)
+    assert route(st(8, 1024, budget=0.05), 8, "cpu", resident=False) is None

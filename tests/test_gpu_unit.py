@@ -9,8 +9,10 @@ layout, path "fused", which "auto" also picks for these batches).  Cases: config
 (B = 1, 4096 tokens, top-b 5 %, the shape the pipeline is for) checked against the CPU
 oracle as well; ragged batches over the three row widths (1, 2 and 4 pages per selection
 thread: rows of 256, 1024 and 2048 pages), G = 4 and 8, top-b with both tie rules and
-coverage; the attend phase under coverage (called explicitly); graph replay equal to
-eager; shapes outside its scope refused before anything runs.
+coverage; the attend phase under coverage (called explicitly); several workgroups per
+unit (the last to finish selects, behind a per-unit ticket that every launch leaves at
+zero); graph replay equal to eager; shapes outside its scope refused before anything
+runs.
 """
 import ctypes as C
 
@@ -26,7 +28,7 @@ from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
 from amass.bench.synth import build_quad_state, config_case, make_case
 from amass.selection import derive_page_params, select_pages_quad
 from amass.selection.quad_score import (_quad_args, _tile_max, kept_pages_bound,
-                                        select_attend_quad, select_then_attend,
+                                        select_attend_quad, select_then_attend, unit_route,
                                         unit_step_supported)
 from amass.selection.select import select_args
 from helpers import announce, npf, npi
@@ -61,8 +63,9 @@ def _equal(a, b):
         assert np.array_equal(x.view(np.uint8), y.view(np.uint8))
 
 
-def _compare(case, st, *, attend):
-    """Separate launches, then the unit pipeline, from poisoned outputs: bit-identical."""
+def _compare(case, st, *, attend, wgs=1):
+    """Separate launches, then the unit pipeline (wgs workgroups per unit), from poisoned
+    outputs: bit-identical, and the per-unit tickets back at zero."""
     B = case.q.shape[0]
     H = case.n_kv * case.G
     derive_page_params(st, case.seq_lens, B)
@@ -82,12 +85,14 @@ def _compare(case, st, *, attend):
     out = torch.full_like(ref_out, float("nan"))
     if attend:
         select_attend_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
-                           kv_cache=case.kv_cache, out=out, vsource=vs)
+                           kv_cache=case.kv_cache, out=out, vsource=vs, wgs_per_unit=wgs)
     else:
-        select_attend_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale)
+        select_attend_quad(st, 0, case.q, case.block_table, case.seq_lens, B, case.scale,
+                           wgs_per_unit=wgs)
         sparse_paged_decode_batched(case.q, case.kv_cache, case.block_table, case.seq_lens,
                                     st, out, vs, scale=case.scale, path="fused")
     torch.cuda.synchronize()
+    assert not st.unit_tickets.any()
     _equal(_outputs(st, B), ref)
     assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
     return out, auto_out
@@ -98,6 +103,7 @@ def test_config0_one_launch_matches_separate_and_oracle():
     case = config_case(0, seed=0, device=DEV)
     st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", budget=0.05)
     assert unit_step_supported(st) and kept_pages_bound(st) <= 32
+    assert unit_route(st, 1, DEV) == (2, True)
     out, auto_out = _compare(case, st, attend=True)
     # "auto" picks the same one-workgroup-per-unit layout for this batch
     assert torch.equal(out.view(torch.int16), auto_out.view(torch.int16))
@@ -158,9 +164,29 @@ def test_short_and_padded_rows_match_separate(mode):
     assert int(st.page_cnt[0].max()) == 0          # the padded row keeps nothing
 
 
+@pytest.mark.parametrize("B,hi,G,mode,tie,wgs", [
+    (1, 4096, 4, "topb", "index", 2),      # config 0's shape, two workgroups per unit
+    (2, 16384, 4, "coverage", "index", 8),
+    (3, 32768, 8, "topb", "all", 16),
+    (4, 32768, 4, "coverage", "index", 5),  # tiles not a multiple of the waves
+])
+def test_multi_workgroup_units_match_separate(B, hi, G, mode, tie, wgs):
+    """Several workgroups per unit (the last to finish selects and attends): the same bits
+    as the separate launches, the tickets back at zero, twice in a row."""
+    announce(f"unit pipeline: {wgs} workgroups per unit, B={B} ctx<={hi} G={G} {mode}")
+    case = make_case(B=B, ctx=(64, hi), n_kv=8, G=G, heavy=0.05, table="perm", seed=40 + B,
+                     device=DEV)
+    kw = dict(coverage=0.95) if mode == "coverage" else dict(budget=0.05)
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", **kw)
+    st.tie_mode = tie
+    for attend in (False, True, True):
+        _compare(case, st, attend=attend, wgs=wgs)
+
+
 def test_runtime_route_and_graph_replay():
     """select_then_attend (the route the backend and the bench take) picks the one-launch
-    pipeline for config 0; its graph replays equal the eager result."""
+    pipeline for config 0 (two workgroups per unit); its graph replays equal the eager
+    result and leave the tickets at zero."""
     announce("unit pipeline: select_then_attend in a HIP graph")
     case = config_case(0, seed=3, device=DEV)
     st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", budget=0.05)
@@ -193,6 +219,7 @@ def test_runtime_route_and_graph_replay():
         torch.cuda.synchronize()
         for x, e in zip(outs, eager):
             assert torch.equal(x, e), f"replay {i}"
+        assert not st.unit_tickets.any()
 
 
 def test_out_of_scope_shapes_are_refused():
@@ -208,7 +235,7 @@ def test_out_of_scope_shapes_are_refused():
     sa = select_args(st, 1, score_h=st.score_h, tile_max=_tile_max(st))
     st.page_cnt.fill_(-7)
     lib = _hip.load_library()
-    rc = lib.amass_quad_select_attend(C.byref(qa), C.byref(sa), None, 0,
+    rc = lib.amass_quad_select_attend(C.byref(qa), C.byref(sa), None, 0, None, 1,
                                       C.c_void_p(_hip.current_stream()))
     torch.cuda.synchronize()
     assert rc == -3 and int(st.page_cnt.min()) == -7
