@@ -307,6 +307,33 @@ __device__ __forceinline__ unsigned long long mass_q(float score, float smax, in
     return (unsigned long long)(__fmul_rn(w, 4294967296.0f));
 }
 
+// ---------------------------------------------------------------- cross-workgroup tickets
+// Whether this workgroup is the last of `n` to arrive at the int32 ticket *t (every thread
+// gets the answer; call it from every thread of the workgroup).  Every wave first waits
+// until its global stores have reached the L2 (a vector store leaves the counter once the
+// write-through L1 has passed it on), the barrier gathers the waves, and thread 0 releases
+// the workgroup's stores device-wide (an agent-scope fence: a write-back of the XCD's L2)
+// before it takes the ticket.  The last arrival resets the ticket to zero, so every launch
+// leaves it as it found it, and acquires the other workgroups' stores (an agent-scope
+// fence: an invalidate of this CU's L1 and the XCD's L2) before the barrier lets its waves
+// read them.  One fence per workgroup, not per wave: the L2 write-back and invalidate are
+// whole-cache actions.  No workgroup ever waits for another.
+__device__ __forceinline__ bool last_arrival(int32_t* t, int n) {
+    __shared__ int last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        last = atomicAdd(t, 1) == n - 1;
+        if (last) {
+            atomicExch(t, 0);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+    }
+    __syncthreads();
+    return last;
+}
+
 }  // namespace amass
 
 // status bookkeeping shared by the host wrappers

@@ -21,8 +21,9 @@
 //
 // One workgroup streams a unit's summaries at only ~40 GB/s, so a long row's score phase
 // is spread over `ns` workgroups per unit (wgs_per_unit): each scores every ns-th group of
-// 8 tiles, releases its stores device-wide (__threadfence) and takes a ticket; the last of
-// the unit's workgroups acquires the others' stores and runs the selection and attend.
+// 8 tiles, releases its stores device-wide (one agent-scope fence per workgroup) and
+// takes a ticket; the last of the unit's workgroups acquires the others' stores and runs
+// the selection and attend.
 // The per-unit tickets are the caller's zeroed int32 array, left zero by every launch.
 //
 // Served: quad nrm states (score_h and tile maxima), r' = 8 int8 summaries, G <= 8, rows
@@ -49,7 +50,6 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
     __shared__ QuadLds qlds;
     __shared__ XSel xs;
     __shared__ WholeLds wl;
-    __shared__ int last;
     // workgroup j < ns of unit (r, kh): MULTI spreads a unit's tiles over ns workgroups
     const int j = MULTI ? (int)blockIdx.x % ns : 0;
     const int kh = MULTI ? (int)blockIdx.x / ns : (int)blockIdx.x, r = blockIdx.y;
@@ -63,28 +63,9 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
         quad_walk<RP, VB, true, false>(qp, qlds, wave, kh, r, nsh, gw, (tiles - gw + nw - 1) / nw,
                                        nw);
     if constexpr (MULTI) {
-        // the unit's last workgroup to finish scoring runs its selection.  Every wave
-        // waits until its score_h / tile-max stores have reached the L2 (a vector store
-        // leaves the counter once the write-through L1 has passed it on), the barrier
-        // gathers the waves, and one thread releases the workgroup's stores device-wide
-        // (an agent-scope fence writes back the XCD's L2) before it takes the ticket; the
-        // last workgroup's thread acquires the others' (an agent-scope fence invalidates
-        // this CU's L1 and the XCD's L2) before the barrier lets its waves read.  One
-        // fence per workgroup: the L2 write-back and invalidate are whole-cache actions,
-        // too dear to repeat per wave.  The ticket returns to zero for the next launch.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-            int* t = tickets + (int64_t)r * qp.n_kv + kh;
-            last = atomicAdd(t, 1) == ns - 1;
-            if (last) {
-                atomicExch(t, 0);
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            }
-        }
-        __syncthreads();
-        if (!last) return;
+        // the unit's last workgroup to finish scoring runs its selection (the ticket
+        // returns to zero for the next launch)
+        if (!last_arrival(tickets + (int64_t)r * qp.n_kv + kh, ns)) return;
     } else {
         __syncthreads();
     }
