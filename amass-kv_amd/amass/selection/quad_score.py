@@ -22,16 +22,19 @@ from .select import derive_page_params, select_args, select_pages
 # The per-unit pipeline (amass_quad_select_attend): the rows it serves and the most
 # workgroups per unit.  select_then_attend's route, measured on MI355X against the
 # separate score / select / decode launches (graphs of 10 steps, 8 kv heads, contexts of
-# 4K-32K tokens): with the attend in the launch it is faster at every batch of 1-64
-# requests while each unit keeps <= ~55 pages, and slower from ~100 kept pages on (one
+# 4K-32K tokens, uniform and ragged batches, the device's balanced plan): with the attend
+# in the launch it is faster at batches of 1-64 requests while each unit keeps <= ~55
+# pages (at a single request only up to ~32), and slower from ~100 kept pages on (one
 # workgroup attends what the decode's split layout spreads over many); without the
-# attend it gains only at <= 16 units with <= 128 pages per workgroup (B <= 2), and is
-# within +-4 us, either way, elsewhere.
+# attend it gains only at <= 16 units (B <= 2) with rows of <= 1024 pages, and is within
+# +-4 us either way elsewhere.
 UNIT_MAX_PAGES = 2048
 UNIT_MAX_WGS = 16
-UNIT_ATTEND_MAX_PAGES = 64      # kept-page bound up to which the launch attends
+UNIT_ATTEND_MAX_PAGES = 64      # kept-page bound up to which the launch attends ...
+UNIT_ATTEND_FEW_UNITS = 16      # ... at this many units or more,
+UNIT_ATTEND_MAX_PAGES_FEW = 32  # ... and up to which below it
 UNIT_ROUTE_MAX_UNITS = 16       # without the attend: units ...
-UNIT_ROUTE_MAX_PAGES = 128      # ... and pages per workgroup up to which it is taken
+UNIT_ROUTE_MAX_PAGES = 1024     # ... and row width up to which it is taken
 UNIT_MAX_UNITS_PER_CU = 2       # the largest batch measured: 512 units on 256 CUs
 
 _CUS = {}
@@ -191,25 +194,30 @@ def kept_pages_bound(st):
 
 def unit_route(st, n_req: int, device, resident: bool = True):
     """(workgroups per unit, attend in the launch) of the per-unit pipeline for this
-    batch, or None when the separate launches are the faster route.  A unit's tiles are
-    spread over as many workgroups as one resident round holds (one per CU) and the row
-    needs (8 tiles per workgroup at least).  The launch attends when top-b bounds every
-    unit's kept pages by UNIT_ATTEND_MAX_PAGES; without the attend the route is taken for
-    at most UNIT_ROUTE_MAX_UNITS units with at most UNIT_ROUTE_MAX_PAGES pages of the
-    longest possible row per workgroup.  ``resident``: V is read from the paged cache (the
-    launch attends only then)."""
+    batch, or None when the separate launches are the faster route.  The workgroups per
+    unit are the device's balanced plan (0: each workgroup about one CU's share of the
+    batch's tiles, so the long rows of a ragged batch take more), or for one request a
+    count from the row width.  The launch attends when
+    top-b bounds every unit's kept pages by UNIT_ATTEND_MAX_PAGES (UNIT_ATTEND_MAX_PAGES_FEW
+    below UNIT_ATTEND_FEW_UNITS units) and V is resident (``resident``); without the
+    attend the route is taken for at most UNIT_ROUTE_MAX_UNITS units with rows of at most
+    UNIT_ROUTE_MAX_PAGES pages."""
     if not unit_step_supported(st) or n_req < 1:
         return None
     units = n_req * st.n_kv
     cus = _num_cus(device)
     if units > UNIT_MAX_UNITS_PER_CU * cus:
         return None
-    tiles = (st.max_pages + 15) // 16
-    ns = max(1, min(UNIT_MAX_WGS, cus // units, (tiles + 7) // 8))
+    # one request cannot be ragged: its count from the row width (a tile per wave at
+    # least), without the plan's prologue
+    ns = 0 if n_req > 1 else max(1, min(UNIT_MAX_WGS, cus // units,
+                                        ((st.max_pages + 15) // 16 + 7) // 8))
     bound = kept_pages_bound(st)
-    if resident and bound is not None and bound <= UNIT_ATTEND_MAX_PAGES:
+    limit = (UNIT_ATTEND_MAX_PAGES if units >= UNIT_ATTEND_FEW_UNITS
+             else UNIT_ATTEND_MAX_PAGES_FEW)
+    if resident and bound is not None and bound <= limit:
         return ns, True
-    if units <= UNIT_ROUTE_MAX_UNITS and (st.max_pages + ns - 1) // ns <= UNIT_ROUTE_MAX_PAGES:
+    if units <= UNIT_ROUTE_MAX_UNITS and st.max_pages <= UNIT_ROUTE_MAX_PAGES:
         return ns, False
     return None
 
@@ -223,12 +231,13 @@ def select_attend_quad(st, layer: int, q, block_table, seq_lens, n_req: int, sca
     for bit -- with one workgroup per (request, kv head).  With ``out`` (and ``kv_cache``,
     ``vsource``: resident V) the same workgroup then attends the kept pages into out, as
     sparse_paged_decode_batched(path="fused") would.  ``wgs_per_unit`` workgroups score
-    each unit (the last to finish selects, counted in st.unit_tickets)."""
+    each unit, or with 0 as many as the device's balanced plan gives each request (the
+    last of a unit's workgroups to finish selects, counted in st.unit_tickets)."""
     if not unit_step_supported(st):
         raise ValueError("amass_quad_select_attend serves quad nrm states with r'=8 int8 "
                          f"summaries, G <= 8 and <= {UNIT_MAX_PAGES} pages per row")
-    if not 1 <= wgs_per_unit <= UNIT_MAX_WGS:
-        raise ValueError(f"wgs_per_unit must be 1..{UNIT_MAX_WGS}")
+    if not 0 <= wgs_per_unit <= UNIT_MAX_WGS:
+        raise ValueError(f"wgs_per_unit must be 0 (balanced) or 1..{UNIT_MAX_WGS}")
     if n_req > st.max_reqs:
         raise ValueError(f"n_req {n_req} exceeds max_reqs {st.max_reqs}")
     if derive:
@@ -243,7 +252,7 @@ def select_attend_quad(st, layer: int, q, block_table, seq_lens, n_req: int, sca
         k, _ = _split_kv(kv_cache)
         da = _decode_args(q, k, vsource, block_table, seq_lens, st, out, scale, n_req,
                           dense=False, path="fused")
-    tickets = ptr(st.unit_tickets) if wgs_per_unit > 1 else None
+    tickets = ptr(st.unit_tickets) if wgs_per_unit != 1 else None
     call_select_attend(qa, sa, da, sa.mode, tickets, wgs_per_unit, current_stream(q.device))
 
 

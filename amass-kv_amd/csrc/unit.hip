@@ -20,10 +20,11 @@
 // separate decode picks for such batches, and what its fused path always runs).
 //
 // One workgroup streams a unit's summaries at only ~40 GB/s, so a long row's score phase
-// is spread over `ns` workgroups per unit (wgs_per_unit): each scores every ns-th group of
-// 8 tiles, releases its stores device-wide (one agent-scope fence per workgroup) and
-// takes a ticket; the last of the unit's workgroups acquires the others' stores and runs
-// the selection and attend.
+// is spread over several workgroups per unit: each scores every c-th group of 8 tiles,
+// releases its stores device-wide (one agent-scope fence per workgroup) and takes a
+// ticket; the last of the unit's workgroups acquires the others' stores and runs the
+// selection and attend.  c is the caller's wgs_per_unit, or (0) the balanced plan's
+// count per request, which spreads a ragged batch's long rows over more workgroups.
 // The per-unit tickets are the caller's zeroed int32 array, left zero by every launch.
 //
 // Served: quad nrm states (score_h and tile maxima), r' = 8 int8 summaries, G <= 8, rows
@@ -42,30 +43,113 @@ constexpr int UN_MAXP = 4 * UN_THREADS;         // pages per row: 4 per selectio
 constexpr int UN_MAXWG = 16;                    // workgroups per unit: a 2048-page row's
                                                 // 128 tiles at one tile per wave
 
-template <int RP, int VB, int PPT, bool ATTEND, bool MULTI>
+// ---- the balanced plan (wgs_per_unit 0) ----------------------------------------------
+// Request r's n_kv units take c_r = max(1, ceil(T_r / tpw)) workgroups each, T_r the tiles
+// of its scored pages.  First choice: tpw = max(8, ceil(n_kv sum T / target)), about one
+// resident round's share of the batch's tiles per workgroup (at least a tile per wave):
+// a uniform batch then takes one round, and in a ragged one the long rows' units take
+// many workgroups and the short ones one each.  That may exceed a round; it is kept
+// while the excess is at most a quarter round (those workgroups start where short units
+// finish), since each late workgroup adds its unit's selection and attend to the step's
+// tail.  Otherwise tpw is the smallest count whose total fits one round, or the longest
+// row's tiles (one workgroup per unit) when none does.  Every wave computes the plan from
+// n_sel_hi -- the same numbers in every workgroup, so the units' ticket counts agree --
+// and workgroup x takes the x-th (request, kv head, j) in request-major order; the plan
+// takes at most target + units workgroups.
+struct UnitPlan {
+    int r, kh, j, c;     // unit (r, kh); workgroup j of its c
+};
+
+__device__ __forceinline__ int unit_wgs(int t, int tpw) { return max(1, (t + tpw - 1) / tpw); }
+
+// workgroups of the whole batch at tpw (every lane gets the sum); t0 = lane_tiles(0)
+__device__ __forceinline__ int plan_wgs(const QuadParams& qp, int t0, int tpw) {
+    const int lane = threadIdx.x & 63;
+    int tot = wave_sum_uniform(lane < qp.n_req ? unit_wgs(t0, tpw) : 0);
+    for (int base = WAVE; base < qp.n_req; base += WAVE)
+        tot += wave_sum_uniform(base + lane < qp.n_req
+                                    ? unit_wgs(lane_tiles(qp.nsh, qp.n_req, qp.max_pages, base),
+                                               tpw)
+                                    : 0);
+    return tot * qp.n_kv;
+}
+
+__device__ __forceinline__ bool unit_plan(const QuadParams& qp, int target, int x, UnitPlan& u) {
+    const int lane = threadIdx.x & 63;
+    const int t0 = lane_tiles(qp.nsh, qp.n_req, qp.max_pages, 0);
+    int total = wave_sum_uniform(t0), tmax = wave_max_uniform(t0);
+    for (int base = WAVE; base < qp.n_req; base += WAVE) {
+        const int t = lane_tiles(qp.nsh, qp.n_req, qp.max_pages, base);
+        total += wave_sum_uniform(t);
+        tmax = max(tmax, wave_max_uniform(t));
+    }
+    const int64_t unit_tiles = (int64_t)total * qp.n_kv;
+    int tpw = (int)max((int64_t)UN_WAVES, (unit_tiles + target - 1) / target);
+    if (plan_wgs(qp, t0, tpw) > target + target / 4) {
+        int a = tpw + 1, b = max(tpw + 1, tmax);     // at tmax every unit takes one
+        while (a < b) {
+            const int mid = (a + b) >> 1;
+            if (plan_wgs(qp, t0, mid) <= target) b = mid;
+            else a = mid + 1;
+        }
+        tpw = a;
+    }
+    int before = 0;                                  // workgroups of earlier requests
+    for (int base = 0; base < qp.n_req; base += WAVE) {
+        const int t = base == 0 ? t0 : lane_tiles(qp.nsh, qp.n_req, qp.max_pages, base);
+        const int c = base + lane < qp.n_req ? unit_wgs(t, tpw) : 0;
+        const int n = c * qp.n_kv;
+        const int incl = wave_incl_scan(n);
+        const int in_batch = __builtin_amdgcn_readlane(incl, WAVE - 1);
+        if (x < before + in_batch) {
+            const unsigned long long hit = __ballot(before + incl > x);
+            const int src = __ffsll((long long)hit) - 1;
+            const int cs = __builtin_amdgcn_readlane(c, src);
+            const int off = x - before - __builtin_amdgcn_readlane(incl - n, src);
+            u.r = base + src;
+            u.c = cs;
+            u.kh = off / cs;
+            u.j = off - u.kh * cs;
+            return true;
+        }
+        before += in_batch;
+    }
+    return false;
+}
+
+// ns > 0: ns workgroups per unit, grid (n_kv * ns, n_req); ns == 0: the balanced plan,
+// grid (target + units).  A unit of c > 1 workgroups hands over behind its ticket.
+template <int RP, int VB, int PPT, bool ATTEND>
 __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
                                                           const amass_select_args sa,
                                                           const amass_decode_args da,
-                                                          int ns, int32_t* tickets) {
+                                                          int ns, int target, int32_t* tickets) {
     __shared__ QuadLds qlds;
     __shared__ XSel xs;
     __shared__ WholeLds wl;
-    // workgroup j < ns of unit (r, kh): MULTI spreads a unit's tiles over ns workgroups
-    const int j = MULTI ? (int)blockIdx.x % ns : 0;
-    const int kh = MULTI ? (int)blockIdx.x / ns : (int)blockIdx.x, r = blockIdx.y;
+    UnitPlan u;
+    if (ns > 0) {
+        u.c = ns;
+        u.j = (int)blockIdx.x % ns;
+        u.kh = (int)blockIdx.x / ns;
+        u.r = blockIdx.y;
+    } else if (!unit_plan(qp, target, blockIdx.x, u)) {
+        return;                                      // past the plan's workgroups
+    }
+    const int kh = u.kh, r = u.r;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
     // ---- score: the unit's tiles over its workgroups' waves -----------------------------
     const int nsh = scored_of(qp.nsh, r, qp.max_pages);
     const int tiles = tiles_of(nsh);
-    const int gw = j * UN_WAVES + wave, nw = (MULTI ? ns : 1) * UN_WAVES;
+    const int gw = u.j * UN_WAVES + wave, nw = u.c * UN_WAVES;
     if (gw < tiles)
         quad_walk<RP, VB, true, false>(qp, qlds, wave, kh, r, nsh, gw, (tiles - gw + nw - 1) / nw,
                                        nw);
-    if constexpr (MULTI) {
+    if (u.c > 1) {
         // the unit's last workgroup to finish scoring runs its selection (the ticket
         // returns to zero for the next launch)
-        if (!last_arrival(tickets + (int64_t)r * qp.n_kv + kh, ns)) return;
+        if (!last_arrival(tickets + (int64_t)r * qp.n_kv + kh, u.c)) return;
     } else {
         __syncthreads();
     }
@@ -81,33 +165,46 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
     }
 }
 
-template <int PPT, bool MULTI>
-static void launch_unit_m(const QuadParams& qp, const amass_select_args& sa,
-                          const amass_decode_args& da, bool attend, int ns, int32_t* tickets,
-                          hipStream_t s) {
-    const dim3 grid(sa.n_kv * ns, sa.n_req), blk(UN_THREADS);
-    if (attend)
-        hipLaunchKernelGGL((unit_kernel<8, 8, PPT, true, MULTI>), grid, blk, 0, s, qp, sa, da, ns,
-                           tickets);
-    else
-        hipLaunchKernelGGL((unit_kernel<8, 8, PPT, false, MULTI>), grid, blk, 0, s, qp, sa, da,
-                           ns, tickets);
+// One resident round of the kernel's workgroups: one per CU (178 VGPRs, 8 waves).
+static int unit_target() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n < 1)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
 }
 
 template <int PPT>
 static void launch_unit(const QuadParams& qp, const amass_select_args& sa,
                         const amass_decode_args& da, bool attend, int ns, int32_t* tickets,
                         hipStream_t s) {
-    if (ns > 1) launch_unit_m<PPT, true>(qp, sa, da, attend, ns, tickets, s);
-    else launch_unit_m<PPT, false>(qp, sa, da, attend, 1, nullptr, s);
+    const int target = unit_target();
+    const int units = sa.n_kv * sa.n_req;
+    // a batch of at least a round of units gives each unit one workgroup in any plan:
+    // skip the plan's prologue
+    if (ns == 0 && units >= target) ns = 1;
+    const dim3 grid = ns > 0 ? dim3(sa.n_kv * ns, sa.n_req) : dim3(target + units, 1);
+    const dim3 blk(UN_THREADS);
+    if (attend)
+        hipLaunchKernelGGL((unit_kernel<8, 8, PPT, true>), grid, blk, 0, s, qp, sa, da, ns,
+                           target, tickets);
+    else
+        hipLaunchKernelGGL((unit_kernel<8, 8, PPT, false>), grid, blk, 0, s, qp, sa, da, ns,
+                           target, tickets);
 }
 
 static int unit_step(const amass_quad_score_args* q, const amass_select_args* sel,
                      const amass_decode_args* dec, int mode, int32_t* tickets, int ns,
                      hipStream_t s) {
     if (!q || !sel) return AMASS_ERR_NULL;
-    if (ns < 1 || ns > UN_MAXWG) return AMASS_ERR_GEOMETRY;
-    if (ns > 1 && !tickets) return AMASS_ERR_NULL;
+    if (ns < 0 || ns > UN_MAXWG) return AMASS_ERR_GEOMETRY;
+    if (ns != 1 && !tickets) return AMASS_ERR_NULL;
     // score: the nrm combine's outputs are what the selection stages
     if (!q->q || !q->rec || !q->block_table || !q->n_sel_hi || !q->score_h || !q->tile_max)
         return AMASS_ERR_NULL;
@@ -179,7 +276,7 @@ static int unit_step(const amass_quad_score_args* q, const amass_select_args* se
     int ppt = 1;
     while (ppt * UN_THREADS < p.max_pages) ppt *= 2;           // <= 4 (UN_MAXP)
     const bool attend = dec != nullptr;
-    if ((int64_t)q->n_kv * ns > 0x7FFFFFFF) return AMASS_ERR_GEOMETRY;
+    if ((int64_t)q->n_kv * q->n_req > 0x7FFFFFFF / UN_MAXWG) return AMASS_ERR_GEOMETRY;
     switch (ppt) {
         case 1: launch_unit<1>(p, sa, da, attend, ns, tickets, s); break;
         case 2: launch_unit<2>(p, sa, da, attend, ns, tickets, s); break;

@@ -509,11 +509,11 @@ def measure_step(case, st, args, *, score="quad", name="config1"):
         kernels["quad_select_attend"] = kernel_entry(us_unit, b_unit,
                                                      traffic.get("quad_select_attend"),
                                                      mf.get("quad_select_attend"))
-    route = (f"one launch (amass_quad_select_attend: score, select and attend; {ns} "
-             f"workgroup(s) per unit)" if unit_attend
-             else f"amass_quad_select_attend (score, select; {ns} workgroup(s) per unit) + "
-                  "amass_sparse_decode" if unit
-             else "separate launches: score, select, decode")
+    wgs = "the balanced plan's workgroups per unit" if ns == 0 else f"{ns} workgroup(s) per unit"
+    route = (f"one launch (amass_quad_select_attend: score, select and attend; {wgs})"
+             if unit_attend
+             else f"amass_quad_select_attend (score, select; {wgs}) + amass_sparse_decode"
+             if unit else "separate launches: score, select, decode")
     return dict(us=round(ms_sparse * 1e3, 2), route=route,
                 gb_s=round((b_score + b_sel + b_att) / (ms_sparse * 1e-3) / 1e9, 1),
                 dense_us=round(ms_dense * 1e3, 2),

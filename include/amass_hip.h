@@ -312,10 +312,13 @@ int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
  * few pages (a unit of many pages streams faster through amass_sparse_decode's split
  * layout); with NULL the caller runs amass_sparse_decode next.  wgs_per_unit (1..16)
  * workgroups score each unit's tiles (a long row's summaries stream faster over several
- * CUs); above 1 the last of them to finish runs the selection and attend, counted in
- * `tickets`, an int32 array of n_req * n_kv entries (unit r * n_kv + kh) that must be zero
- * before the launch and that every launch leaves zero (so calls that overlap on one
- * tickets array race); with wgs_per_unit 1 it may be NULL. */
+ * CUs); 0 lets the device plan it per request from n_sel_hi (each workgroup about one
+ * CU's share of the batch's tiles, so a ragged batch's long rows take more workgroups
+ * than its short ones).  A unit of several workgroups is selected and attended by the last of them to
+ * finish, counted in `tickets`, an int32 array of n_req * n_kv entries (unit
+ * r * n_kv + kh) that must be zero before the launch and that every launch leaves zero
+ * (so calls that overlap on one tickets array race); with wgs_per_unit 1 it may be
+ * NULL. */
 int amass_quad_select_attend(const amass_quad_score_args* score,
                              const amass_select_args* select,
                              const amass_decode_args* decode, int mode, int32_t* tickets,

@@ -328,9 +328,11 @@ def test_quad_states_take_the_one_launch_route(monkeypatch):
 
 
 def test_unit_route_decisions(monkeypatch):
-    """select_then_attend's route on a 256-CU GPU: workgroups per unit = what one resident
-    round holds and the row needs; the attend in the launch when top-b bounds the kept
-    pages by 64; without it, at most 16 units of at most 128 pages per workgroup."""
+    """select_then_attend's route on a 256-CU GPU: the balanced plan (0; at one request a
+    count from the row width); the attend in
+    the launch when top-b bounds the kept pages by 64 (by 32 below 16 units) and V is
+    resident; without it, at most 16 units with rows of at most 1024 pages; at most 512
+    units."""
     import importlib
     from amass.selection import QuadState
     quad_score = importlib.import_module("amass.selection.quad_score")
@@ -344,20 +346,21 @@ def test_unit_route_decisions(monkeypatch):
         return s
 
     route = quad_score.unit_route
-    assert route(st(1, 256, budget=0.05), 1, "cpu") == (2, True)       # config 0
-    assert route(st(1, 256, coverage=0.95), 1, "cpu") == (2, False)
-    assert route(st(2, 1024, coverage=0.95), 2, "cpu") == (8, False)
-    assert route(st(1, 2048, budget=0.05), 1, "cpu") == (16, False)    # bound 106 > 64
-    assert route(st(8, 1024, budget=0.05), 8, "cpu") == (4, True)     # bound 55
-    assert route(st(32, 1024, budget=0.05), 32, "cpu") == (1, True)
-    assert route(st(64, 256, budget=0.05), 64, "cpu") == (1, True)    # short rows, many units
-    assert route(st(4, 1024, coverage=0.95), 4, "cpu") is None        # 32 units
-    assert route(st(16, 1024, coverage=0.95), 16, "cpu") is None
-    assert route(st(32, 1024, coverage=0.95), 32, "cpu") is None      # config 1
-    assert route(st(4, 2048, budget=0.05), 4, "cpu") is None          # bound 106, 32 units
-    assert route(st(128, 256, budget=0.05), 128, "cpu") is None       # 1024 units
-    assert route(st(1, 4096, budget=0.05), 1, "cpu") is None          # beyond 2048 pages
-    assert route(st(1, 256, budget=0.05, rank=4), 1, "cpu") is None   # r' = 8 only
+    assert route(st(1, 256, budget=0.05), 1, "cpu") == (2, True)       # config 0: bound 16
+    assert route(st(1, 256, coverage=0.95), 1, "cpu") == (2, False)    # B = 1: from the row
+    assert route(st(1, 1024, budget=0.05), 1, "cpu") == (8, False)     # bound 55, 8 units
+    assert route(st(2, 1024, budget=0.05), 2, "cpu") == (0, True)      # bound 55, 16 units
+    assert route(st(2, 1024, coverage=0.95), 2, "cpu") == (0, False)
+    assert route(st(2, 2048, coverage=0.95), 2, "cpu") is None         # rows of 2048 pages
+    assert route(st(8, 1024, budget=0.05), 8, "cpu") == (0, True)
+    assert route(st(32, 1024, budget=0.05), 32, "cpu") == (0, True)
+    assert route(st(64, 256, budget=0.05), 64, "cpu") == (0, True)     # 512 units
+    assert route(st(4, 1024, coverage=0.95), 4, "cpu") is None         # 32 units
+    assert route(st(32, 1024, coverage=0.95), 32, "cpu") is None       # config 1
+    assert route(st(4, 2048, budget=0.05), 4, "cpu") is None           # bound 106
+    assert route(st(128, 256, budget=0.05), 128, "cpu") is None        # 1024 units
+    assert route(st(1, 4096, budget=0.05), 1, "cpu") is None           # beyond 2048 pages
+    assert route(st(1, 256, budget=0.05, rank=4), 1, "cpu") is None    # r' = 8 only
     # V not resident (the mem-v tier's sources): the launch does not attend
     assert route(st(1, 256, budget=0.05), 1, "cpu", resident=False) == (2, False)
     assert route(st(8, 1024, budget=0.05), 8, "cpu", resident=False) is None

@@ -489,8 +489,8 @@ def test_write_path_matches_oracle_on_generated_schedules(c):
 # fused nrm staging, the decode's one-workgroup-per-unit layout) over generated batches:
 # kv-head counts, GQA groups (odd ones included), sink and window widths, lengths from 0
 # (padded rows) to 2048 pages, top-b and coverage, both tie rules, both boosts, with and
-# without the attend in the launch, 1 to 16 workgroups per unit.  Every output
-# bit-identical, the tickets back at zero.
+# without the attend in the launch, 1 to 16 workgroups per unit or the balanced plan.
+# Every output bit-identical, the tickets back at zero.
 @hs.composite
 def unit_cases(draw):
     R = draw(hs.integers(1, 6))
@@ -503,7 +503,7 @@ def unit_cases(draw):
                 tie=draw(hs.sampled_from(["index", "all"])),
                 budget=draw(hs.floats(0.01, 0.6)), cov=draw(hs.floats(0.3, 1.0)),
                 boost=draw(hs.sampled_from(["sigma", "keynorm"])),
-                attend=draw(hs.booleans()), wgs=draw(hs.sampled_from([1, 2, 5, 16])),
+                attend=draw(hs.booleans()), wgs=draw(hs.sampled_from([0, 1, 2, 5, 16])),
                 seed=draw(hs.integers(0, 100000)))
 
 

@@ -169,10 +169,15 @@ def test_short_and_padded_rows_match_separate(mode):
     (2, 16384, 4, "coverage", "index", 8),
     (3, 32768, 8, "topb", "all", 16),
     (4, 32768, 4, "coverage", "index", 5),  # tiles not a multiple of the waves
+    (1, 4096, 4, "topb", "index", 0),       # the balanced plan: 2 workgroups per unit
+    (3, 32768, 8, "coverage", "all", 0),
+    (8, 16384, 4, "topb", "index", 0),
+    (40, 2048, 4, "coverage", "index", 0),  # 320 units > 256 CUs: one workgroup each
 ])
 def test_multi_workgroup_units_match_separate(B, hi, G, mode, tie, wgs):
-    """Several workgroups per unit (the last to finish selects and attends): the same bits
-    as the separate launches, the tickets back at zero, twice in a row."""
+    """Several workgroups per unit (the last to finish selects and attends; wgs 0: the
+    device's balanced plan): the same bits as the separate launches, the tickets back at
+    zero, twice in a row."""
     announce(f"unit pipeline: {wgs} workgroups per unit, B={B} ctx<={hi} G={G} {mode}")
     case = make_case(B=B, ctx=(64, hi), n_kv=8, G=G, heavy=0.05, table="perm", seed=40 + B,
                      device=DEV)
@@ -183,10 +188,31 @@ def test_multi_workgroup_units_match_separate(B, hi, G, mode, tie, wgs):
         _compare(case, st, attend=attend, wgs=wgs)
 
 
+@pytest.mark.parametrize("B,long_rows,hi,lo,mode", [
+    (8, 1, 16384, 1024, "topb"),      # one long row: its units take most workgroups
+    (32, 1, 16384, 1024, "coverage"),
+    (32, 16, 16384, 1024, "topb"),
+    (5, 2, 32768, 0, "coverage"),     # padded rows (length 0) among long ones
+])
+def test_balanced_plan_ragged_batches(B, long_rows, hi, lo, mode):
+    """The balanced plan on ragged batches (long rows among short or empty ones): the same
+    bits as the separate launches, with and without the attend, the tickets at zero."""
+    announce(f"unit pipeline balanced plan: B={B} {long_rows} x {hi} + {lo} {mode}")
+    case = make_case(B=B, ctx=hi, n_kv=8, G=4, heavy=0.05, table="perm", seed=60 + B,
+                     device=DEV)
+    sl = case.seq_lens.clone()
+    sl[long_rows:] = lo
+    case.seq_lens = sl
+    kw = dict(coverage=0.95) if mode == "coverage" else dict(budget=0.05)
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", **kw)
+    for attend in (False, True, True):
+        _compare(case, st, attend=attend, wgs=0)
+
+
 def test_runtime_route_and_graph_replay():
     """select_then_attend (the route the backend and the bench take) picks the one-launch
-    pipeline for config 0 (two workgroups per unit); its graph replays equal the eager
-    result and leave the tickets at zero."""
+    pipeline for config 0 (two workgroups per unit); its graph replays
+    equal the eager result and leave the tickets at zero."""
     announce("unit pipeline: select_then_attend in a HIP graph")
     case = config_case(0, seed=3, device=DEV)
     st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", budget=0.05)
