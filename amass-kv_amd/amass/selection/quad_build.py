@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from .build import (CHUNK, _page_eigh, _quant_c, _quant_mu, _quant_vk, _refresh, _tail_blocks,
-                    _write_blocks, _write_layers, finalized_blocks)
+                    _write_layers, finalized_blocks)
 from .quad_state import v_to_device
 
 

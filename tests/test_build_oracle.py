@@ -10,7 +10,6 @@ match the oracle's codes up to fp32-vs-fp64 rounding at code boundaries.
 """
 import numpy as np
 import pytest
-import torch
 
 import oracle.build as ob
 import oracle.quant as oq

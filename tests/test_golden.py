@@ -63,7 +63,7 @@ def _rel(got, ref):
 @pytest.mark.parametrize("name,rank,v_bits", [("quad_i8", 8, 8), ("quad_i4_r4", 4, 4)])
 def test_gpu_quad_fixture(name, rank, v_bits):
     import torch
-    from amass.selection import QuadState, derive_page_params  # noqa: F401
+    from amass.selection import QuadState  # noqa: F401
     from amass.selection.quad_score import nrm_combine, quad_score_launch
     from helpers import announce, npf, npi
     announce(f"golden {name}")

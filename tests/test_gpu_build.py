@@ -32,8 +32,7 @@ import oracle.build as ob
 import oracle.quant as oq
 import oracle.score as osc
 from amass.bench.synth import make_case
-from amass.selection import QuadState, R8State, derive_page_params
-from amass.selection.build import summary_build_hip
+from amass.selection import QuadState, R8State
 from amass.selection.quad_build import quad_build_refresh, quad_build_tail
 from helpers import announce, npf, npi
 

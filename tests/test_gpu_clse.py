@@ -14,7 +14,6 @@ import torch
 
 import oracle.build as ob
 import oracle.decode as odec
-import oracle.quant as oq
 import oracle.score as osc
 import oracle.select as osel
 from amass.attention.decode import ResidentVSource, sparse_paged_decode_batched
