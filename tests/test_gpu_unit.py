@@ -209,6 +209,20 @@ def test_balanced_plan_ragged_batches(B, long_rows, hi, lo, mode):
         _compare(case, st, attend=attend, wgs=0)
 
 
+@pytest.mark.parametrize("mode", ["topb", "coverage"])
+def test_balanced_plan_more_than_64_requests(mode):
+    """The balanced plan's walk over more than one wave of requests (100 requests of two
+    kv heads: 200 units, below a round, so the device plans): the same bits as the
+    separate launches, the tickets at zero."""
+    announce(f"unit pipeline balanced plan: 100 requests x 2 kv heads, {mode}")
+    case = make_case(B=100, ctx=(64, 8192), n_kv=2, G=4, heavy=0.05, table="perm", seed=77,
+                     device=DEV)
+    kw = dict(coverage=0.95) if mode == "coverage" else dict(budget=0.05)
+    st = build_quad_state(case, rank=8, v_bits=8, combine="nrm", **kw)
+    for attend in (False, True):
+        _compare(case, st, attend=attend, wgs=0)
+
+
 def test_runtime_route_and_graph_replay():
     """select_then_attend (the route the backend and the bench take) picks the one-launch
     pipeline for config 0 (two workgroups per unit); its graph replays
