@@ -1,16 +1,18 @@
 // Per-unit pipeline for small batches on gfx950: quad score -> nrm combine + top-b /
-// coverage selection -> (optionally) the sparse decode, one workgroup per (request, kv
-// head) unit, one launch.
+// coverage selection -> (optionally) the sparse decode of each (request, kv head) unit,
+// one launch.
 //
 // The three Stage-A/B launches of a layer (quad_score.hip, select.hip, decode.hip) each
 // spread a small batch over few workgroups and each pays a launch, a chain of dependent
 // memory rounds before its first useful load, and the gap to the next graph node; at
 // batch 1 those fixed costs are most of the step (three launches of 6-10 us for 2.5 MB).
-// Here the unit's workgroup runs the same device code back to back:
-//   score   wave w walks tiles w, w + 8, ... of the unit's kv head (quad_walk, the score
-//           kernel's tile loop), writing score_h and the per-tile maxima;
+// Here the unit's workgroups run the same device code back to back:
+//   score   wave w of the unit's workgroup j (of c) walks tiles 8 j + w, 8 (j + c) + w,
+//           ... of the unit's kv head (quad_walk, the score kernel's tile loop), writing
+//           score_h and the per-tile maxima;
 //   select  the selection kernel's body (select_unit, fused nrm staging) reads them back
-//           after a workgroup barrier and writes score, page_table, page_cnt;
+//           (after a workgroup barrier, or the ticket hand-over below) and writes score,
+//           page_table, page_cnt;
 //   attend  (ATTEND) the decode's whole layout (attend_whole): the 8 waves split the kept
 //           pages and merge through LDS into the output.
 // Global stores of one phase are read by other waves of the same workgroup in the next;

@@ -302,9 +302,10 @@ int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
  * then amass_topb_select (mode 0) or amass_coverage_select (mode 1) with the fused nrm
  * staging over that score_h / tile_max, then -- when `decode` is not NULL --
  * amass_sparse_decode over the new page table in the layout that attends each
- * (request, kv-head) unit with one workgroup (path 2's).  One workgroup per unit runs
- * the three phases back to back, so a batch of few units pays one launch instead of
- * three.  The structs are those of the three entry points and must describe one batch:
+ * (request, kv-head) unit with one workgroup (path 2's).  The unit's workgroups run the
+ * three phases back to back (the last of them to finish scoring selects and attends),
+ * so a small batch pays one launch instead of three.  The structs are those of the
+ * three entry points and must describe one batch:
  * select->score_h / tile_max / n_sel_hi are score's, decode->page_table / page_cnt are
  * select's, decode->block_table is score's.  Served: combine 1, rank 8, v_bits 8,
  * G <= 8, max_pages <= 2048, resident V (v_src 0); other shapes return
@@ -314,10 +315,10 @@ int amass_sparse_decode_noalloc(const amass_decode_args* a, void* stream);
  * workgroups score each unit's tiles (a long row's summaries stream faster over several
  * CUs); 0 lets the device plan it per request from n_sel_hi (each workgroup about one
  * CU's share of the batch's tiles, so a ragged batch's long rows take more workgroups
- * than its short ones).  A unit of several workgroups is selected and attended by the last of them to
- * finish, counted in `tickets`, an int32 array of n_req * n_kv entries (unit
- * r * n_kv + kh) that must be zero before the launch and that every launch leaves zero
- * (so calls that overlap on one tickets array race); with wgs_per_unit 1 it may be
+ * than its short ones).  A unit of several workgroups is selected and attended by the
+ * last of them to finish, counted in `tickets`, an int32 array of n_req * n_kv entries
+ * (unit r * n_kv + kh) that must be zero before the launch and that every launch leaves
+ * zero (so calls that overlap on one tickets array race); with wgs_per_unit 1 it may be
  * NULL. */
 int amass_quad_select_attend(const amass_quad_score_args* score,
                              const amass_select_args* select,
