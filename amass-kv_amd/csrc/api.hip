@@ -93,10 +93,15 @@ extern "C" int amass_host_pool_free(void* host_ptr) {
 extern "C" int amass_tier_dma(const amass_copy_run* runs, int32_t n, void* stream) {
     if (n < 0) return AMASS_ERR_GEOMETRY;
     if (n > 0 && !runs) return AMASS_ERR_NULL;
-    hipStream_t s = (hipStream_t)stream;
+    // every run is checked before the first copy is issued
     for (int32_t i = 0; i < n; ++i) {
         const amass_copy_run& c = runs[i];
         if (!c.dst || !c.src || c.width <= 0 || c.height <= 0) return AMASS_ERR_GEOMETRY;
+        if (c.height > 1 && (c.dpitch < c.width || c.spitch < c.width)) return AMASS_ERR_GEOMETRY;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    for (int32_t i = 0; i < n; ++i) {
+        const amass_copy_run& c = runs[i];
         int rc;
         if (c.height == 1)
             rc = record_hip(hipMemcpyAsync(c.dst, c.src, (size_t)c.width, hipMemcpyHostToDevice, s));

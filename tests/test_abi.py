@@ -84,6 +84,21 @@ def test_status_strings_and_null_rejection():
     assert lib.amass_host_pool_alloc(16, None, None) == -1
 
 
+def test_copy_runs_checked_before_any_copy():
+    """amass_tier_dma checks the whole run list before issuing a copy: a bad run after good
+    ones (zero width; a pitch narrower than the row) is refused with no HIP call made."""
+    lib = _hip.load_library()
+    runs = (_hip.CopyRun * 2)()
+    for r in runs:
+        r.dst, r.src, r.dpitch, r.spitch, r.width, r.height = 0x1000, 0x2000, 256, 256, 256, 4
+    runs[1].width = 0
+    assert lib.amass_tier_dma(runs, 2, None) == -2
+    runs[1].width, runs[1].spitch = 256, 128
+    assert lib.amass_tier_dma(runs, 2, None) == -2
+    assert lib.amass_tier_dma(None, 1, None) == -1
+    assert lib.amass_tier_dma(runs, -1, None) == -2
+
+
 def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_hip, "_LIB", None)
     with pytest.raises(_hip.AmassError, match="missing"):
