@@ -270,12 +270,17 @@ __device__ __forceinline__ void quad_walk(const QuadParams& p, QuadLds& lds, int
 
     // ---- tile loop: group A of tile i+1 streams in while group B of tile i is used,
     // and group B of tile i+1 while group A of tile i+1 is used.  Every load in the
-    // steady state is unconditional so the wait counts stay exact. -----------------------
+    // steady state is unconditional so the wait counts stay exact.  The loop runs from
+    // the middle of one tile to the middle of the next (it enters with tile i's group A
+    // used and group B in flight): written with the tile boundary at the back edge, the
+    // compiler put group B's refill after a full drain of the memory counter at the loop
+    // header (every load waited for, every tile) and kept a second copy of group A,
+    // 178 VGPRs against 128 here. ------------------------------------------------------
     float q[2][RP];
     float qmu[2];
+    GroupScales<RP> sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
+    tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);
     for (int i = 0; i + 1 < cnt; ++i) {
-        const GroupScales<RP> sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
-        tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);
         // keep the refill of a buffer after its last use (bounds the live registers)
         __builtin_amdgcn_sched_barrier(0);
         group_blocks<RP>(blk_next, n, gb);
@@ -289,9 +294,9 @@ __device__ __forceinline__ void quad_walk(const QuadParams& p, QuadLds& lds, int
         __builtin_amdgcn_sched_barrier(0);
         load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, p.rec_sb, gb, gbuf.v);
         tile += wstride;
+        sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
+        tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);
     }
-    const GroupScales<RP> sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
-    tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);
     tile_finish<RP, VB, NRM, COMB>(p, qa, gbuf, sc, q, qmu, req, h, tile, nsh, n, kg, qs0, qs1,
                                    qcoef);
 }

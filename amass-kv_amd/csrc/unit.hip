@@ -167,7 +167,8 @@ __global__ __launch_bounds__(UN_THREADS) void unit_kernel(const QuadParams qp,
     }
 }
 
-// One resident round of the kernel's workgroups: one per CU (178 VGPRs, 8 waves).
+// One resident round of the kernel's workgroups, taken as one per CU (8 waves of up to 168
+// VGPRs and 65 KB of LDS each).
 static int unit_target() {
     static int cus[64] = {0};
     int dev = 0;
