@@ -68,6 +68,7 @@ struct R8Geom {
     static constexpr int CB = col_bytes<VB>();
     static constexpr int CROW = RP * CBITS / 8;          // bytes per token row of c
     static constexpr int VM = RP * CB + 128 + 16 * CROW; // record bytes before the scales
+    static constexpr bool NT = VM % 128 == 0;            // V loads non-temporal (whole lines)
 };
 
 template <int G>
@@ -96,20 +97,20 @@ struct R8GroupC {                         // the lane's c rows
 // `vbase` = rec + h * VM + the lane's V offset, `gb` the blocks of the lane's group
 // pages; `lr` = the lane's own-page record (block + head * VM + 16 kg), `moff` = its
 // scale block - lr
-template <int RP, int VB>
+template <int RP, int VB, bool NT>
 __device__ __forceinline__ void r8_load_a(const int8_t* vbase, int64_t rec_sb,
                                           const int (&gb)[RP], const int8_t* lr,
                                           R8GroupA<RP, VB>& a, int moff) {
-    load_groups<RP, VB, 0, RP / 2>(vbase, rec_sb, gb, a.v);
+    load_groups<RP, VB, 0, RP / 2, NT>(vbase, rec_sb, gb, a.v);
     a.mu[0] = ld16(lr + RP * col_bytes<VB>());
     a.mu[1] = ld16(lr + RP * col_bytes<VB>() + 64);
     a.meta = ld16(lr + moff);
 }
 
-template <int RP, int VB>
+template <int RP, int VB, bool NT>
 __device__ __forceinline__ void r8_load_b(const int8_t* vbase, int64_t rec_sb,
                                           const int (&gb)[RP], R8GroupB<RP, VB>& b) {
-    load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, rec_sb, gb, b.v);
+    load_groups<RP, VB, RP / 2, RP - RP / 2, NT>(vbase, rec_sb, gb, b.v);
 }
 
 template <int CL>
@@ -458,10 +459,10 @@ void r8_score_kernel(const R8Params p) {
     R8GroupA<RP, VB> ga;
     R8GroupB<RP, VB> gb;
     R8GroupC<CL> gc;
-    r8_load_a<RP, VB>(vbase, p.rec_sb, gbk, lr, ga, moff);
+    r8_load_a<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, lr, ga, moff);
     int bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
     __builtin_amdgcn_sched_barrier(0);
-    r8_load_b<RP, VB>(vbase, p.rec_sb, gbk, gb);
+    r8_load_b<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, gb);
     __builtin_amdgcn_sched_barrier(0);
     r8_load_c<CL>(lr + coff, gc);
 
@@ -494,12 +495,12 @@ void r8_score_kernel(const R8Params p) {
         __builtin_amdgcn_sched_barrier(0);
         group_blocks<RP>(bn_next, n, gbk);
         const int8_t* ln = lane_rec(bn_next);
-        r8_load_a<RP, VB>(vbase, p.rec_sb, gbk, ln, ga, moff);
+        r8_load_a<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, ln, ga, moff);
         bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
         r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, row, req, h, page, valid,
                                      pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
-        r8_load_b<RP, VB>(vbase, p.rec_sb, gbk, gb);
+        r8_load_b<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, gb);
         r8_tile_tail<RP, CBITS, G, CLSE>(p, gc, sc, acc, req, h, page, valid, pair, part, kg, sl,
                                          qsq0, qsq1);
         __builtin_amdgcn_sched_barrier(0);

@@ -80,9 +80,15 @@ __device__ __forceinline__ int lane_page(int n) {
 
 // V codes stream once per step: non-temporal 16-byte loads (each instruction reads PP
 // runs of 64 r' contiguous bytes; the hint measured +10 % over plain loads on this
-// pattern, and -10 % on one of 16 pages x 64 bytes)
+// pattern, and -10 % on one of 16 pages x 64 bytes).  NT = false gives plain loads, for
+// records whose per-head size is not a whole number of 128-byte lines: there two heads'
+// waves read the two parts of a shared line, and under the hint the L2 does not keep the
+// line for the second of them (CLSE r' = 2, int4: 272-byte records fetched 1.06x their
+// bytes with the hint, 21.1 against 22.8 us without it at the config-1 shape).
+template <bool NT = true>
 __device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
+    else return *reinterpret_cast<const i32x4_t*>(p);
 }
 
 // block id of every group's page for this lane: lane m of a row carries page
@@ -109,17 +115,17 @@ __device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) 
 }
 
 // `base` = rec + h * VM + the lane's V offset (16 (kg r' + n % r')); group j of block b
-template <int RP, int VB, int J0, int NG>
+template <int RP, int VB, int J0, int NG, bool NT = true>
 __device__ __forceinline__ void load_groups(const int8_t* base, int64_t rec_sb,
                                             const int (&gb)[RP], i32x4_t* v) {
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
         const int8_t* p = base + (int64_t)gb[J0 + j] * rec_sb;
         if constexpr (VB == 8) {
-            v[2 * j] = ld16_stream(p);
-            v[2 * j + 1] = ld16_stream(p + 64 * RP);
+            v[2 * j] = ld16_stream<NT>(p);
+            v[2 * j + 1] = ld16_stream<NT>(p + 64 * RP);
         } else {
-            v[j] = ld16_stream(p);
+            v[j] = ld16_stream<NT>(p);
         }
     }
 }
