@@ -26,12 +26,15 @@ and the reference layout; ``load_reference`` and ``reference_V`` use them.  CLSE
 the r8 records keep V in the same tiled order.
 
 CLSE (``coords="lse"``, the reference's ``score="clse"``) keeps the per-key coordinates
-and the residual scatter energy instead of sig2, in the r8 record layout
-(AMASS_R8_REC_BYTES, see :mod:`amass.selection.state`): per head
-``[quad_V tiled | quad_mu | quad_c (page, r'[/2])]`` and a 64-byte scale block
-with V_scale at half 0, c_scale at halves 8..23 (``c_grain="page"``: one scale per
-(block, head), kept in all 16 halves and exposed as half 8), mu_scale at half 24 and
-quad_resid at half 25; ``quad_sig2`` is None there.
+and the residual scatter energy instead of sig2, in its own record
+(AMASS_CLSE_REC_BYTES = VQ + TB per head): the n_kv heads' ``[quad_V tiled | quad_mu]``
+(VQ = r' * CB + 128 bytes, whole lines, as above), then per head a tail of
+TB = 16 * rc + 16 * ceil((36 + 2 r') / 16) bytes at n_kv * VQ + TB * h:
+``quad_c (page, rc)`` (rc = r' or r'/2 bytes per token row), then fp16 halves c_scale
+0..15 (``c_grain="page"``: one scale per (block, head), kept in all 16 halves and exposed
+as half 0), V_scale at half 16, mu_scale at half 16 + r' and quad_resid at half
+17 + r', zero to the end (320 bytes per head at r' = 2 with int4 V and c, against 336 in
+the r8 layout with its 64-byte scale block); ``quad_sig2`` is None there.
 
 Per-step outputs are those of :class:`R8State`; combine="nrm" adds score_h
 (R, n_kv, G, MP) and score_tmax (R, n_kv, G, ceil(MP / 16)), the per-16-page-tile
@@ -150,24 +153,31 @@ class QuadState:
                              "(and 16-token pages with CLSE coordinates)")
         cb = D // 2 if v_bits == 4 else D
         vb = r * cb
-        rc = (r // 2 if c_bits == 4 else r) if coords == "lse" else 0
-        vm = vb + D + page * rc                           # V + mu (+ c) bytes per head
-        self.rec_bytes = vm + 64                          # + the head's scale block
+        vm = vb + D                                       # V + mu bytes per head
+        if coords == "lse":
+            rc = r // 2 if c_bits == 4 else r             # c bytes per token row
+            tb = page * rc + 16 * ((36 + 2 * r + 15) // 16)   # the head's tail
+        else:
+            tb = 64                                       # the head's scale block
+        self.rec_bytes = vm + tb
         self.quad_rec = torch.zeros(L, NB, n_kv * self.rec_bytes, device=device, dtype=i8)
         recs = self.quad_rec[..., :n_kv * vm].unflatten(-1, (n_kv, vm))
-        meta = self.quad_rec[..., n_kv * vm:].unflatten(-1, (n_kv, 64)).view(f16)
+        tails = self.quad_rec[..., n_kv * vm:].unflatten(-1, (n_kv, tb))
         self.quad_V = recs[..., :vb].unflatten(-1, (r, cb))
         self.quad_mu = recs[..., vb:vb + D]
-        self.V_scale = meta[..., 0:r]
         self.quad_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=device, dtype=bf16)
         if coords == "lse":
-            self.quad_c = recs[..., vb + D:].unflatten(-1, (page, rc))
-            self._c_scale16 = meta[..., 8:8 + page]
-            self.c_scale = self._c_scale16 if c_grain == "token" else meta[..., 8]
-            self.mu_scale = meta[..., 24]
-            self.quad_resid = meta[..., 25]
+            self.quad_c = tails[..., :page * rc].unflatten(-1, (page, rc))
+            sp = tails[..., page * rc:].view(f16)         # the tail's scale halves
+            self._c_scale16 = sp[..., 0:page]
+            self.c_scale = self._c_scale16 if c_grain == "token" else sp[..., 0]
+            self.V_scale = sp[..., 16:16 + r]
+            self.mu_scale = sp[..., 16 + r]
+            self.quad_resid = sp[..., 17 + r]
             self.quad_sig2 = None
         else:
+            meta = tails.view(f16)
+            self.V_scale = meta[..., 0:r]
             self.quad_sig2 = meta[..., 8:8 + r]
             self.mu_scale = meta[..., 16]
             self.quad_c = self.c_scale = self.quad_resid = self._c_scale16 = None

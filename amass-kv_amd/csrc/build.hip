@@ -11,7 +11,7 @@
 //          (block, head) ("tensor"), c per token ("page") or per (block, head) ("tensor")
 //   quad stores sig2 = fp16(S2r); r8 stores c; both the content tag K[15][:TAGW].
 // Output goes straight into the packed records the score kernels read
-// (AMASS_QUAD_REC_BYTES / AMASS_R8_REC_BYTES).
+// (AMASS_QUAD_REC_BYTES / AMASS_R8_REC_BYTES / AMASS_CLSE_REC_BYTES).
 //
 // One wave per (block, kv-head, layer), one wave per workgroup (the Jacobi rounds'
 // barriers then wait for no other wave).  The K page is staged in LDS as
@@ -225,12 +225,18 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
     __syncthreads();
 
     // ---- record addressing ---------------------------------------------------------------
+    // quad / r8: head h's record [V | mu (| c rows)] at h VM, its 64-byte scale block at
+    // n_kv VM + 64 h.  CLSE: [V | mu] at h VM, its tail of TB bytes [c rows | scale part]
+    // at n_kv VM + TB h (AMASS_CLSE_REC_BYTES).
     const int CB = a.v_bits == 8 ? BD : BD / 2;
     const int crow = R8 ? r * a.c_bits / 8 : 0;
-    const int VM = r * CB + BD + 16 * crow;
+    const int VM = r * CB + BD + (CLSE ? 0 : 16 * crow);
+    const int TB = CLSE ? 16 * crow + 16 * ((36 + 2 * r + 15) / 16) : 64;
     int8_t* lrec = a.rec + layer * a.rec_lsb + blk * a.rec_sb;
     int8_t* rec = lrec + (int64_t)h * VM;
-    uint16_t* meta = (uint16_t*)(lrec + (int64_t)a.n_kv * VM + 64 * h);
+    int8_t* tail = lrec + (int64_t)a.n_kv * VM + (int64_t)TB * h;
+    int8_t* crows = CLSE ? tail : rec + r * CB + BD;
+    uint16_t* meta = (uint16_t*)(CLSE ? tail + 16 * crow : tail);
     const float vlvl = a.v_bits == 8 ? 127.f : 7.f;
 
     // ---- Vk = dc^T U8 / S8, per-column (or per-head) int8 / int4 ----------------------
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         }
         csc_t = quant_scale(m, clvl);
         if (lane < BP) {
-            int8_t* cr = rec + r * CB + BD + t * crow;
+            int8_t* cr = crows + t * crow;
             if (a.c_bits == 8) {
                 for (int k = 0; k < r; ++k) cr[k] = (int8_t)quant_code(cv[k], csc_t, clvl);
             } else {
@@ -320,9 +326,29 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         }
     }
 
-    // ---- the 64-byte fp16 scale block ----------------------------------------------------
+    // ---- the 64-byte fp16 scale block (CLSE: the tail's scale part) ---------------------
     const float cs_in = __shfl(csc_t, (lane - 8) & 63, WAVE);   // c_scale of token lane - 8
     const uint32_t cs_bits = __float_as_uint(__shfl(csc_t, 0, WAVE));  // c_grain 2: fp32
+    if constexpr (CLSE) {
+        // halves: c_scale of token lane (0..15), V_scale (16..16+r), mu_scale, the residual,
+        // zero to the tail's end
+        const float cs_t = __shfl(csc_t, lane & 15, WAVE);
+        if (lane < (TB - 16 * crow) / 2) {
+            float v = 0.f;
+            if (lane < 16) v = cs_t;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (k < r && lane == 16 + k) v = vsc[k];
+            if (lane == 16 + r) v = msc;
+            if (lane == 17 + r) {
+                float top = 0.f;
+                for (int k = 0; k < r; ++k) top += L.s2[w][k];
+                v = fmaxf(trace - top, 0.f);
+            }
+            meta[lane] = f2h_bits(v);
+        }
+        return;
+    }
     if (lane < 32) {
         float v = 0.f;
         bool set = false;
@@ -332,12 +358,6 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         if constexpr (R8) {
             if (lane >= 8 && lane < 24 && a.c_grain != 2) { v = cs_in; set = true; }
             else if (lane == 24) { v = msc; set = true; }
-            else if (CLSE && lane == 25) {
-                float top = 0.f;
-                for (int k = 0; k < r; ++k) top += L.s2[w][k];
-                v = fmaxf(trace - top, 0.f);
-                set = true;
-            }
         } else {
             if (lane >= 8 && lane < 8 + r) { v = L.s2[w][lane - 8]; set = true; }
             else if (lane == 16) { v = msc; set = true; }
@@ -371,7 +391,9 @@ extern "C" int amass_summary_build(const amass_build_args* a, void* stream) {
     if (a->n_kv % nw != 0) return AMASS_ERR_GEOMETRY;
     const int crow = a->kind >= 1 ? a->rank * a->c_bits / 8 : 0;
     const int vm = a->rank * (a->v_bits == 8 ? BD : BD / 2) + BD + 16 * crow;
-    if (a->rec_sb < (int64_t)a->n_kv * (vm + 64)) return AMASS_ERR_GEOMETRY;
+    const int64_t rec_bytes = a->kind == 2
+        ? AMASS_CLSE_REC_BYTES(a->rank, a->v_bits, a->c_bits) : vm + 64;
+    if (a->rec_sb < (int64_t)a->n_kv * rec_bytes) return AMASS_ERR_GEOMETRY;
     if (a->n_layers < 1 || (a->n_layers > 1 && !a->k_layers)) return AMASS_ERR_GEOMETRY;
     if (a->n == 0) return AMASS_OK;
     const dim3 grid(a->n, a->n_kv / nw, a->n_layers), blk(nw * WAVE);

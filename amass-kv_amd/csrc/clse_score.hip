@@ -18,7 +18,7 @@ extern "C" int amass_clse_score(const amass_clse_score_args* a, void* stream) {
         return AMASS_ERR_GEOMETRY;
     if (a->rank != 2 && a->rank != 4 && a->rank != 8) return AMASS_ERR_UNSUPPORTED;
     if ((((uintptr_t)a->rec) & 15) != 0 || (a->rec_sb & 15) != 0) return AMASS_ERR_GEOMETRY;
-    if (a->rec_sb < (int64_t)a->n_kv * AMASS_R8_REC_BYTES(a->rank, a->v_bits, a->c_bits))
+    if (a->rec_sb < (int64_t)a->n_kv * AMASS_CLSE_REC_BYTES(a->rank, a->v_bits, a->c_bits))
         return AMASS_ERR_GEOMETRY;
     if (a->n_req == 0) return AMASS_OK;
     R8Params p;

@@ -19,7 +19,7 @@
 // between them (TPL tokens each): the token tail needs no exchange of q~, only a max and
 // a sum across those groups for the logsumexp, and a max across pairs for the group max.
 //
-// Layout (AMASS_R8_REC_BYTES per kv head).  Per block, the n_kv heads' records
+// r8 layout (AMASS_R8_REC_BYTES per kv head).  Per block, the n_kv heads' records
 // [Vk tiled: 16 bytes per (K-step t, d group kg, column k) at ((t * 4 + kg) * r + k) * 16
 // (int4: t folded into the nibbles) | 128 mu codes | c: 16 token rows of r * c_bits / 8
 // bytes], then the n_kv heads' 64-byte fp16 scale blocks (Vk_scale at half 0, c_scale at
@@ -29,12 +29,21 @@
 // quad kernel.
 //
 // CLSE (reference selection/quad_score.py:156-276, score="clse") is the same computation
-// over the same record (its quad_V / quad_mu / quad_c / c_scale; the residual scatter
-// energy at half 25 of the scale block) plus an isotropic term for the key variance
-// outside the stored subspace:
+// over its quad_V / quad_mu / quad_c / c_scale and the residual scatter energy, plus an
+// isotropic term for the key variance outside the stored subspace:
 //   iso_g = max(|q_g|^2 - |q~_g|^2, 0) * resid * s^2 / (2 P (d - r))
 //   S_g   = s mu.q_g + logsumexp_t tok[g,t] + iso_g ; combine "max" or per head ("nrm").
 // |q_g|^2 comes from the bf16 query in fp32, |q~_g|^2 from the lane's own q~.
+// Its record (AMASS_CLSE_REC_BYTES per kv head) keeps no dead bytes in the lines it
+// streams: per block the n_kv heads' [V tiled | 128 mu codes] (whole lines), then per
+// head a tail of TB bytes: the c rows, then fp16 c_scale[0..16), V_scale[0..r) at half
+// 16, mu_scale at half 16 + r and the residual at half 17 + r.  (The r8 layout's 64-byte
+// scale block leaves 24 of its bytes unused at r = 2, and its 272-byte head records at
+// r = 2, int4 split lines between heads.)  The lanes load the tail's scale part so that
+// `meta` holds what the r8 layout's 16 bytes kg would: lane group 0 the V scales (bytes
+// 32.., which at r <= 4 also hold mu_scale and the residual), 1 and 2 the c scales of
+// tokens 0..7 and 8..15, 3 at r = 8 the bytes 48.. (mu_scale and the residual; at
+// r <= 4 it repeats group 0's load).
 #pragma once
 #include "score_mfma.h"
 
@@ -63,12 +72,18 @@ struct R8Params {
     int target;     // workgroups the batch's tiles are balanced over
 };
 
-template <int RP, int VB, int CBITS>
+template <int RP, int VB, int CBITS, bool CLSE>
 struct R8Geom {
     static constexpr int CB = col_bytes<VB>();
     static constexpr int CROW = RP * CBITS / 8;          // bytes per token row of c
-    static constexpr int VM = RP * CB + 128 + 16 * CROW; // record bytes before the scales
-    static constexpr bool NT = VM % 128 == 0;            // V loads non-temporal (whole lines)
+    // a head's record before the scales (r8: V, mu, c) or before its tail (CLSE: V, mu)
+    static constexpr int VM = RP * CB + 128 + (CLSE ? 0 : 16 * CROW);
+    // bytes of a head's scale block (r8) or tail (CLSE: c rows + scale part)
+    static constexpr int TB = CLSE ? 16 * CROW + 16 * ((36 + 2 * RP + 15) / 16) : 64;
+    // V loads non-temporal for whole-line records with runs of >= 256 bytes per page; at
+    // r = 2 (128-byte runs) plain loads measured faster (CLSE config-1 shape: 20.1 against
+    // 20.4-20.7 us)
+    static constexpr bool NT = VM % 128 == 0 && RP >= 4;
 };
 
 template <int G>
@@ -140,14 +155,18 @@ struct R8Scales {
     float cs[TPL];
 };
 
-template <int RP, int TPL>
+template <int RP, int TPL, bool CLSE>
 __device__ __forceinline__ R8Scales<RP, TPL> r8_gather_scales(i32x4_t meta, int n, int part,
                                                               bool c_fp32) {
     R8Scales<RP, TPL> s;
     constexpr int NW = RP / 2;            // dwords holding r halves
 #pragma unroll
     for (int i = 0; i < 4; ++i) s.vs[i] = i < NW ? (uint32_t)__shfl(meta[i], n, WAVE) : 0u;
-    const uint32_t w24 = (uint32_t)__shfl(meta[0], n + 48, WAVE);   // halves 24, 25
+    // mu_scale and the residual: halves 24, 25 of the r8 scale block (lane group 3); in
+    // the CLSE tail at r <= 4 they follow the V scales in lane group 0's dword r / 2
+    uint32_t w24;
+    if constexpr (CLSE && RP <= 4) w24 = (uint32_t)__shfl(meta[RP / 2], n, WAVE);
+    else w24 = (uint32_t)__shfl(meta[0], n + 48, WAVE);
     s.mus = fp16_to_f32((uint16_t)(w24 & 0xFFFFu));
     s.resid = fp16_to_f32((uint16_t)(w24 >> 16));
     if (c_fp32) {                         // one fp32 for the page: bytes 16..19 (group 1)
@@ -407,7 +426,7 @@ __device__ __forceinline__ void r8_tile_tail(const R8Params& p,
 template <int RP, int VB, int CBITS, int G, bool COMB, bool CLSE>
 __global__ __launch_bounds__(R8_MAXW * WAVE)
 void r8_score_kernel(const R8Params p) {
-    using Geo = R8Geom<RP, VB, CBITS>;
+    using Geo = R8Geom<RP, VB, CBITS, CLSE>;
     constexpr int VM = Geo::VM;
     constexpr int TPL = R8Split<G>::TPL;
     constexpr int GP = R8Split<G>::GP;
@@ -440,8 +459,13 @@ void r8_score_kernel(const R8Params p) {
         return p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)];
     };
     const int64_t rhead = (int64_t)h * VM + 16 * kg;
-    const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
-    const int coff = RP * Geo::CB + 128 + part * CL - 16 * kg;
+    // lr + moff: the lane's 16 bytes of the head's scale block (r8) or tail (CLSE);
+    // lr + coff: its c rows
+    const int tail = p.n_kv * VM + h * (Geo::TB - VM) - 16 * kg;   // the head's tail - lr
+    const int moff = CLSE ? tail + 16 * Geo::CROW +
+                                (kg == 0 ? 32 : (kg == 3 ? (RP == 8 ? 48 : 32) : 16 * (kg - 1)))
+                          : tail + 16 * kg;
+    const int coff = CLSE ? tail + part * CL : RP * Geo::CB + 128 + part * CL - 16 * kg;
     auto lane_rec = [&](int blk) { return p.rec + (int64_t)blk * p.rec_sb + rhead; };
     const int8_t* vbase = p.rec + (int64_t)h * VM + 16 * (kg * RP + n % RP);
     __shared__ R8Lds lds;
@@ -489,7 +513,7 @@ void r8_score_kernel(const R8Params p) {
     for (int i = 0; i + 1 < cnt; ++i) {
         const int page = page_of(tile);
         const bool valid = page < nsh;
-        const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part, p.c_fp32 != 0);
+        const auto sc = r8_gather_scales<RP, TPL, CLSE>(ga.meta, n, part, p.c_fp32 != 0);
         r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid,
                                        pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
@@ -509,7 +533,7 @@ void r8_score_kernel(const R8Params p) {
     }
     const int page = page_of(tile);
     const bool valid = page < nsh;
-    const auto sc = r8_gather_scales<RP, TPL>(ga.meta, n, part, p.c_fp32 != 0);
+    const auto sc = r8_gather_scales<RP, TPL, CLSE>(ga.meta, n, part, p.c_fp32 != 0);
     r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid, pair,
                                    part, n);
     r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, row, req, h, page, valid, pair,

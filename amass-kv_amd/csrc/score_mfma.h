@@ -81,10 +81,10 @@ __device__ __forceinline__ int lane_page(int n) {
 // V codes stream once per step: non-temporal 16-byte loads (each instruction reads PP
 // runs of 64 r' contiguous bytes; the hint measured +10 % over plain loads on this
 // pattern, and -10 % on one of 16 pages x 64 bytes).  NT = false gives plain loads, for
-// records whose per-head size is not a whole number of 128-byte lines: there two heads'
-// waves read the two parts of a shared line, and under the hint the L2 does not keep the
-// line for the second of them (CLSE r' = 2, int4: 272-byte records fetched 1.06x their
-// bytes with the hint, 21.1 against 22.8 us without it at the config-1 shape).
+// records whose per-head size is not a whole number of 128-byte lines (two heads' waves
+// then read the two parts of a shared line, and under the hint the L2 does not keep the
+// line for the second of them: 272-byte records fetched 1.05x their bytes with the hint)
+// and for the short runs of r' = 2.
 template <bool NT = true>
 __device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
     if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 9
+#define AMASS_ABI_VERSION 10
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -124,8 +124,8 @@ int amass_r8_score(const amass_r8_score_args* a, void* stream);
  * v_grain 0 or per head for 1; c per token for c_grain 0 or per head for 1; r8 only:
  * c_grain 2 = per head with the scale stored as fp32, the c_fp32 layout of the r8 score).  Writes the
  * block's packed record (kind 0: quad, AMASS_QUAD_REC_BYTES layout with sig2 = fp16(S2r);
- * kind 1: r8, AMASS_R8_REC_BYTES layout; kind 2: CLSE, the r8 layout plus the residual
- * scatter energy resid = max(trace(Gm) - sum S2r, 0) as fp16 at half 25, c_grain 0 per
+ * kind 1: r8, AMASS_R8_REC_BYTES layout; kind 2: CLSE, AMASS_CLSE_REC_BYTES layout with
+ * the residual scatter energy resid = max(trace(Gm) - sum S2r, 0), c_grain 0 per
  * token / 1 one scale per head written to all 16 c_scale halves) and, if tag != NULL,
  * the content tag
  * K[page-1][h][0:tagw].  rank 1..8 (even for int4 codes).  n_layers layers in one launch:
@@ -145,16 +145,25 @@ int amass_summary_build(const amass_build_args* a, void* stream);
 /* ---- CLSE page score (quad storage + per-key coordinates) -------------------------- */
 /* Replaces clse_score (selection/quad_score.py:156-393, the reference's default score) and
  * its hand-CUDA clse_score_cuda (backend/_runtime.py:214-229).  Per (request, kv-head,
- * page p < n_sel_hi) and group head g, over the record of AMASS_R8_REC_BYTES layout
- * (quad_V tiled | quad_mu | quad_c rows; scale block: V_scale half 0, c_scale halves
- * 8..23 (a per-page "page" grain scale repeated 16 times), mu_scale half 24, quad_resid
- * half 25):
+ * page p < n_sel_hi) and group head g, over the record of AMASS_CLSE_REC_BYTES layout.
+ * Per block, the n_kv heads' [quad_V tiled as for the quad score | quad_mu 128 int8]
+ * (VQ = r'*CB + 128 bytes each, whole 128-byte lines), head h at h*VQ, then the n_kv
+ * heads' tails of TB bytes, head h at n_kv*VQ + TB*h: quad_c (16 token rows of
+ * r'*c_bits/8 bytes, int4 two columns per byte, low nibble = even column), then fp16
+ * halves c_scale[0..16) (a per-page "page" grain scale repeated 16 times), V_scale[0..r')
+ * at half 16, mu_scale at half 16 + r', quad_resid at half 17 + r', zero to the end.
+ * TB = 16*r'*c_bits/8 + 16*ceil((36 + 2r')/16): 320 bytes per head at the reference's
+ * default (r' = 2, int4 V and c), 8 of them padding.  (No counterpart in the reference's
+ * slabs; the views of the reference's tensors are selection/quad_state.py here.)
  *   q~[g,k] = (V_code[:,k] V_scale[k]) . q_g ; tok[g,t] = s c_scale[t] (c_code[t,:] . q~[g])
  *   iso[g]  = max(|q_g|^2 - |q~[g]|^2, 0) * resid * s^2 / (2 page max(d - r', 1))
  *   S_g = s mu.q_g + logsumexp_{t : 16p+t < seq_len} tok[g,t] + iso[g]
  * combine 0: score[r,kh,p] = max_g S_g; combine 1: score_h[r,kh,g,p] = S_g (the input of
  * the nrm combine fused into amass_coverage_select / amass_topb_select).  rank 2, 4 or 8;
  * comb_out as for amass_r8_score. */
+#define AMASS_CLSE_REC_BYTES(rank, v_bits, c_bits) \
+    ((rank) * ((v_bits) == 8 ? 128 : 64) + 128 + 2 * (rank) * (c_bits) + \
+     16 * ((36 + 2 * (rank) + 15) / 16))
 typedef struct amass_clse_score_args {
     const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
     const int8_t*  rec;      int64_t rec_sb;         /* (NB,n_kv,REC) summary records   */

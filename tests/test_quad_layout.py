@@ -148,3 +148,62 @@ def test_r8_page_f32_scale_position():
             assert blk[48:50].view(np.float16)[0] == mus[b, h]
     tcs = st.token_c_scale(0).numpy()
     assert tcs.shape == (NB, n_kv, 16) and np.array_equal(tcs, np.repeat(cs[..., None], 16, -1))
+
+
+@pytest.mark.parametrize("v_bits,c_bits,r", [(4, 4, 2), (8, 4, 2), (4, 8, 4), (8, 8, 8),
+                                             (4, 4, 8)])
+@pytest.mark.parametrize("c_grain", ["token", "page"])
+def test_clse_record_positions(v_bits, c_bits, r, c_grain):
+    """The packed CLSE record (include/amass_hip.h, AMASS_CLSE_REC_BYTES): per block the
+    n_kv heads' [V tiled | mu] at h * VQ (whole 128-byte lines), then per head a tail of
+    TB bytes at n_kv * VQ + TB * h: the c rows, then fp16 c_scale[0..16), V_scale at
+    half 16, mu_scale at half 16 + r', the residual at half 17 + r', zeros to the end.
+    Every field is checked at that byte offset in the raw buffer."""
+    n_kv, NB = 3, 4
+    st = QuadState("cpu", num_layers=1, num_blocks=NB, n_kv=n_kv, G=4, head_dim=128,
+                   page=16, max_reqs=1, max_pages=4, rank=r, v_bits=v_bits, coords="lse",
+                   c_bits=c_bits, c_grain=c_grain)
+    cb = 128 if v_bits == 8 else 64
+    vq = r * cb + 128
+    crow = r * c_bits // 8
+    tb = 16 * crow + 16 * ((36 + 2 * r + 15) // 16)
+    rec_bytes = r * cb + 128 + 2 * r * c_bits + 16 * ((36 + 2 * r + 15) // 16)  # the macro
+    assert vq % 128 == 0 and tb % 16 == 0
+    assert st.rec_bytes == rec_bytes == vq + tb and st.quad_rec.shape[-1] == n_kv * rec_bytes
+    if (v_bits, c_bits, r) == (4, 4, 2):
+        assert rec_bytes == 320                     # the reference's default CLSE record
+    rng = np.random.default_rng(r * 100 + v_bits * 10 + c_bits)
+    lv, lc = (127 if v_bits == 8 else 7), (127 if c_bits == 8 else 7)
+    vcode = rng.integers(-lv, lv + 1, (NB, n_kv, 128, r)).astype(np.int8)
+    V = vcode if v_bits == 8 else oq.pack_i4(vcode)
+    ccode = rng.integers(-lc, lc + 1, (NB, n_kv, 16, r)).astype(np.int8)
+    c = ccode if c_bits == 8 else oq.pack_i4(ccode)
+    mu = rng.integers(-127, 128, (NB, n_kv, 128)).astype(np.int8)
+    mus = (rng.random((NB, n_kv)) + 0.5).astype(np.float16)
+    vs = (rng.random((NB, n_kv, r)) + 0.5).astype(np.float16)
+    cs = (rng.random((NB, n_kv, 16) if c_grain == "token" else (NB, n_kv)) + 0.5
+          ).astype(np.float16)
+    res = (rng.random((NB, n_kv)) + 0.5).astype(np.float16)
+    st.load_reference(0, mu, mus, V, vs, c=c, c_scale=cs, resid=res)
+    assert np.array_equal(st.reference_V(0).numpy(), V)
+    raw = st.quad_rec[0].numpy().view(np.uint8)             # (NB, n_kv * REC)
+    for b in range(NB):
+        for h in range(n_kv):
+            base = h * vq
+            if v_bits == 8:               # d = 77: K-step 1, d group 0, byte 13
+                off = ((1 * 4 + 0) * r + (r - 1)) * 16 + 13
+                assert raw[b, base + off].view(np.int8) == vcode[b, h, 77, r - 1]
+            assert np.array_equal(raw[b, base + r * cb: base + r * cb + 128].view(np.int8),
+                                  mu[b, h])
+            tail = raw[b, n_kv * vq + tb * h: n_kv * vq + tb * (h + 1)]
+            assert np.array_equal(tail[:16 * crow].reshape(16, crow).view(np.int8), c[b, h])
+            halves = tail[16 * crow:].view(np.float16)
+            want_cs = cs[b, h] if c_grain == "token" else np.full(16, cs[b, h], np.float16)
+            assert np.array_equal(halves[:16], want_cs)
+            assert np.array_equal(halves[16:16 + r], vs[b, h])
+            assert halves[16 + r] == mus[b, h] and halves[17 + r] == res[b, h]
+            assert not halves[18 + r:].any()
+    # the views the kernels' inputs are read back through
+    assert np.array_equal(st.quad_c[0].numpy(), c)
+    assert np.array_equal(st.V_scale[0].numpy(), vs) and np.array_equal(st.quad_resid[0].numpy(), res)
+    assert np.array_equal(st.mu_scale[0].numpy(), mus)
