@@ -17,6 +17,7 @@ import torch
 
 from .._hip import (ClseScoreArgs, NrmArgs, QuadScoreArgs, call, call_select_attend,
                     current_stream, ptr, require_cuda)
+from .score import check_rec_span
 from .select import derive_page_params, select_args, select_pages
 
 # The per-unit pipeline (amass_quad_select_attend): the rows it serves and the most
@@ -69,6 +70,7 @@ def _quad_args(st, layer, q, block_table, n_req, scale, comb_out=None) -> QuadSc
         raise ValueError("block_table narrower than the scored page range")
     if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
         raise ValueError("quad_rec must hold each block's records contiguously")
+    check_rec_span(rec)
     if getattr(st, "coords", "none") != "none":
         raise ValueError("a CLSE state (coords='lse') is scored by clse_score")
     nrm = st.combine == "nrm"
@@ -145,6 +147,7 @@ def clse_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: floa
         raise ValueError("seq_lens must be int32")
     if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
         raise ValueError("quad_rec must hold each block's records contiguously")
+    check_rec_span(rec)
     nrm = st.combine == "nrm"
     sh = st.score_h
     a = ClseScoreArgs(

@@ -12,6 +12,15 @@ import torch
 from .._hip import R8ScoreArgs, call, current_stream, ptr, require_cuda
 
 
+def check_rec_span(rec) -> None:
+    """The score kernels address a layer's records with 32-bit byte offsets from its base
+    (block * rec_sb + head and lane offsets), so the layer's record buffer must span less
+    than 4 GiB."""
+    if rec.shape[0] * rec.stride(0) > (1 << 32):
+        raise ValueError(f"a layer's summary records span {rec.shape[0] * rec.stride(0)} "
+                         "bytes; the score kernels address at most 4 GiB per layer")
+
+
 def r8_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
              comb_out=None) -> None:
     if n_req > st.max_reqs:
@@ -26,6 +35,7 @@ def r8_score(st, layer: int, q, block_table, seq_lens, n_req: int, scale: float,
         raise ValueError("block_table must have unit column stride")
     if rec.stride(1) != 1 or rec.shape[1] != st.n_kv * st.rec_bytes:
         raise ValueError("r8_rec must hold each block's records contiguously")
+    check_rec_span(rec)
     if comb_out is not None and (comb_out.dtype != torch.int32 or not comb_out.is_contiguous()
                                  or tuple(comb_out.shape[1:]) != (st.n_kv, st.max_pages, st.G,
                                                                   st.r + 1)):

@@ -238,29 +238,30 @@ __device__ __forceinline__ void quad_walk(const QuadParams& p, QuadLds& lds, int
     // lane n's own page (mu, scales, score) is lane_page(n) of the tile; clamped pages
     // load valid data and are never written
     const int own = lane_page<RP>(n);
-    auto own_blk = [&](int tile) -> int {
+    // the record offset (rec_off) of the lane's own page of a tile
+    auto own_off = [&](int tile) -> int {
         const int page = tile * QS_TILE + own;
-        return p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)];
+        return rec_off(p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)],
+                       p.rec_sb);
     };
-    const int8_t* hrec = p.rec + (int64_t)h * VM;
-    const int8_t* vbase = hrec + 16 * (kg * RP + n % RP);          // + block * rec_sb
-    const int64_t rhead = (int64_t)h * VM + 16 * kg;
+    const int lv = h * VM + 16 * (kg * RP + n % RP);   // the lane's V bytes in a block
+    const int rhead = h * VM + 16 * kg;
     const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
-    auto lane_rec = [&](int blk) { return p.rec + (int64_t)blk * p.rec_sb + rhead; };
+    auto lane_rec = [&](int off) { return at_off(p.rec, off + rhead); };
 
     int tile = t0;
-    int blk = own_blk(tile);
+    int off = own_off(tile);
     int gb[RP];
-    group_blocks<RP>(blk, n, gb);
+    group_blocks<RP>(off, n, gb);
     QuadGroupA<RP, VB> ga;
     QuadGroupB<RP, VB> gbuf;
-    load_groups<RP, VB, 0, RP / 2>(vbase, p.rec_sb, gb, ga.v);
-    ga.mu[0] = ld16(lane_rec(blk) + RP * col_bytes<VB>());
-    ga.mu[1] = ld16(lane_rec(blk) + RP * col_bytes<VB>() + 64);
-    ga.meta = ld16(lane_rec(blk) + moff);
-    int blk_next = own_blk(cnt > 1 ? tile + wstride : tile);
+    load_groups<RP, VB, 0, RP / 2>(p.rec, lv, gb, ga.v);
+    ga.mu[0] = ld16(lane_rec(off) + RP * col_bytes<VB>());
+    ga.mu[1] = ld16(lane_rec(off) + RP * col_bytes<VB>() + 64);
+    ga.meta = ld16(lane_rec(off) + moff);
+    int off_next = own_off(cnt > 1 ? tile + wstride : tile);
     __builtin_amdgcn_sched_barrier(0);
-    load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, p.rec_sb, gb, gbuf.v);
+    load_groups<RP, VB, RP / 2, RP - RP / 2>(p.rec, lv, gb, gbuf.v);
 
     i32x4_t qa[2];
     const float qs = quantize_q_rows(qw, n, qa);
@@ -283,16 +284,16 @@ __device__ __forceinline__ void quad_walk(const QuadParams& p, QuadLds& lds, int
     for (int i = 0; i + 1 < cnt; ++i) {
         // keep the refill of a buffer after its last use (bounds the live registers)
         __builtin_amdgcn_sched_barrier(0);
-        group_blocks<RP>(blk_next, n, gb);
-        load_groups<RP, VB, 0, RP / 2>(vbase, p.rec_sb, gb, ga.v);
-        ga.mu[0] = ld16(lane_rec(blk_next) + RP * col_bytes<VB>());
-        ga.mu[1] = ld16(lane_rec(blk_next) + RP * col_bytes<VB>() + 64);
-        ga.meta = ld16(lane_rec(blk_next) + moff);
-        blk_next = own_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
+        group_blocks<RP>(off_next, n, gb);
+        load_groups<RP, VB, 0, RP / 2>(p.rec, lv, gb, ga.v);
+        ga.mu[0] = ld16(lane_rec(off_next) + RP * col_bytes<VB>());
+        ga.mu[1] = ld16(lane_rec(off_next) + RP * col_bytes<VB>() + 64);
+        ga.meta = ld16(lane_rec(off_next) + moff);
+        off_next = own_off((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
         tile_finish<RP, VB, NRM, COMB>(p, qa, gbuf, sc, q, qmu, req, h, tile, nsh, n, kg, qs0,
                                        qs1, qcoef);
         __builtin_amdgcn_sched_barrier(0);
-        load_groups<RP, VB, RP / 2, RP - RP / 2>(vbase, p.rec_sb, gb, gbuf.v);
+        load_groups<RP, VB, RP / 2, RP - RP / 2>(p.rec, lv, gb, gbuf.v);
         tile += wstride;
         sc = group_scales<RP>(lds, wave, ga.meta, n, kg);
         tile_start<RP, VB, COMB>(p, qa, ga, sc, qs0, qs1, q, qmu, req, h, tile, nsh, n, kg);

@@ -113,19 +113,18 @@ struct R8GroupC {                         // the lane's c rows
 // pages; `lr` = the lane's own-page record (block + head * VM + 16 kg), `moff` = its
 // scale block - lr
 template <int RP, int VB, bool NT>
-__device__ __forceinline__ void r8_load_a(const int8_t* vbase, int64_t rec_sb,
-                                          const int (&gb)[RP], const int8_t* lr,
-                                          R8GroupA<RP, VB>& a, int moff) {
-    load_groups<RP, VB, 0, RP / 2, NT>(vbase, rec_sb, gb, a.v);
+__device__ __forceinline__ void r8_load_a(const int8_t* rec, int lv, const int (&gb)[RP],
+                                          const int8_t* lr, R8GroupA<RP, VB>& a, int moff) {
+    load_groups<RP, VB, 0, RP / 2, NT>(rec, lv, gb, a.v);
     a.mu[0] = ld16(lr + RP * col_bytes<VB>());
     a.mu[1] = ld16(lr + RP * col_bytes<VB>() + 64);
     a.meta = ld16(lr + moff);
 }
 
 template <int RP, int VB, bool NT>
-__device__ __forceinline__ void r8_load_b(const int8_t* vbase, int64_t rec_sb,
-                                          const int (&gb)[RP], R8GroupB<RP, VB>& b) {
-    load_groups<RP, VB, RP / 2, RP - RP / 2, NT>(vbase, rec_sb, gb, b.v);
+__device__ __forceinline__ void r8_load_b(const int8_t* rec, int lv, const int (&gb)[RP],
+                                          R8GroupB<RP, VB>& b) {
+    load_groups<RP, VB, RP / 2, RP - RP / 2, NT>(rec, lv, gb, b.v);
 }
 
 template <int CL>
@@ -454,11 +453,13 @@ void r8_score_kernel(const R8Params p) {
     // pages load valid data and are never written
     const int own = lane_page<RP>(n);
     auto page_of = [&](int tile) { return tile * SC_TILE + own; };
-    auto lane_blk = [&](int tile) -> int {
+    // the record offset (rec_off) of the lane's own page of a tile
+    auto lane_off = [&](int tile) -> int {
         const int page = page_of(tile);
-        return p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)];
+        return rec_off(p.bt[(int64_t)req * p.bt_st + (page < nsh ? page : nsh - 1)],
+                       p.rec_sb);
     };
-    const int64_t rhead = (int64_t)h * VM + 16 * kg;
+    const int rhead = h * VM + 16 * kg;
     // lr + moff: the lane's 16 bytes of the head's scale block (r8) or tail (CLSE);
     // lr + coff: its c rows
     const int tail = p.n_kv * VM + h * (Geo::TB - VM) - 16 * kg;   // the head's tail - lr
@@ -466,8 +467,8 @@ void r8_score_kernel(const R8Params p) {
                                 (kg == 0 ? 32 : (kg == 3 ? (RP == 8 ? 48 : 32) : 16 * (kg - 1)))
                           : tail + 16 * kg;
     const int coff = CLSE ? tail + part * CL : RP * Geo::CB + 128 + part * CL - 16 * kg;
-    auto lane_rec = [&](int blk) { return p.rec + (int64_t)blk * p.rec_sb + rhead; };
-    const int8_t* vbase = p.rec + (int64_t)h * VM + 16 * (kg * RP + n % RP);
+    auto lane_rec = [&](int off) { return at_off(p.rec, off + rhead); };
+    const int lv = h * VM + 16 * (kg * RP + n % RP);   // the lane's V bytes in a block
     __shared__ R8Lds lds;
     int2 (&row)[SC_TILE][8] = lds.x[wave][kg];
 
@@ -476,17 +477,17 @@ void r8_score_kernel(const R8Params p) {
     // matrix-core product, C (the lane's c rows) by the token tail, so both column groups
     // of the next tile are in flight during this tile's tail.
     int tile = t0;
-    int blk = lane_blk(tile);
+    int off = lane_off(tile);
     int gbk[RP];
-    group_blocks<RP>(blk, n, gbk);
-    const int8_t* lr = lane_rec(blk);
+    group_blocks<RP>(off, n, gbk);
+    const int8_t* lr = lane_rec(off);
     R8GroupA<RP, VB> ga;
     R8GroupB<RP, VB> gb;
     R8GroupC<CL> gc;
-    r8_load_a<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, lr, ga, moff);
-    int bn_next = lane_blk(cnt > 1 ? tile + wstride : tile);
+    r8_load_a<RP, VB, Geo::NT>(p.rec, lv, gbk, lr, ga, moff);
+    int on_next = lane_off(cnt > 1 ? tile + wstride : tile);
     __builtin_amdgcn_sched_barrier(0);
-    r8_load_b<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, gb);
+    r8_load_b<RP, VB, Geo::NT>(p.rec, lv, gbk, gb);
     __builtin_amdgcn_sched_barrier(0);
     r8_load_c<CL>(lr + coff, gc);
 
@@ -517,14 +518,14 @@ void r8_score_kernel(const R8Params p) {
         r8_tile_start<RP, VB, G, COMB>(p, qa, ga, sc, qs0, qs1, acc, row, req, h, page, valid,
                                        pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
-        group_blocks<RP>(bn_next, n, gbk);
-        const int8_t* ln = lane_rec(bn_next);
-        r8_load_a<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, ln, ga, moff);
-        bn_next = lane_blk((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
+        group_blocks<RP>(on_next, n, gbk);
+        const int8_t* ln = lane_rec(on_next);
+        r8_load_a<RP, VB, Geo::NT>(p.rec, lv, gbk, ln, ga, moff);
+        on_next = lane_off((i + 2 < cnt) ? tile + 2 * wstride : tile + wstride);
         r8_tile_mid<RP, VB, G, COMB>(p, qa, gb, sc, qs0, qs1, acc, row, req, h, page, valid,
                                      pair, part, n);
         __builtin_amdgcn_sched_barrier(0);
-        r8_load_b<RP, VB, Geo::NT>(vbase, p.rec_sb, gbk, gb);
+        r8_load_b<RP, VB, Geo::NT>(p.rec, lv, gbk, gb);
         r8_tile_tail<RP, CBITS, G, CLSE>(p, gc, sc, acc, req, h, page, valid, pair, part, kg, sl,
                                          qsq0, qsq1);
         __builtin_amdgcn_sched_barrier(0);

@@ -91,8 +91,22 @@ __device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
     else return *reinterpret_cast<const i32x4_t*>(p);
 }
 
-// block id of every group's page for this lane: lane m of a row carries page
-// lane_page(m); group j's page for lane n is lane_page((n / RP) RP + j)
+// Record addresses as 32-bit byte offsets from the record buffer's base: block b's
+// records start at rec + b rec_sb, one 32-bit product per lane and tile, which the lanes
+// then exchange (group_blocks) instead of block ids.  A load is then the kernel's uniform
+// base plus one 32-bit offset (the scalar-base form of the global load: no 64-bit
+// arithmetic per lane and one VGPR per address; a 64-bit product per group load costs
+// three quarter-rate multiplies).  The callers keep a layer's record buffer under 4 GiB,
+// so every offset fits.
+__device__ __forceinline__ int rec_off(int blk, int64_t rec_sb) {
+    return (int)((uint32_t)blk * (uint32_t)rec_sb);
+}
+__device__ __forceinline__ const int8_t* at_off(const int8_t* base, int off) {
+    return base + (uint32_t)off;
+}
+
+// the record offset (rec_off) of every group's page for this lane: lane m of a row
+// carries page lane_page(m); group j's page for lane n is lane_page((n / RP) RP + j)
 template <int RP>
 __device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) {
     constexpr int PP = group_pages<RP>();
@@ -114,13 +128,14 @@ __device__ __forceinline__ void group_blocks(int blk_own, int n, int (&gb)[RP]) 
     }
 }
 
-// `base` = rec + h * VM + the lane's V offset (16 (kg r' + n % r')); group j of block b
+// group j's V at rec + gb[j] (its record offset, rec_off) + lv, lv = h * VM + the lane's
+// V offset 16 (kg r' + n % r')
 template <int RP, int VB, int J0, int NG, bool NT = true>
-__device__ __forceinline__ void load_groups(const int8_t* base, int64_t rec_sb,
-                                            const int (&gb)[RP], i32x4_t* v) {
+__device__ __forceinline__ void load_groups(const int8_t* rec, int lv, const int (&gb)[RP],
+                                            i32x4_t* v) {
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
-        const int8_t* p = base + (int64_t)gb[J0 + j] * rec_sb;
+        const int8_t* p = at_off(rec, gb[J0 + j] + lv);
         if constexpr (VB == 8) {
             v[2 * j] = ld16_stream<NT>(p);
             v[2 * j + 1] = ld16_stream<NT>(p + 64 * RP);

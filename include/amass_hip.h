@@ -56,6 +56,8 @@ extern "C" {
  *                           mu_scale at half 16, the rest zero
  * rec points at block 0 of the layer, rec_sb is the block stride in bytes (at least
  * n_kv * AMASS_QUAD_REC_BYTES, a multiple of 16).  n_kv <= 8 or a multiple of 8.
+ * The score kernels (quad, r8, CLSE and the per-unit pipeline) address records with
+ * 32-bit byte offsets from rec: (largest block id + 1) * rec_sb <= 2^32.
  * tile_max (combine 1, optional): tile_max[r,kh,g,t] = max of S_g over the scored pages
  * of tile t (pages 16t .. 16t+15), t < ceil(n_sel_hi / 16), (R,n_kv,G,ceil(MP/16)) fp32;
  * the per-head maxima the nrm combine needs, so the selection reads score_h once. */
