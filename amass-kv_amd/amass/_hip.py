@@ -18,7 +18,7 @@ _F32 = C.c_float
 _F64 = C.c_double
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libamass_hip.so")
-ABI_VERSION = 10    # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
+ABI_VERSION = 11    # AMASS_ABI_VERSION of include/amass_hip.h these mirrors follow
 
 
 class AmassError(RuntimeError):

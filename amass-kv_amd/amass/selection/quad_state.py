@@ -2,7 +2,7 @@
 
 The reference (``selection/quad_state.py:36-151``) keeps five slabs per layer; this
 build packs them into one block-keyed buffer and exposes the reference's names as views
-into it.  Per (layer, block), REC = r' * CB + 192 bytes per kv head:
+into it.  Per (layer, block), REC = r' * CB + 176 bytes per kv head:
 
   quad_rec   (L, NB, n_kv * REC)  int8, per block:
     n_kv records of VM = r' * CB + 128 bytes, head h at h * VM:
@@ -12,7 +12,7 @@ into it.  Per (layer, block), REC = r' * CB + 192 bytes per kv head:
                int4 CB = d/2 with byte i of (kg, k) = code[16 kg + i] | code[16 kg + i + 64] << 4
                (the reference keeps (.., d, r') with two columns per int4 byte)
       quad_mu  (L, NB, n_kv, d)      int8  page-mean codes
-    then n_kv scale blocks of 64 bytes (fp16 halves), head h at n_kv * VM + 64 h:
+    then n_kv scale blocks of 48 bytes (fp16 halves), head h at n_kv * VM + 48 h:
       V_scale  (L, NB, n_kv, r')     half 0..r'-1
       quad_sig2(L, NB, n_kv, r')     half 8..8+r'-1 (eigenvalues of the centred key scatter)
       mu_scale (L, NB, n_kv)         half 16; the other halves are zero
@@ -158,7 +158,7 @@ class QuadState:
             rc = r // 2 if c_bits == 4 else r             # c bytes per token row
             tb = page * rc + 16 * ((36 + 2 * r + 15) // 16)   # the head's tail
         else:
-            tb = 64                                       # the head's scale block
+            tb = 48                                       # the head's scale block
         self.rec_bytes = vm + tb
         self.quad_rec = torch.zeros(L, NB, n_kv * self.rec_bytes, device=device, dtype=i8)
         recs = self.quad_rec[..., :n_kv * vm].unflatten(-1, (n_kv, vm))

@@ -225,13 +225,13 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
     __syncthreads();
 
     // ---- record addressing ---------------------------------------------------------------
-    // quad / r8: head h's record [V | mu (| c rows)] at h VM, its 64-byte scale block at
-    // n_kv VM + 64 h.  CLSE: [V | mu] at h VM, its tail of TB bytes [c rows | scale part]
-    // at n_kv VM + TB h (AMASS_CLSE_REC_BYTES).
+    // quad / r8: head h's record [V | mu (| c rows)] at h VM, its scale block (quad 48,
+    // r8 64 bytes) at n_kv VM + TB h.  CLSE: [V | mu] at h VM, its tail of TB bytes
+    // [c rows | scale part] at n_kv VM + TB h (AMASS_CLSE_REC_BYTES).
     const int CB = a.v_bits == 8 ? BD : BD / 2;
     const int crow = R8 ? r * a.c_bits / 8 : 0;
     const int VM = r * CB + BD + (CLSE ? 0 : 16 * crow);
-    const int TB = CLSE ? 16 * crow + 16 * ((36 + 2 * r + 15) / 16) : 64;
+    const int TB = CLSE ? 16 * crow + 16 * ((36 + 2 * r + 15) / 16) : (R8 ? 64 : 48);
     int8_t* lrec = a.rec + layer * a.rec_lsb + blk * a.rec_sb;
     int8_t* rec = lrec + (int64_t)h * VM;
     int8_t* tail = lrec + (int64_t)a.n_kv * VM + (int64_t)TB * h;
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
         }
     }
 
-    // ---- the 64-byte fp16 scale block (CLSE: the tail's scale part) ---------------------
+    // ---- the fp16 scale block (CLSE: the tail's scale part) ------------------------------
     const float cs_in = __shfl(csc_t, (lane - 8) & 63, WAVE);   // c_scale of token lane - 8
     const uint32_t cs_bits = __float_as_uint(__shfl(csc_t, 0, WAVE));  // c_grain 2: fp32
     if constexpr (CLSE) {
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(BW * WAVE) void summary_build_kernel(const amass_bu
             if (a.c_grain == 2 && (lane == 8 || lane == 9))   // the page's fp32 c scale
                 h = (uint16_t)(lane == 8 ? (cs_bits & 0xFFFFu) : (cs_bits >> 16));
         }
-        meta[lane] = h;
+        if (lane < TB / 2) meta[lane] = h;
     }
 }
 
@@ -391,8 +391,8 @@ extern "C" int amass_summary_build(const amass_build_args* a, void* stream) {
     if (a->n_kv % nw != 0) return AMASS_ERR_GEOMETRY;
     const int crow = a->kind >= 1 ? a->rank * a->c_bits / 8 : 0;
     const int vm = a->rank * (a->v_bits == 8 ? BD : BD / 2) + BD + 16 * crow;
-    const int64_t rec_bytes = a->kind == 2
-        ? AMASS_CLSE_REC_BYTES(a->rank, a->v_bits, a->c_bits) : vm + 64;
+    const int64_t rec_bytes = a->kind == 2 ? AMASS_CLSE_REC_BYTES(a->rank, a->v_bits, a->c_bits)
+                              : (a->kind == 1 ? vm + 64 : AMASS_QUAD_REC_BYTES(a->rank, a->v_bits));
     if (a->rec_sb < (int64_t)a->n_kv * rec_bytes) return AMASS_ERR_GEOMETRY;
     if (a->n_layers < 1 || (a->n_layers > 1 && !a->k_layers)) return AMASS_ERR_GEOMETRY;
     if (a->n == 0) return AMASS_OK;

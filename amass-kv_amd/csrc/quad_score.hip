@@ -16,7 +16,7 @@
 // contraction is an exact int32 sum: comb = 128 * (hi . x) + (lo . x).
 //
 // Layout.  Per block, the n_kv heads' records [quad_V tiled (r' CB bytes) | 128 mu
-// codes], then the n_kv heads' 64-byte fp16 scale blocks (V_scale at half 0, sig2 at half
+// codes], then the n_kv heads' 48-byte fp16 scale blocks (V_scale at half 0, sig2 at half
 // 8, mu_scale at half 16) -- AMASS_QUAD_REC_BYTES per head.  quad_V holds 16 bytes per
 // (K-step t, d group kg, column k) at ((t * 4 + kg) * r' + k) * 16 (byte i = code of
 // d = 64 t + 16 kg + i); int4 (CB = 64) folds t into the nibbles (byte i of (kg, k) =

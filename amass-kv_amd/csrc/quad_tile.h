@@ -26,13 +26,14 @@ struct QuadParams {
 };
 
 template <int RP, int VB> constexpr int vm_bytes() { return RP * col_bytes<VB>() + 128; }
+constexpr int QS_SCALE_BYTES = 48;   // a head's scale block: V_scale, sig2, mu_scale
 
 template <int RP, int VB>
 struct QuadGroupA {                       // groups [0, RP/2), mu, the page's scales
     static constexpr int NG = RP / 2;
     i32x4_t v[NG * loads_per_col<VB>()];
     i32x4_t mu[2];
-    i32x4_t meta;                         // 16 bytes kg of the 64-byte scale block
+    i32x4_t meta;                         // 16 bytes kg of the 48-byte scale block
 };
 template <int RP, int VB>
 struct QuadGroupB {                       // groups [RP/2, RP)
@@ -246,7 +247,9 @@ __device__ __forceinline__ void quad_walk(const QuadParams& p, QuadLds& lds, int
     };
     const int lv = h * VM + 16 * (kg * RP + n % RP);   // the lane's V bytes in a block
     const int rhead = h * VM + 16 * kg;
-    const int moff = p.n_kv * VM + h * (64 - VM);     // this head's scale block - lr
+    // lr + moff: the lane's 16 bytes of the head's 48-byte scale block (lane group 3,
+    // whose bytes the kernel does not use, repeats group 2's load)
+    const int moff = p.n_kv * VM + h * (QS_SCALE_BYTES - VM) + (kg == 3 ? -16 : 0);
     auto lane_rec = [&](int off) { return at_off(p.rec, off + rhead); };
 
     int tile = t0;

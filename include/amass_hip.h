@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define AMASS_ABI_VERSION 10
+#define AMASS_ABI_VERSION 11
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define AMASS_OK               0
@@ -47,12 +47,12 @@ extern "C" {
  *
  * Summary records.  The reference's five per-(block, kv-head) slabs (quad_mu, mu_scale,
  * quad_V, V_scale, quad_sig2) are packed per block, AMASS_QUAD_REC_BYTES(rank, v_bits)
- * bytes per kv head (VM = r'*CB + 128 of them first, in head order, then 64 per head):
+ * bytes per kv head (VM = r'*CB + 128 of them first, in head order, then 48 per head):
  *   head h at h*VM:         quad_V tiled, r'*CB bytes: 16 bytes per (K-step t, d group kg,
  *                           column k) at ((t*4 + kg)*r' + k)*16, byte i = code[64t + 16kg + i]
  *                           (int8, CB = 128); int4 (CB = 64): t = 0 only, byte i of (kg, k) =
  *                           code[16kg+i] | code[16kg+i+64] << 4; then the 128 quad_mu int8 codes
- *   head h at n_kv*VM+64h:  fp16 V_scale[0..r') at half 0, sig2[0..r') at half 8,
+ *   head h at n_kv*VM+48h:  fp16 V_scale[0..r') at half 0, sig2[0..r') at half 8,
  *                           mu_scale at half 16, the rest zero
  * rec points at block 0 of the layer, rec_sb is the block stride in bytes (at least
  * n_kv * AMASS_QUAD_REC_BYTES, a multiple of 16).  n_kv <= 8 or a multiple of 8.
@@ -61,7 +61,7 @@ extern "C" {
  * tile_max (combine 1, optional): tile_max[r,kh,g,t] = max of S_g over the scored pages
  * of tile t (pages 16t .. 16t+15), t < ceil(n_sel_hi / 16), (R,n_kv,G,ceil(MP/16)) fp32;
  * the per-head maxima the nrm combine needs, so the selection reads score_h once. */
-#define AMASS_QUAD_REC_BYTES(rank, v_bits) ((rank) * ((v_bits) == 8 ? 128 : 64) + 192)
+#define AMASS_QUAD_REC_BYTES(rank, v_bits) ((rank) * ((v_bits) == 8 ? 128 : 64) + 176)
 typedef struct amass_quad_score_args {
     const void*    q;        int64_t q_st, q_hs;     /* (T,H,d) bf16                    */
     const int8_t*  rec;      int64_t rec_sb;         /* (NB,n_kv,REC) summary records   */

@@ -55,7 +55,7 @@ def test_library_loads_and_exports_every_symbol():
     assert len(names) == 25
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
-    assert lib.amass_abi_version() == 10
+    assert lib.amass_abi_version() == 11
 
 
 def test_struct_mirrors_header():

@@ -75,6 +75,44 @@ def test_state_load_reference_round_trip():
     assert not st.quad_V[0].any()
 
 
+
+@pytest.mark.parametrize("v_bits,r", [(8, 8), (4, 8), (8, 4), (4, 2), (8, 2)])
+def test_quad_record_positions(v_bits, r):
+    """The packed quad record (include/amass_hip.h, AMASS_QUAD_REC_BYTES): per block the
+    n_kv heads' [V tiled | mu] at h * VM (whole 128-byte lines), then 48-byte fp16 scale
+    blocks at n_kv * VM + 48 h with V_scale at half 0, sig2 at half 8, mu_scale at half 16
+    and zeros to the end.  Every field is checked at that offset in the raw buffer."""
+    n_kv, NB = 3, 4
+    st = QuadState("cpu", num_layers=1, num_blocks=NB, n_kv=n_kv, G=4, head_dim=128,
+                   page=16, max_reqs=1, max_pages=4, rank=r, v_bits=v_bits)
+    cb = 128 if v_bits == 8 else 64
+    vm = r * cb + 128
+    rec_bytes = r * cb + 176                                # AMASS_QUAD_REC_BYTES
+    assert vm % 128 == 0 and st.rec_bytes == rec_bytes == vm + 48
+    assert st.quad_rec.shape[-1] == n_kv * rec_bytes
+    rng = np.random.default_rng(r * 10 + v_bits)
+    lv = 127 if v_bits == 8 else 7
+    vcode = rng.integers(-lv, lv + 1, (NB, n_kv, 128, r)).astype(np.int8)
+    V = vcode if v_bits == 8 else oq.pack_i4(vcode)
+    mu = rng.integers(-127, 128, (NB, n_kv, 128)).astype(np.int8)
+    mus = (rng.random((NB, n_kv)) + 0.5).astype(np.float16)
+    vs = (rng.random((NB, n_kv, r)) + 0.5).astype(np.float16)
+    sg = (rng.random((NB, n_kv, r)) + 0.5).astype(np.float16)
+    st.load_reference(0, mu, mus, V, vs, sg)
+    raw = st.quad_rec[0].numpy().view(np.uint8)
+    for b in range(NB):
+        for h in range(n_kv):
+            base = h * vm
+            if v_bits == 8:               # d = 77: K-step 1, d group 0, byte 13
+                off = ((1 * 4 + 0) * r + (r - 1)) * 16 + 13
+                assert raw[b, base + off].view(np.int8) == vcode[b, h, 77, r - 1]
+            assert np.array_equal(raw[b, base + r * cb: base + vm].view(np.int8), mu[b, h])
+            meta = raw[b, n_kv * vm + 48 * h: n_kv * vm + 48 * (h + 1)].view(np.float16)
+            assert np.array_equal(meta[:r], vs[b, h]) and not meta[r:8].any()
+            assert np.array_equal(meta[8:8 + r], sg[b, h]) and not meta[8 + r:16].any()
+            assert meta[16] == mus[b, h] and not meta[17:].any()
+
+
 @pytest.mark.parametrize("vk_bits,c_bits,r", [(8, 8, 8), (4, 4, 8), (8, 4, 4), (4, 8, 4)])
 def test_r8_record_positions(vk_bits, c_bits, r):
     """The packed r8 record (include/amass_hip.h, AMASS_R8_REC_BYTES): per block the n_kv
