@@ -245,3 +245,14 @@ def test_clse_record_positions(v_bits, c_bits, r, c_grain):
     assert np.array_equal(st.quad_c[0].numpy(), c)
     assert np.array_equal(st.V_scale[0].numpy(), vs) and np.array_equal(st.quad_resid[0].numpy(), res)
     assert np.array_equal(st.mu_scale[0].numpy(), mus)
+
+
+def test_record_span_guard():
+    """The score kernels address a layer's records with 32-bit offsets: the wrappers accept
+    a record buffer of up to 4 GiB per layer and refuse a larger one (meta tensors, so
+    nothing is allocated)."""
+    from amass.selection.score import check_rec_span
+    check_rec_span(torch.empty(1 << 20, 4096, dtype=torch.int8, device="meta"))   # 4 GiB
+    check_rec_span(torch.empty(32768, 9600, dtype=torch.int8, device="meta"))    # config 1
+    with pytest.raises(ValueError, match="4 GiB"):
+        check_rec_span(torch.empty((1 << 20) + 1, 4096, dtype=torch.int8, device="meta"))
