@@ -198,9 +198,15 @@ __device__ __forceinline__ int select_unit(const amass_select_args& a, int r, in
                                 &hv[g][c * V]);
             }
     } else {
+        // plain scores: only the row's scored pages (a ragged batch's short rows would
+        // otherwise stream their whole MP-wide rows; config 2: 1.36x the algorithmic bytes).
+        // The n_sel_hi load goes first; at these launches' latency it measured no slower
+        // (config 2 10.4 us either way), where the fused staging above, whose rows the
+        // latency-bound single-request and config-1 launches read whole, lost ~0.1-0.2 us.
+        const int lb = min(max(a.n_sel_hi[r], 0), MP);
         const bool vec = (((uintptr_t)gscore) & 15) == 0;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) ld_pages<V>(gscore, page_of(c, 0), MP, vec, 0.f, &v[c * V]);
+        for (int c = 0; c < NC; ++c) ld_pages<V>(gscore, page_of(c, 0), lb, vec, 0.f, &v[c * V]);
     }
     // fused: every wave loads all of the row's tile maxima (lane l: tiles l + 64 i, in
     // bounds: tiles < ceil(MP / 16) <= PPT NT / 16) and reduces them itself, masked below,
