@@ -250,7 +250,7 @@ __device__ __forceinline__ void quad_walk(const QuadParams& p, QuadLds& lds, int
     // lr + moff: the lane's 16 bytes of the head's 48-byte scale block (lane group 3,
     // whose bytes the kernel does not use, repeats group 2's load)
     const int moff = p.n_kv * VM + h * (QS_SCALE_BYTES - VM) + (kg == 3 ? -16 : 0);
-    auto lane_rec = [&](int off) { return at_off(p.rec, off + rhead); };
+    auto lane_rec = [&](int off) { return at_off(p.rec, off, rhead); };
 
     int tile = t0;
     int off = own_off(tile);

@@ -109,9 +109,9 @@ struct R8GroupC {                         // the lane's c rows
     uint32_t c[CL / 4];
 };
 
-// `vbase` = rec + h * VM + the lane's V offset, `gb` the blocks of the lane's group
-// pages; `lr` = the lane's own-page record (block + head * VM + 16 kg), `moff` = its
-// scale block - lr
+// group j's V at rec + gb[j] (the record offset of the lane's group page j) + lv (h * VM +
+// the lane's V offset); `lr` = the lane's own-page record (its block's records + h * VM +
+// 16 kg), `moff` = its 16 bytes of the scale block (r8) or tail (CLSE) - lr
 template <int RP, int VB, bool NT>
 __device__ __forceinline__ void r8_load_a(const int8_t* rec, int lv, const int (&gb)[RP],
                                           const int8_t* lr, R8GroupA<RP, VB>& a, int moff) {
@@ -467,7 +467,7 @@ void r8_score_kernel(const R8Params p) {
                                 (kg == 0 ? 32 : (kg == 3 ? (RP == 8 ? 48 : 32) : 16 * (kg - 1)))
                           : tail + 16 * kg;
     const int coff = CLSE ? tail + part * CL : RP * Geo::CB + 128 + part * CL - 16 * kg;
-    auto lane_rec = [&](int off) { return at_off(p.rec, off + rhead); };
+    auto lane_rec = [&](int off) { return at_off(p.rec, off, rhead); };
     const int lv = h * VM + 16 * (kg * RP + n % RP);   // the lane's V bytes in a block
     __shared__ R8Lds lds;
     int2 (&row)[SC_TILE][8] = lds.x[wave][kg];

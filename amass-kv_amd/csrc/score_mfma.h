@@ -101,8 +101,10 @@ __device__ __forceinline__ i32x4_t ld16_stream(const int8_t* p) {
 __device__ __forceinline__ int rec_off(int blk, int64_t rec_sb) {
     return (int)((uint32_t)blk * (uint32_t)rec_sb);
 }
-__device__ __forceinline__ const int8_t* at_off(const int8_t* base, int off) {
-    return base + (uint32_t)off;
+// base + the block's offset + a byte offset inside the block, summed as unsigned 32-bit
+// (the offsets are carried in int lanes but may exceed 2^31)
+__device__ __forceinline__ const int8_t* at_off(const int8_t* base, int off, int add) {
+    return base + ((uint32_t)off + (uint32_t)add);
 }
 
 // the record offset (rec_off) of every group's page for this lane: lane m of a row
@@ -135,7 +137,7 @@ __device__ __forceinline__ void load_groups(const int8_t* rec, int lv, const int
                                             i32x4_t* v) {
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
-        const int8_t* p = at_off(rec, gb[J0 + j] + lv);
+        const int8_t* p = at_off(rec, gb[J0 + j], lv);
         if constexpr (VB == 8) {
             v[2 * j] = ld16_stream<NT>(p);
             v[2 * j + 1] = ld16_stream<NT>(p + 64 * RP);
