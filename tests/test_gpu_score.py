@@ -250,3 +250,57 @@ def test_r8_page_f32_scale(vk_bits, c_bits, G):
         assert np.array_equal(got[r, :, :n], ref_comb[r, :, :n])
         assert rel_err(sc[r, :, :n], sc_comb[r, :, :n]) <= 1e-6
         assert rel_err(sc[r, :, :n], ref[r, :, :n]) <= 1e-3
+
+
+@pytest.mark.parametrize("kind", ["quad", "clse"])
+def test_records_beyond_2gib(kind):
+    """The score kernels address records with 32-bit offsets from the layer's base (block
+    * rec_sb, plus head and lane bytes, summed unsigned): records placed at block ids whose
+    offsets exceed 2^31 bytes score bit for bit as the same records at low block ids."""
+    from amass.selection import QuadState
+    from amass.selection.quad_score import clse_score
+    announce(f"records beyond 2 GiB: {kind}")
+    B, MP, n_kv, G = 2, 64, 8, 4
+    if kind == "quad":
+        kw = dict(rank=8, v_bits=8)
+    else:
+        kw = dict(rank=2, v_bits=4, coords="lse", c_bits=4, c_grain="token")
+    rec_block = n_kv * (8 * 128 + 176 if kind == "quad" else 2 * 64 + 128 + 16 + 48)
+    hi0 = (1 << 31) // rec_block + 1                     # first block past 2 GiB
+    NB = hi0 + B * MP
+    st = QuadState(DEV, num_layers=1, num_blocks=NB, n_kv=n_kv, G=G, head_dim=128, page=16,
+                   max_reqs=B, max_pages=MP, combine="max", **kw)
+    assert st.quad_rec.stride(1) == rec_block and NB * rec_block < (1 << 32)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    lo = torch.arange(B * MP, device=DEV)
+    raw = torch.randint(-127, 128, (B * MP, st.quad_rec.shape[-1]), generator=g,
+                        device=DEV, dtype=torch.int8)
+    st.quad_rec[0, lo] = raw
+    # finite fp16 scales over the random bytes
+    half = lambda *s: (torch.rand(*s, generator=g, device=DEV) * 0.02 + 0.01).half()  # noqa: E731
+    st.V_scale[0, lo] = half(B * MP, n_kv, st.r)
+    st.mu_scale[0, lo] = half(B * MP, n_kv)
+    if kind == "quad":
+        st.quad_sig2[0, lo] = half(B * MP, n_kv, st.r)
+    else:
+        st._c_scale16[0, lo] = half(B * MP, n_kv, 16)
+        st.quad_resid[0, lo] = half(B * MP, n_kv)
+    st.quad_rec[0, hi0 + lo] = st.quad_rec[0, lo]
+    q = torch.randn(B, n_kv * G, 128, generator=g, device=DEV).to(torch.bfloat16)
+    sl = torch.full((B,), MP * 16, dtype=torch.int32, device=DEV)
+    derive_page_params(st, sl, B)
+    bt_lo = lo.view(B, MP).to(torch.int32)
+    scores = []
+    for bt in (bt_lo, bt_lo + hi0):
+        st.score.fill_(float("nan"))
+        if kind == "quad":
+            quad_score_launch(st, 0, q, bt.contiguous(), B, 128 ** -0.5)
+        else:
+            clse_score(st, 0, q, bt.contiguous(), sl, B, 128 ** -0.5)
+        torch.cuda.synchronize()
+        scores.append(st.score.clone())
+    nsh = int(st.n_sel_hi[0])
+    assert torch.isfinite(scores[0][:, :, :nsh]).all()
+    assert torch.equal(scores[0][:, :, :nsh], scores[1][:, :, :nsh])
+    del st
+    torch.cuda.empty_cache()
